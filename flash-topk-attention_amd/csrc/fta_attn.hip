@@ -1,0 +1,1109 @@
+// Block-sparse attention forward and backward for gfx950.
+//
+// Reference semantics: flash_topk_attn_v2/sparse_attn.py:24-127 (forward),
+// sparse_attn_bwd.py:111-294 (dQ, dK, dV), kernels
+// csrc/sparse_attn_kernel.cu:6-365, csrc/sparse_attn_bwd_dq_kernel.cu:6-419,
+// csrc/sparse_attn_bwd_dkv_kernel.cu:6-435.
+//
+// Design (MI355X-first, not a translation of the CuTe kernels):
+//  * A workgroup owns 32-query tiles of one (b, h) (forward / dQ) or 32-key tiles
+//    (dK/dV).  It builds, in LDS, a per-tile 32-bit column mask for every KV
+//    block (resp. 32-query chunk) from the merged lists, takes the union of
+//    the blocks any of its tiles needs, and stages each union block in LDS
+//    once for all its tiles.  Tiles whose mask is empty skip the MFMAs; tiles
+//    whose mask is partial mask columns.  This handles any q_block_size,
+//    kv_block_size and virtual padding with one code path, and reuses every
+//    gathered KV byte across up to 8 q-blocks.
+//  * dK/dV walk the transposed membership (KV block -> q-blocks) directly, so no
+//    atomics are needed on the gradient path.
+//  * Operands that are contracted over tokens (V in P.V, K in dS.K, Q and dO in
+//    the dK/dV products) are read from token-transposed copies ("T layout"),
+//    keeping every MFMA operand load a contiguous 8/16-byte LDS read.
+#include "fta_common.h"
+#include "fta_host.h"
+
+namespace fta {
+int launch_transpose(const void* x, const int64_t* s, int B, int H, int N, int Dreal, int Dk, int Np, int pad,
+                     int blk_len, int blk_stride, void* out, hipStream_t st);
+int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint32_t* sel, hipStream_t st);
+}  // namespace fta
+
+constexpr int kSeg = 512;  // KV blocks (forward / dQ) or q-chunks (dK/dV) per mask segment
+
+struct AttnArgs {
+    const uint16_t* q;
+    int64_t q_sb, q_sh, q_sn;
+    const uint16_t* k;
+    int64_t k_sb, k_sh, k_sn;
+    const uint16_t* v;
+    int64_t v_sb, v_sh, v_sn;
+    const uint16_t* dout;
+    int64_t d_sb, d_sh, d_sn;
+    const uint16_t* kvT;  // T layout of V (forward) or K (dQ): [BH][Dk][Npk], block stride sbk
+    int Npk, sbk;
+    const uint16_t* qT;   // T layout of Q (dK/dV): [BH][Dk][Npq]
+    const uint16_t* doT;  // T layout of dO (dK/dV)
+    int Npq;
+    const int32_t* merged;  // [BH][QM][W]
+    const uint32_t* sel;    // [BH][Mkv][QW] membership bitmap (dK/dV)
+    int QM, W, QW;
+    uint16_t* out0;  // o (forward) / dq / dk
+    int64_t o0_sb, o0_sh, o0_sn;
+    uint16_t* out1;  // dv
+    int64_t o1_sb, o1_sh, o1_sn;
+    float* lse;             // forward output, natural log, [BH][N]
+    const float* lse_in;    // backward input
+    const float* delta_in;  // backward input
+    int H, N, Dreal, g, kvb, q_pad, kv_pad, Mkv, NC;
+    float c, scale;
+    int wg_per_bh, total;
+};
+
+__device__ __forceinline__ uint32_t fta_range_bits(int lo, int hi) {  // bits [lo, hi) of 32
+    if (hi <= lo) return 0u;
+    const uint32_t up = (hi >= 32) ? 0xffffffffu : ((1u << hi) - 1u);
+    const uint32_t dn = (lo <= 0) ? 0u : ((1u << lo) - 1u);
+    return up & ~dn;
+}
+
+// Column masks of the WG's query tiles for KV blocks [seg0, seg0 + segn), then
+// the ascending union list.  Returns the list length.
+template <int T>
+__device__ int fta_build_q_masks(const AttnArgs& a, int bh, int p0, int seg0, int segn, uint32_t (*sMask)[kSeg],
+                                 int* sList, int* s_tmp) {
+    const int tid = threadIdx.x;
+    for (int i = tid; i < T * kSeg; i += blockDim.x) sMask[i / kSeg][i % kSeg] = 0u;
+    __syncthreads();
+    const int pend = p0 + 32 * T;
+    const int qb_lo = p0 / a.g;
+    int qb_hi = (pend - 1) / a.g;
+    if (qb_hi > a.QM - 1) qb_hi = a.QM - 1;
+    const int vlo = a.q_pad, vhi = a.q_pad + a.N;  // valid padded query positions
+    const int npairs = (qb_hi - qb_lo + 1) * a.W;
+    for (int pi = tid; pi < npairs; pi += blockDim.x) {
+        const int qb = qb_lo + pi / a.W;
+        const int s = pi - (pi / a.W) * a.W;
+        const int m = a.merged[((int64_t)bh * a.QM + qb) * a.W + s];
+        if (m < seg0 || m >= seg0 + segn || m >= a.Mkv) continue;
+        int lo = qb * a.g, hi = qb * a.g + a.g;
+        lo = max(lo, max(p0, vlo));
+        hi = min(hi, min(pend, vhi));
+        if (lo >= hi) continue;
+        for (int tau = (lo - p0) >> 5; tau <= (hi - 1 - p0) >> 5; ++tau) {
+            const int tb = p0 + 32 * tau;
+            const uint32_t bits = fta_range_bits(max(lo, tb) - tb, min(hi, tb + 32) - tb);
+            atomicOr(&sMask[tau][m - seg0], bits);
+        }
+    }
+    __syncthreads();
+    int U = 0;
+    for (int base = 0; base < segn; base += 256) {
+        const int ml = base + tid;
+        int any = 0;
+        if (tid < 256 && ml < segn) {
+#pragma unroll
+            for (int t = 0; t < T; ++t) any |= (sMask[t][ml] != 0u);
+        }
+        // 256-wide scan (threads >= 256, if any, contribute 0)
+        const int lane = tid & 63, wave = tid >> 6;
+        int x = any;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(x, off, 64);
+            if (lane >= off) x += y;
+        }
+        if (lane == 63 && wave < 8) s_tmp[wave] = x;
+        __syncthreads();
+        const int nw = blockDim.x >> 6;
+        int wbase = 0, tot = 0;
+        for (int w = 0; w < nw; ++w) {
+            const int t = s_tmp[w];
+            if (w < wave) wbase += t;
+            tot += t;
+        }
+        if (any) sList[U + wbase + x - any] = ml;
+        __syncthreads();
+        U += tot;
+    }
+    return U;
+}
+
+// ----------------------------------------------------------------------------
+// Forward.  WG = 4 waves x TPW tiles x 32 queries.  For every union KV block,
+// 64-key chunks of K (row layout) and V (T layout) are double-buffered in LDS.
+// Per tile: S^T = K Q^T (32 keys x 32 queries per MFMA), online softmax with a
+// lazily rescaled running max (rescale only when the max grows by > 2^8),
+// O^T += V^T P^T.
+// ----------------------------------------------------------------------------
+template <int DT, int D, int TPW>
+__global__ __launch_bounds__(256, 1) void fta_sparse_fwd_kernel(AttnArgs a) {
+    using E = Elem<DT>;
+    constexpr int T = 4 * TPW;
+    constexpr int KS = D / 16;
+    constexpr int DT32 = D / 32;
+    constexpr int KROW = D + 8;
+    constexpr int VROW = 64 + 8;
+    constexpr int KSEG = D / 8;
+    constexpr int KLOADS = 64 * KSEG / 256;
+    constexpr int VLOADS = D * 8 / 256;
+    __shared__ __align__(16) uint16_t sK[2][64 * KROW];
+    __shared__ __align__(16) uint16_t sV[2][D * VROW];
+    __shared__ uint32_t sMask[T][kSeg];
+    __shared__ int sList[kSeg];
+    __shared__ int s_tmp[8];
+
+    const int wgi = fta_xcd_remap(blockIdx.x, a.total);
+    const int bh = wgi / a.wg_per_bh;
+    const int wq = wgi - bh * a.wg_per_bh;
+    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int hf = lane >> 5;
+    const int p0 = wq * 32 * T;
+
+    const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
+    const uint16_t* vtp = a.kvT + (int64_t)bh * D * a.Npk;
+
+    uint4 qf[TPW][KS];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+        const int t = p0 + 32 * (wave * TPW + tt) + (lane & 31) - a.q_pad;
+        const bool ok = t >= 0 && t < a.N;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d = ks * 16 + hf * 8;
+            qf[tt][ks] = (ok && d < a.Dreal) ? *reinterpret_cast<const uint4*>(qp + (int64_t)t * a.q_sn + d)
+                                             : fta_zero4();
+        }
+    }
+
+    f32x16 oacc[TPW][DT32];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt)
+#pragma unroll
+        for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[tt][dt][i] = 0.f;
+    float m_run[TPW], l_run[TPW];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+        m_run[tt] = -FTA_INF;
+        l_run[tt] = 0.f;
+    }
+
+    const int nch = (a.kvb + 63) >> 6;
+    uint4 kst[KLOADS], vst[VLOADS];
+
+    for (int seg0 = 0; seg0 < a.Mkv; seg0 += kSeg) {
+        const int segn = min(kSeg, a.Mkv - seg0);
+        const int U = fta_build_q_masks<T>(a, bh, p0, seg0, segn, sMask, sList, s_tmp);
+        if (U == 0) continue;
+        const int iters = U * nch;
+
+        auto load = [&](int it) {
+            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int m = seg0 + sList[u];
+            const int kb = m * a.kvb - a.kv_pad + ch * 64;
+            const int rem = a.kvb - ch * 64;
+#pragma unroll
+            for (int i = 0; i < KLOADS; ++i) {
+                const int s = tid + i * 256;
+                const int row = s / KSEG, sg = s - (s / KSEG) * KSEG;
+                const int t = kb + row;
+                const bool ok = row < rem && t >= 0 && t < a.N && sg * 8 < a.Dreal;
+                kst[i] = ok ? *reinterpret_cast<const uint4*>(kp + (int64_t)t * a.k_sn + sg * 8) : fta_zero4();
+            }
+            const int pb = m * a.sbk + ch * 64;
+#pragma unroll
+            for (int i = 0; i < VLOADS; ++i) {
+                const int s = tid + i * 256;
+                const int dr = s >> 3, sg = s & 7;
+                vst[i] = *reinterpret_cast<const uint4*>(vtp + (int64_t)dr * a.Npk + pb + sg * 8);
+            }
+        };
+        auto store = [&](int buf) {
+#pragma unroll
+            for (int i = 0; i < KLOADS; ++i) {
+                const int s = tid + i * 256;
+                const int row = s / KSEG, sg = s - (s / KSEG) * KSEG;
+                *reinterpret_cast<uint4*>(&sK[buf][row * KROW + sg * 8]) = kst[i];
+            }
+#pragma unroll
+            for (int i = 0; i < VLOADS; ++i) {
+                const int s = tid + i * 256;
+                const int dr = s >> 3, sg = s & 7;
+                *reinterpret_cast<uint4*>(&sV[buf][dr * VROW + sg * 8]) = vst[i];
+            }
+        };
+
+        load(0);
+        store(0);
+        __syncthreads();
+        for (int it = 0; it < iters; ++it) {
+            const int buf = it & 1;
+            if (it + 1 < iters) load(it + 1);
+            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int ml = sList[u];
+            const int m = seg0 + ml;
+            const int kb = m * a.kvb - a.kv_pad + ch * 64;
+            const int rem = a.kvb - ch * 64;
+            const bool two = rem > 32;
+            uint32_t mk[TPW];
+            bool anyt = false;
+#pragma unroll
+            for (int tt = 0; tt < TPW; ++tt) {
+                mk[tt] = __builtin_amdgcn_readfirstlane(sMask[wave * TPW + tt][ml]);
+                anyt |= mk[tt] != 0u;
+            }
+            if (anyt) {
+                f32x16 s[TPW][2];
+#pragma unroll
+                for (int tt = 0; tt < TPW; ++tt)
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) s[tt][sb][i] = 0.f;
+                const uint16_t* kbase = &sK[buf][0];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const uint4 a0 =
+                        *reinterpret_cast<const uint4*>(kbase + (lane & 31) * KROW + ks * 16 + hf * 8);
+#pragma unroll
+                    for (int tt = 0; tt < TPW; ++tt)
+                        if (mk[tt]) s[tt][0] = E::mma(a0, qf[tt][ks], s[tt][0]);
+                }
+                if (two) {
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        const uint4 a1 = *reinterpret_cast<const uint4*>(kbase + (32 + (lane & 31)) * KROW +
+                                                                         ks * 16 + hf * 8);
+#pragma unroll
+                        for (int tt = 0; tt < TPW; ++tt)
+                            if (mk[tt]) s[tt][1] = E::mma(a1, qf[tt][ks], s[tt][1]);
+                    }
+                }
+                const bool kmask = kb < 0 || kb + 64 > a.N || rem < 64;
+#pragma unroll
+                for (int tt = 0; tt < TPW; ++tt) {
+                    if (!mk[tt]) continue;
+                    const bool colok = (mk[tt] >> (lane & 31)) & 1u;
+                    float mx = -FTA_INF;
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            const int rel = sb * 32 + c_row(i, lane);
+                            const int t = kb + rel;
+                            const bool ok = colok && (!kmask || (rel < rem && t >= 0 && t < a.N));
+                            const float v = ok ? s[tt][sb][i] : -FTA_INF;
+                            s[tt][sb][i] = v;
+                            mx = fmaxf(mx, v);
+                        }
+                    mx = fmaxf(mx, fta_xor32(mx));
+                    const float mn = fmaxf(m_run[tt], mx);
+                    const bool grow = (mn - m_run[tt]) * a.c > 8.f;
+                    if (__ballot(grow) != 0ull) {
+                        const float alpha = grow ? fta_exp2((m_run[tt] - mn) * a.c) : 1.f;
+#pragma unroll
+                        for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+                            for (int i = 0; i < 16; ++i) oacc[tt][dt][i] *= alpha;
+                        l_run[tt] *= alpha;
+                        if (grow) m_run[tt] = mn;
+                    }
+                    const float mc = (m_run[tt] == -FTA_INF) ? 0.f : m_run[tt] * a.c;
+                    float ls = 0.f;
+                    uint4 pf[4];
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) {
+                        float pv[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            pv[e] = fta_exp2(fmaf(s[tt][ks >> 1][8 * (ks & 1) + e], a.c, -mc));
+                            ls += pv[e];
+                        }
+                        pf[ks] = make_uint4(E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
+                                            E::pack2(pv[6], pv[7]));
+                    }
+                    l_run[tt] += ls;
+                    const uint16_t* vbase = &sV[buf][0];
+                    const int nks = two ? 4 : 2;
+                    for (int ks = 0; ks < nks; ++ks) {
+#pragma unroll
+                        for (int dt = 0; dt < DT32; ++dt) {
+                            const uint16_t* vr = vbase + (dt * 32 + (lane & 31)) * VROW + ks * 16 + hf * 4;
+                            const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+                            const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
+                            oacc[tt][dt] = E::mma(make_uint4(lo.x, lo.y, hi.x, hi.y), pf[ks], oacc[tt][dt]);
+                        }
+                    }
+                }
+            }
+            if (it + 1 < iters) store(buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    // finalize: O = O^T / L, lse = ln(sum) + max
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+        const float L = l_run[tt] + fta_xor32(l_run[tt]);
+        const float inv = (L > 0.f) ? 1.f / L : 0.f;
+        const int t = p0 + 32 * (wave * TPW + tt) + (lane & 31) - a.q_pad;
+        if (t < 0 || t >= a.N) continue;
+        if (lane < 32)
+            a.lse[(int64_t)bh * a.N + t] =
+                (L > 0.f) ? (fmaf(m_run[tt], a.c, fta_log2(L))) * 0.69314718055994531f : -FTA_INF;
+        uint16_t* op = a.out0 + b * a.o0_sb + h * a.o0_sh + (int64_t)t * a.o0_sn;
+#pragma unroll
+        for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const int d = dt * 32 + c_row(i, lane);
+                if (d < a.Dreal) {
+                    uint2 w;
+                    w.x = E::pack2(oacc[tt][dt][i] * inv, oacc[tt][dt][i + 1] * inv);
+                    w.y = E::pack2(oacc[tt][dt][i + 2] * inv, oacc[tt][dt][i + 3] * inv);
+                    *reinterpret_cast<uint2*>(op + d) = w;
+                }
+            }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// dQ.  Same tiling as the forward (one tile per wave).  Per union KV chunk:
+//   S^T = K Q^T, P^T = 2^{c S^T - lse2}, dP^T = V dO^T, dS^T = P^T (dP^T - delta),
+//   dQ^T += K^T dS^T  (K^T from the T layout).
+// ----------------------------------------------------------------------------
+template <int DT, int D>
+__global__ __launch_bounds__(256, 1) void fta_sparse_dq_kernel(AttnArgs a) {
+    using E = Elem<DT>;
+    constexpr int NB = (D <= 160) ? 2 : 1;  // LDS buffers (D = 256 single-buffers to fit 160 KB)
+    constexpr int T = 4;
+    constexpr int KS = D / 16;
+    constexpr int DT32 = D / 32;
+    constexpr int KROW = D + 8;
+    constexpr int VROW = 64 + 8;
+    constexpr int KSEG = D / 8;
+    constexpr int KLOADS = 64 * KSEG / 256;
+    constexpr int TLOADS = D * 8 / 256;
+    __shared__ __align__(16) uint16_t sK[NB][64 * KROW];
+    __shared__ __align__(16) uint16_t sV[NB][64 * KROW];
+    __shared__ __align__(16) uint16_t sKt[NB][D * VROW];
+    __shared__ uint32_t sMask[T][kSeg];
+    __shared__ int sList[kSeg];
+    __shared__ int s_tmp[8];
+
+    const int wgi = fta_xcd_remap(blockIdx.x, a.total);
+    const int bh = wgi / a.wg_per_bh;
+    const int wq = wgi - bh * a.wg_per_bh;
+    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int hf = lane >> 5;
+    const int p0 = wq * 32 * T;
+
+    const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
+    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+    const uint16_t* dp = a.dout + b * a.d_sb + h * a.d_sh;
+    const uint16_t* ktp = a.kvT + (int64_t)bh * D * a.Npk;
+
+    const int tq = p0 + 32 * wave + (lane & 31) - a.q_pad;
+    const bool qok = tq >= 0 && tq < a.N;
+    uint4 qf[KS], df[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const int d = ks * 16 + hf * 8;
+        const bool ok = qok && d < a.Dreal;
+        qf[ks] = ok ? *reinterpret_cast<const uint4*>(qp + (int64_t)tq * a.q_sn + d) : fta_zero4();
+        df[ks] = ok ? *reinterpret_cast<const uint4*>(dp + (int64_t)tq * a.d_sn + d) : fta_zero4();
+    }
+    float lse2 = -FTA_INF, dl = 0.f;
+    if (qok) {
+        lse2 = a.lse_in[(int64_t)bh * a.N + tq] * 1.4426950408889634f;
+        dl = a.delta_in[(int64_t)bh * a.N + tq];
+    }
+    const bool rowlive = lse2 != -FTA_INF;
+
+    f32x16 acc[DT32];
+#pragma unroll
+    for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+
+    const int nch = (a.kvb + 63) >> 6;
+    uint4 kst[KLOADS], vst[KLOADS], tst[TLOADS];
+
+    for (int seg0 = 0; seg0 < a.Mkv; seg0 += kSeg) {
+        const int segn = min(kSeg, a.Mkv - seg0);
+        const int U = fta_build_q_masks<T>(a, bh, p0, seg0, segn, sMask, sList, s_tmp);
+        if (U == 0) continue;
+        const int iters = U * nch;
+        auto load = [&](int it) {
+            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int m = seg0 + sList[u];
+            const int kb = m * a.kvb - a.kv_pad + ch * 64;
+            const int rem = a.kvb - ch * 64;
+#pragma unroll
+            for (int i = 0; i < KLOADS; ++i) {
+                const int s = tid + i * 256;
+                const int row = s / KSEG, sg = s - (s / KSEG) * KSEG;
+                const int t = kb + row;
+                const bool ok = row < rem && t >= 0 && t < a.N && sg * 8 < a.Dreal;
+                kst[i] = ok ? *reinterpret_cast<const uint4*>(kp + (int64_t)t * a.k_sn + sg * 8) : fta_zero4();
+                vst[i] = ok ? *reinterpret_cast<const uint4*>(vp + (int64_t)t * a.v_sn + sg * 8) : fta_zero4();
+            }
+            const int pb = m * a.sbk + ch * 64;
+#pragma unroll
+            for (int i = 0; i < TLOADS; ++i) {
+                const int s = tid + i * 256;
+                const int dr = s >> 3, sg = s & 7;
+                tst[i] = *reinterpret_cast<const uint4*>(ktp + (int64_t)dr * a.Npk + pb + sg * 8);
+            }
+        };
+        auto store = [&](int buf) {
+#pragma unroll
+            for (int i = 0; i < KLOADS; ++i) {
+                const int s = tid + i * 256;
+                const int row = s / KSEG, sg = s - (s / KSEG) * KSEG;
+                *reinterpret_cast<uint4*>(&sK[buf][row * KROW + sg * 8]) = kst[i];
+                *reinterpret_cast<uint4*>(&sV[buf][row * KROW + sg * 8]) = vst[i];
+            }
+#pragma unroll
+            for (int i = 0; i < TLOADS; ++i) {
+                const int s = tid + i * 256;
+                const int dr = s >> 3, sg = s & 7;
+                *reinterpret_cast<uint4*>(&sKt[buf][dr * VROW + sg * 8]) = tst[i];
+            }
+        };
+
+        load(0);
+        store(0);
+        __syncthreads();
+        for (int it = 0; it < iters; ++it) {
+            const int buf = (NB == 2) ? (it & 1) : 0;
+            if (it + 1 < iters) load(it + 1);
+            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int ml = sList[u];
+            const int m = seg0 + ml;
+            const int kb = m * a.kvb - a.kv_pad + ch * 64;
+            const int rem = a.kvb - ch * 64;
+            const bool two = rem > 32;
+            const uint32_t mk = __builtin_amdgcn_readfirstlane(sMask[wave][ml]);
+            if (mk) {
+                f32x16 s[2], dpv[2];
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        s[sb][i] = 0.f;
+                        dpv[sb][i] = 0.f;
+                    }
+                const uint16_t* kbase = &sK[buf][0];
+                const uint16_t* vbase = &sV[buf][0];
+                const int nsb = two ? 2 : 1;
+                for (int sb = 0; sb < nsb; ++sb) {
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        const int off = (sb * 32 + (lane & 31)) * KROW + ks * 16 + hf * 8;
+                        s[sb] = E::mma(*reinterpret_cast<const uint4*>(kbase + off), qf[ks], s[sb]);
+                        dpv[sb] = E::mma(*reinterpret_cast<const uint4*>(vbase + off), df[ks], dpv[sb]);
+                    }
+                }
+                const bool colok = rowlive && ((mk >> (lane & 31)) & 1u);
+                const bool kmask = kb < 0 || kb + 64 > a.N || rem < 64;
+                uint4 dsf[4];
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    float dsv[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int sb = ks >> 1, i = 8 * (ks & 1) + e;
+                        const int rel = sb * 32 + c_row(i, lane);
+                        const int t = kb + rel;
+                        const bool ok = colok && (!kmask || (rel < rem && t >= 0 && t < a.N));
+                        const float p = ok ? fta_exp2(fmaf(s[sb][i], a.c, -lse2)) : 0.f;
+                        dsv[e] = p * (dpv[sb][i] - dl);
+                    }
+                    dsf[ks] = make_uint4(E::pack2(dsv[0], dsv[1]), E::pack2(dsv[2], dsv[3]),
+                                         E::pack2(dsv[4], dsv[5]), E::pack2(dsv[6], dsv[7]));
+                }
+                const uint16_t* tbase = &sKt[buf][0];
+                const int nks = two ? 4 : 2;
+                for (int ks = 0; ks < nks; ++ks) {
+#pragma unroll
+                    for (int dt = 0; dt < DT32; ++dt) {
+                        const uint16_t* tr = tbase + (dt * 32 + (lane & 31)) * VROW + ks * 16 + hf * 4;
+                        const uint2 lo = *reinterpret_cast<const uint2*>(tr);
+                        const uint2 hi = *reinterpret_cast<const uint2*>(tr + 8);
+                        acc[dt] = E::mma(make_uint4(lo.x, lo.y, hi.x, hi.y), dsf[ks], acc[dt]);
+                    }
+                }
+            }
+            if (NB == 1) __syncthreads();
+            if (it + 1 < iters) store((NB == 2) ? (buf ^ 1) : 0);
+            __syncthreads();
+        }
+    }
+
+    if (!qok) return;
+    uint16_t* op = a.out0 + b * a.o0_sb + h * a.o0_sh + (int64_t)tq * a.o0_sn;
+#pragma unroll
+    for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const int d = dt * 32 + c_row(i, lane);
+            if (d < a.Dreal) {
+                uint2 w;
+                w.x = E::pack2(acc[dt][i] * a.scale, acc[dt][i + 1] * a.scale);
+                w.y = E::pack2(acc[dt][i + 2] * a.scale, acc[dt][i + 3] * a.scale);
+                *reinterpret_cast<uint2*>(op + d) = w;
+            }
+        }
+}
+
+// ----------------------------------------------------------------------------
+// dK / dV.  WG = 4 waves x one 32-key tile; tiles enumerate (KV block, 32-key
+// sub-tile) pairs.  Column masks over 32-query chunks come from the membership
+// bitmap.  Per union chunk (Q, dO rows and T-layout copies staged in LDS):
+//   S = Q K^T, P = 2^{c S - lse2}, dP = dO V^T, dS = P (dP - delta),
+//   dV += P^T dO, dK += dS^T Q.  No atomics.
+// ----------------------------------------------------------------------------
+template <int DT, int D>
+__global__ __launch_bounds__(256, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
+    using E = Elem<DT>;
+    constexpr int T = 4;
+    constexpr int KS = D / 16;
+    constexpr int DT32 = D / 32;
+    constexpr int QROW = D + 8;
+    constexpr int TROW = 32 + 8;
+    constexpr int QSEG = D / 8;
+    constexpr int QLOADS = (32 * QSEG + 255) / 256;
+    constexpr int TLOADS = (D * 4 + 255) / 256;
+    __shared__ __align__(16) uint16_t sQ[2][32 * QROW];
+    __shared__ __align__(16) uint16_t sO[2][32 * QROW];
+    __shared__ __align__(16) uint16_t sQt[2][D * TROW];
+    __shared__ __align__(16) uint16_t sOt[2][D * TROW];
+    __shared__ float sL[2][32];
+    __shared__ float sDl[2][32];
+    __shared__ uint32_t sMask[T][kSeg];
+    __shared__ int sList[kSeg];
+    __shared__ int s_tmp[8];
+
+    const int wgi = fta_xcd_remap(blockIdx.x, a.total);
+    const int bh = wgi / a.wg_per_bh;
+    const int wk = wgi - bh * a.wg_per_bh;
+    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int hf = lane >> 5;
+    const int Tb = (a.kvb + 31) >> 5;  // 32-key tiles per KV block
+
+    // this wave's key tile
+    const int G = wk * T + wave;
+    const int mblk = G / Tb;
+    const int tin = G - (G / Tb) * Tb;
+    const bool tile_live = mblk < a.Mkv;
+    const int krel = 32 * tin + (lane & 31);  // key of this lane's column, relative to block start
+    const int tk = mblk * a.kvb - a.kv_pad + krel;
+    const bool kok = tile_live && krel < a.kvb && tk >= 0 && tk < a.N;
+
+    const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
+    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+    const uint16_t* dp = a.dout + b * a.d_sb + h * a.d_sh;
+    const uint16_t* qtp = a.qT + (int64_t)bh * D * a.Npq;
+    const uint16_t* dtp = a.doT + (int64_t)bh * D * a.Npq;
+
+    uint4 kf[KS], vf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const int d = ks * 16 + hf * 8;
+        const bool ok = kok && d < a.Dreal;
+        kf[ks] = ok ? *reinterpret_cast<const uint4*>(kp + (int64_t)tk * a.k_sn + d) : fta_zero4();
+        vf[ks] = ok ? *reinterpret_cast<const uint4*>(vp + (int64_t)tk * a.v_sn + d) : fta_zero4();
+    }
+    f32x16 dka[DT32], dva[DT32];
+#pragma unroll
+    for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            dka[dt][i] = 0.f;
+            dva[dt][i] = 0.f;
+        }
+
+    uint4 qst[QLOADS], ost[QLOADS], qtst[TLOADS], otst[TLOADS];
+    float lst = 0.f, dst = 0.f;
+    const int qw = a.QW;
+
+    for (int seg0 = 0; seg0 < a.NC; seg0 += kSeg) {
+        const int segn = min(kSeg, a.NC - seg0);
+        // masks: tile tau x chunk (seg0 + cl) -> bits over the chunk's 32 queries
+        for (int i = tid; i < T * kSeg; i += 256) sMask[i / kSeg][i % kSeg] = 0u;
+        __syncthreads();
+        for (int pi = tid; pi < T * segn; pi += 256) {
+            const int tau = pi / segn, cl = pi - (pi / segn) * segn;
+            const int Gt = wk * T + tau;
+            const int mt = Gt / Tb;
+            if (mt >= a.Mkv) continue;
+            const int c = seg0 + cl;
+            const int pc = 32 * c;
+            const int qb_a = pc / a.g;
+            int qb_b = (pc + 31) / a.g;
+            if (qb_b > a.QM - 1) qb_b = a.QM - 1;
+            const uint32_t* srow = a.sel + ((int64_t)bh * a.Mkv + mt) * qw;
+            uint32_t bits = 0u;
+            for (int qb = qb_a; qb <= qb_b; ++qb) {
+                if ((srow[qb >> 5] >> (qb & 31)) & 1u)
+                    bits |= fta_range_bits(qb * a.g - pc, qb * a.g + a.g - pc);
+            }
+            bits &= fta_range_bits(a.q_pad - pc, a.q_pad + a.N - pc);
+            sMask[tau][cl] = bits;
+        }
+        __syncthreads();
+        int U = 0;
+        for (int base = 0; base < segn; base += 256) {
+            const int cl = base + tid;
+            int any = 0;
+            if (cl < segn) {
+#pragma unroll
+                for (int t = 0; t < T; ++t) any |= (sMask[t][cl] != 0u);
+            }
+            int x = any;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int y = __shfl_up(x, off, 64);
+                if (lane >= off) x += y;
+            }
+            if (lane == 63) s_tmp[wave] = x;
+            __syncthreads();
+            int wbase = 0, tot = 0;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const int t = s_tmp[w];
+                if (w < wave) wbase += t;
+                tot += t;
+            }
+            if (any) sList[U + wbase + x - any] = cl;
+            __syncthreads();
+            U += tot;
+        }
+        if (U == 0) continue;
+
+        auto load = [&](int u) {
+            const int c = seg0 + sList[u];
+#pragma unroll
+            for (int i = 0; i < QLOADS; ++i) {
+                const int s = tid + i * 256;
+                const int row = s / QSEG, sg = s - (s / QSEG) * QSEG;
+                const int t = 32 * c + row - a.q_pad;
+                const bool ok = s < 32 * QSEG && t >= 0 && t < a.N && sg * 8 < a.Dreal;
+                qst[i] = ok ? *reinterpret_cast<const uint4*>(qp + (int64_t)t * a.q_sn + sg * 8) : fta_zero4();
+                ost[i] = ok ? *reinterpret_cast<const uint4*>(dp + (int64_t)t * a.d_sn + sg * 8) : fta_zero4();
+            }
+#pragma unroll
+            for (int i = 0; i < TLOADS; ++i) {
+                const int s = tid + i * 256;
+                const int dr = s >> 2, sg = s & 3;
+                const bool ok = s < D * 4;
+                const int64_t off = (int64_t)dr * a.Npq + 32 * c + sg * 8;
+                qtst[i] = ok ? *reinterpret_cast<const uint4*>(qtp + off) : fta_zero4();
+                otst[i] = ok ? *reinterpret_cast<const uint4*>(dtp + off) : fta_zero4();
+            }
+            if (tid < 32) {
+                const int t = 32 * c + tid - a.q_pad;
+                const bool ok = t >= 0 && t < a.N;
+                lst = ok ? a.lse_in[(int64_t)bh * a.N + t] * 1.4426950408889634f : -FTA_INF;
+                dst = ok ? a.delta_in[(int64_t)bh * a.N + t] : 0.f;
+            }
+        };
+        auto store = [&](int buf) {
+#pragma unroll
+            for (int i = 0; i < QLOADS; ++i) {
+                const int s = tid + i * 256;
+                if (s < 32 * QSEG) {
+                    const int row = s / QSEG, sg = s - (s / QSEG) * QSEG;
+                    *reinterpret_cast<uint4*>(&sQ[buf][row * QROW + sg * 8]) = qst[i];
+                    *reinterpret_cast<uint4*>(&sO[buf][row * QROW + sg * 8]) = ost[i];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TLOADS; ++i) {
+                const int s = tid + i * 256;
+                if (s < D * 4) {
+                    const int dr = s >> 2, sg = s & 3;
+                    *reinterpret_cast<uint4*>(&sQt[buf][dr * TROW + sg * 8]) = qtst[i];
+                    *reinterpret_cast<uint4*>(&sOt[buf][dr * TROW + sg * 8]) = otst[i];
+                }
+            }
+            if (tid < 32) {
+                sL[buf][tid] = lst;
+                sDl[buf][tid] = dst;
+            }
+        };
+
+        load(0);
+        store(0);
+        __syncthreads();
+        for (int u = 0; u < U; ++u) {
+            const int buf = u & 1;
+            if (u + 1 < U) load(u + 1);
+            const int cl = sList[u];
+            const uint32_t mk = __builtin_amdgcn_readfirstlane(sMask[wave][cl]);
+            if (mk) {
+                f32x16 s, dpv;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    s[i] = 0.f;
+                    dpv[i] = 0.f;
+                }
+                const uint16_t* qb = &sQ[buf][0];
+                const uint16_t* ob = &sO[buf][0];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int off = (lane & 31) * QROW + ks * 16 + hf * 8;
+                    s = E::mma(*reinterpret_cast<const uint4*>(qb + off), kf[ks], s);
+                    dpv = E::mma(*reinterpret_cast<const uint4*>(ob + off), vf[ks], dpv);
+                }
+                uint4 pf[2], dsf[2];
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    float pv[8], dv8[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int i = 8 * ks + e;
+                        const int r = c_row(i, lane);
+                        const bool ok = kok && ((mk >> r) & 1u);
+                        const float l2 = sL[buf][r];
+                        const float p = (ok && l2 != -FTA_INF) ? fta_exp2(fmaf(s[i], a.c, -l2)) : 0.f;
+                        pv[e] = p;
+                        dv8[e] = p * (dpv[i] - sDl[buf][r]);
+                    }
+                    pf[ks] = make_uint4(E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
+                                        E::pack2(pv[6], pv[7]));
+                    dsf[ks] = make_uint4(E::pack2(dv8[0], dv8[1]), E::pack2(dv8[2], dv8[3]),
+                                         E::pack2(dv8[4], dv8[5]), E::pack2(dv8[6], dv8[7]));
+                }
+                const uint16_t* qtb = &sQt[buf][0];
+                const uint16_t* otb = &sOt[buf][0];
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                    for (int dt = 0; dt < DT32; ++dt) {
+                        const int off = (dt * 32 + (lane & 31)) * TROW + ks * 16 + hf * 4;
+                        const uint2 olo = *reinterpret_cast<const uint2*>(otb + off);
+                        const uint2 ohi = *reinterpret_cast<const uint2*>(otb + off + 8);
+                        dva[dt] = E::mma(pf[ks], make_uint4(olo.x, olo.y, ohi.x, ohi.y), dva[dt]);
+                        const uint2 qlo = *reinterpret_cast<const uint2*>(qtb + off);
+                        const uint2 qhi = *reinterpret_cast<const uint2*>(qtb + off + 8);
+                        dka[dt] = E::mma(dsf[ks], make_uint4(qlo.x, qlo.y, qhi.x, qhi.y), dka[dt]);
+                    }
+                }
+            }
+            if (u + 1 < U) store(buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    if (!tile_live) return;
+    // C layout: lane column = d (dt * 32 + lane & 31), rows = keys c_row(i, lane)
+    uint16_t* kout = a.out0 + b * a.o0_sb + h * a.o0_sh;
+    uint16_t* vout = a.out1 + b * a.o1_sb + h * a.o1_sh;
+#pragma unroll
+    for (int dt = 0; dt < DT32; ++dt) {
+        const int d = dt * 32 + (lane & 31);
+        if (d >= a.Dreal) continue;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int kr = 32 * tin + c_row(i, lane);
+            const int t = mblk * a.kvb - a.kv_pad + kr;
+            if (kr < a.kvb && t >= 0 && t < a.N) {
+                const uint32_t pk = E::pack2(dka[dt][i] * a.scale, dva[dt][i]);
+                kout[(int64_t)t * a.o0_sn + d] = (uint16_t)(pk & 0xffffu);
+                vout[(int64_t)t * a.o1_sn + d] = (uint16_t)(pk >> 16);
+            }
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Host side
+// ----------------------------------------------------------------------------
+namespace {
+
+struct Geo {
+    int Dk, Mkv, QM, nch, sbk, Npk, NC, Npq;
+};
+
+int geometry(int B, int H, int N, int D, int g, int kvb, int qph, int qpt, int kvph, int kvpt, int QM, Geo* o) {
+    if (B <= 0 || H <= 0 || N <= 0 || D <= 0) return fta::arg_error("sparse_attn: dims must be positive");
+    if (D % 16 != 0) return fta::arg_error("sparse_attn: D must be a positive multiple of 16");
+    if (D > 256) return fta::arg_error("sparse_attn: D must be <= 256");
+    if (g <= 0) return fta::arg_error("sparse_attn: q_block_size must be positive");
+    if (kvb <= 0) return fta::arg_error("sparse_attn: kv_block_size must be positive");
+    if (qph < 0 || qpt < 0 || qph >= g || qpt >= g) return fta::arg_error("sparse_attn: bad q_padding");
+    if (kvph < 0 || kvpt < 0 || kvph >= kvb || kvpt >= kvb) return fta::arg_error("sparse_attn: bad kv_padding");
+    const int64_t nq = (int64_t)qph + N + qpt, nk = (int64_t)kvph + N + kvpt;
+    if (nq % g) return fta::arg_error("sparse_attn: q_pad_head + N + q_pad_tail must be divisible by q_block_size");
+    if (nk % kvb) return fta::arg_error("sparse_attn: kv_pad_head + N + kv_pad_tail must be divisible by kv_block_size");
+    if (nq / g != QM) return fta::arg_error("sparse_attn: merged_indices dim 2 must equal QM");
+    o->Dk = fta::kernel_head_dim(D);
+    o->Mkv = (int)(nk / kvb);
+    o->QM = QM;
+    o->nch = (kvb + 63) / 64;
+    o->sbk = o->nch * 64;
+    o->Npk = o->Mkv * o->sbk;
+    o->NC = (int)((nq + 31) / 32);
+    o->Npq = o->NC * 32;
+    return FTA_OK;
+}
+
+void fill_common(AttnArgs& a, int H, int N, int D, int g, int kvb, int qph, int kvph, float scale, const Geo& G) {
+    a.H = H;
+    a.N = N;
+    a.Dreal = D;
+    a.g = g;
+    a.kvb = kvb;
+    a.q_pad = qph;
+    a.kv_pad = kvph;
+    a.Mkv = G.Mkv;
+    a.NC = G.NC;
+    a.QM = G.QM;
+    a.Npk = G.Npk;
+    a.sbk = G.sbk;
+    a.Npq = G.Npq;
+    a.QW = (G.QM + 31) / 32;
+    a.scale = scale;
+    a.c = scale * 1.4426950408889634f;
+}
+
+template <int DT>
+int launch_fwd_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
+    switch (Dk) {
+#define FTA_FWD(DK, TPW)                                                                                  \
+    case DK:                                                                                              \
+        hipLaunchKernelGGL((fta_sparse_fwd_kernel<DT, DK, TPW>), dim3(grid), dim3(256), 0, st, a);       \
+        break;
+        FTA_FWD(32, 2)
+        FTA_FWD(64, 2)
+        FTA_FWD(96, 2)
+        FTA_FWD(128, 2)
+        FTA_FWD(160, 1)
+        FTA_FWD(256, 1)
+#undef FTA_FWD
+        default:
+            return fta::arg_error("sparse_attn: unsupported head dim");
+    }
+    return fta::check_launch("fta_sparse_fwd_kernel");
+}
+
+template <int DT>
+int launch_dq_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
+    switch (Dk) {
+#define FTA_DQ(DK)                                                                                       \
+    case DK:                                                                                             \
+        hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, DK>), dim3(grid), dim3(256), 0, st, a);           \
+        break;
+        FTA_DQ(32)
+        FTA_DQ(64)
+        FTA_DQ(96)
+        FTA_DQ(128)
+        FTA_DQ(160)
+        FTA_DQ(256)
+#undef FTA_DQ
+        default:
+            return fta::arg_error("sparse_attn_bwd: unsupported head dim");
+    }
+    return fta::check_launch("fta_sparse_dq_kernel");
+}
+
+template <int DT>
+int launch_dkv_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
+    switch (Dk) {
+#define FTA_DKV(DK)                                                                                      \
+    case DK:                                                                                             \
+        hipLaunchKernelGGL((fta_sparse_dkv_kernel<DT, DK>), dim3(grid), dim3(256), 0, st, a);          \
+        break;
+        FTA_DKV(32)
+        FTA_DKV(64)
+        FTA_DKV(96)
+        FTA_DKV(128)
+        FTA_DKV(160)
+        FTA_DKV(256)
+#undef FTA_DKV
+        default:
+            return fta::arg_error("sparse_attn_bwd: unsupported head dim");
+    }
+    return fta::check_launch("fta_sparse_dkv_kernel");
+}
+
+size_t t_bytes(int B, int H, int Dk, int Np) { return fta::align_up((size_t)B * H * Dk * Np * sizeof(uint16_t)); }
+
+}  // namespace
+
+extern "C" {
+
+size_t fta_sparse_attn_fwd_workspace_size(int B, int H, int N, int D, int q_block_size, int kv_block_size,
+                                          int q_pad_head, int q_pad_tail, int kv_pad_head, int kv_pad_tail) {
+    Geo G;
+    const int64_t nq = (int64_t)q_pad_head + N + q_pad_tail;
+    const int QM = q_block_size > 0 ? (int)(nq / q_block_size) : 0;
+    if (geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
+                 &G) != FTA_OK)
+        return 0;
+    return t_bytes(B, H, G.Dk, G.Npk);
+}
+
+int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                        const void* v, const int64_t* v_strides, int dtype, int B, int H, int N, int D,
+                        const int32_t* merged_indices, int QM, int W, int q_block_size, int kv_block_size,
+                        int q_pad_head, int q_pad_tail, int kv_pad_head, int kv_pad_tail, float scale, void* o,
+                        const int64_t* o_strides, float* lse, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+    FTA_TRY_BEGIN
+    Geo G;
+    int rc = geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
+                      &G);
+    if (rc != FTA_OK) return rc;
+    if (W <= 0) return fta::arg_error("sparse_attn: qblock_topk must be positive");
+    if (workspace_bytes < t_bytes(B, H, G.Dk, G.Npk)) return fta::arg_error("sparse_attn: workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    rc = fta::launch_transpose(v, v_strides, B, H, N, D, G.Dk, G.Npk, kv_pad_head, kv_block_size, G.sbk, workspace,
+                               st);
+    if (rc != FTA_OK) return rc;
+    AttnArgs a = {};
+    a.q = (const uint16_t*)q;
+    a.q_sb = q_strides[0];
+    a.q_sh = q_strides[1];
+    a.q_sn = q_strides[2];
+    a.k = (const uint16_t*)k;
+    a.k_sb = k_strides[0];
+    a.k_sh = k_strides[1];
+    a.k_sn = k_strides[2];
+    a.kvT = (const uint16_t*)workspace;
+    a.merged = merged_indices;
+    a.W = W;
+    a.out0 = (uint16_t*)o;
+    a.o0_sb = o_strides[0];
+    a.o0_sh = o_strides[1];
+    a.o0_sn = o_strides[2];
+    a.lse = lse;
+    fill_common(a, H, N, D, q_block_size, kv_block_size, q_pad_head, kv_pad_head, scale, G);
+    const int T = (G.Dk <= 128) ? 8 : 4;
+    a.wg_per_bh = (G.Npq + 32 * T - 1) / (32 * T);
+    a.total = a.wg_per_bh * B * H;
+    if (dtype == FTA_DTYPE_BF16) return launch_fwd_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);
+    if (dtype == FTA_DTYPE_F16) return launch_fwd_dt<FTA_DTYPE_F16>(a, G.Dk, a.total, st);
+    return fta::arg_error("sparse_attn: dtype must be bf16 or fp16");
+    FTA_TRY_END
+}
+
+size_t fta_sparse_attn_bwd_workspace_size(int B, int H, int N, int D, int q_block_size, int kv_block_size,
+                                          int q_pad_head, int q_pad_tail, int kv_pad_head, int kv_pad_tail) {
+    Geo G;
+    const int64_t nq = (int64_t)q_pad_head + N + q_pad_tail;
+    const int QM = q_block_size > 0 ? (int)(nq / q_block_size) : 0;
+    if (geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
+                 &G) != FTA_OK)
+        return 0;
+    const size_t kt = t_bytes(B, H, G.Dk, G.Npk);
+    const size_t qt = t_bytes(B, H, G.Dk, G.Npq);
+    const size_t sel = fta::align_up((size_t)B * H * G.Mkv * ((QM + 31) / 32) * sizeof(uint32_t));
+    return kt + 2 * qt + sel;
+}
+
+int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                        const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
+                        int dtype, int B, int H, int N, int D, const int32_t* merged_indices, int QM, int W,
+                        int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head,
+                        int kv_pad_tail, float scale, const float* lse, const float* delta, void* dq,
+                        const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                        const int64_t* dv_strides, void* workspace, size_t workspace_bytes, void* stream) {
+    FTA_TRY_BEGIN
+    Geo G;
+    int rc = geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
+                      &G);
+    if (rc != FTA_OK) return rc;
+    if (W <= 0) return fta::arg_error("sparse_attn_bwd: qblock_topk must be positive");
+    if (G.Mkv > 0x3fffffff / 32) return fta::unsupported("sparse_attn_bwd: too many KV blocks");
+    const size_t kt = t_bytes(B, H, G.Dk, G.Npk);
+    const size_t qt = t_bytes(B, H, G.Dk, G.Npq);
+    if (workspace_bytes < fta_sparse_attn_bwd_workspace_size(B, H, N, D, q_block_size, kv_block_size, q_pad_head,
+                                                              q_pad_tail, kv_pad_head, kv_pad_tail))
+        return fta::arg_error("sparse_attn_bwd: workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    char* ws = (char*)workspace;
+    void* ktb = ws;
+    void* qtb = ws + kt;
+    void* dotb = ws + kt + qt;
+    uint32_t* sel = (uint32_t*)(ws + kt + 2 * qt);
+    if ((rc = fta::launch_transpose(k, k_strides, B, H, N, D, G.Dk, G.Npk, kv_pad_head, kv_block_size, G.sbk, ktb,
+                                    st)) != FTA_OK)
+        return rc;
+    if ((rc = fta::launch_transpose(q, q_strides, B, H, N, D, G.Dk, G.Npq, q_pad_head, G.Npq, G.Npq, qtb, st)) !=
+        FTA_OK)
+        return rc;
+    if ((rc = fta::launch_transpose(dout, do_strides, B, H, N, D, G.Dk, G.Npq, q_pad_head, G.Npq, G.Npq, dotb,
+                                    st)) != FTA_OK)
+        return rc;
+    if ((rc = fta::launch_sel_bitmap(merged_indices, B * H, QM, W, G.Mkv, sel, st)) != FTA_OK) return rc;
+
+    AttnArgs a = {};
+    a.q = (const uint16_t*)q;
+    a.q_sb = q_strides[0];
+    a.q_sh = q_strides[1];
+    a.q_sn = q_strides[2];
+    a.k = (const uint16_t*)k;
+    a.k_sb = k_strides[0];
+    a.k_sh = k_strides[1];
+    a.k_sn = k_strides[2];
+    a.v = (const uint16_t*)v;
+    a.v_sb = v_strides[0];
+    a.v_sh = v_strides[1];
+    a.v_sn = v_strides[2];
+    a.dout = (const uint16_t*)dout;
+    a.d_sb = do_strides[0];
+    a.d_sh = do_strides[1];
+    a.d_sn = do_strides[2];
+    a.kvT = (const uint16_t*)ktb;
+    a.qT = (const uint16_t*)qtb;
+    a.doT = (const uint16_t*)dotb;
+    a.merged = merged_indices;
+    a.sel = sel;
+    a.W = W;
+    a.lse_in = lse;
+    a.delta_in = delta;
+    fill_common(a, H, N, D, q_block_size, kv_block_size, q_pad_head, kv_pad_head, scale, G);
+
+    // dQ
+    a.out0 = (uint16_t*)dq;
+    a.o0_sb = dq_strides[0];
+    a.o0_sh = dq_strides[1];
+    a.o0_sn = dq_strides[2];
+    a.wg_per_bh = (G.Npq + 127) / 128;
+    a.total = a.wg_per_bh * B * H;
+    if (dtype == FTA_DTYPE_BF16)
+        rc = launch_dq_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);
+    else if (dtype == FTA_DTYPE_F16)
+        rc = launch_dq_dt<FTA_DTYPE_F16>(a, G.Dk, a.total, st);
+    else
+        rc = fta::arg_error("sparse_attn_bwd: dtype must be bf16 or fp16");
+    if (rc != FTA_OK) return rc;
+
+    // dK, dV
+    a.out0 = (uint16_t*)dk;
+    a.o0_sb = dk_strides[0];
+    a.o0_sh = dk_strides[1];
+    a.o0_sn = dk_strides[2];
+    a.out1 = (uint16_t*)dv;
+    a.o1_sb = dv_strides[0];
+    a.o1_sh = dv_strides[1];
+    a.o1_sn = dv_strides[2];
+    const int ntiles = G.Mkv * ((kv_block_size + 31) / 32);
+    a.wg_per_bh = (ntiles + 3) / 4;
+    a.total = a.wg_per_bh * B * H;
+    if (dtype == FTA_DTYPE_BF16) return launch_dkv_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);
+    return launch_dkv_dt<FTA_DTYPE_F16>(a, G.Dk, a.total, st);
+    FTA_TRY_END
+}
+
+}  // extern "C"

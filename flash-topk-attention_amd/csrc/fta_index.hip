@@ -1,0 +1,413 @@
+// Index kernels: q-block merge, reverse index, count sorts, delta and the
+// token-transposed ("T layout") copies used by the attention kernels.
+//
+// All of them are deterministic: sums run in a fixed order and no result
+// depends on atomic ordering (the reference's merge and reverse-index kernels,
+// flash_topk_attn_v2/csrc/qblock_merge_kernel.cu:44-52 and
+// csrc/build_reverse_indices_kernel.cu:19-25, are not).
+#include "fta_common.h"
+#include "fta_host.h"
+
+// 256-thread exclusive scan; returns the exclusive prefix and writes the total.
+__device__ __forceinline__ int fta_block_scan256(int v, int* s_tmp, int* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) s_tmp[wave] = x;
+    __syncthreads();
+    int wbase = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const int t = s_tmp[w];
+        if (w < wave) wbase += t;
+        tot += t;
+    }
+    __syncthreads();
+    *total = tot;
+    return wbase + x - v;
+}
+
+// ----------------------------------------------------------------------------
+// q-block merge (reference: flash_topk_attn_v2/qblock_merge.py:27-155,
+// csrc/qblock_merge_kernel.cu:8-89).  One workgroup per (b, h, q-block) slice:
+//   acc[id] += score over the slice's g*K (id, score) pairs in (row, slot) order,
+//   positive entries sorted by (score desc, id asc), first W kept.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fta_qblock_merge_kernel(const int32_t* __restrict__ idx,
+                                                               const float* __restrict__ scr, int g, int K, int Mt,
+                                                               int W, int32_t* __restrict__ out_idx,
+                                                               float* __restrict__ out_scr,
+                                                               int32_t* __restrict__ counts) {
+    __shared__ float acc[4096];
+    __shared__ unsigned long long keys[4096];
+    __shared__ int s_tmp[8];
+    // volatile: the clash test below must really re-read LDS after the store,
+    // and the fallback loop must see the previous lane's update.
+    volatile int* owner = reinterpret_cast<volatile int*>(keys);  // reused before the sort
+    volatile float* vacc = acc;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t slice = blockIdx.x;
+    const int32_t* ip = idx + slice * (int64_t)g * K;
+    const float* sp = scr + slice * (int64_t)g * K;
+
+    for (int m = tid; m < Mt; m += 256) acc[m] = 0.f;
+    __syncthreads();
+
+    if (wave == 0) {
+        for (int r = 0; r < g; ++r) {
+            for (int j0 = 0; j0 < K; j0 += 64) {
+                const int j = j0 + lane;
+                int id = -1;
+                float s = 0.f;
+                if (j < K) {
+                    id = ip[r * K + j];
+                    s = sp[r * K + j];
+                }
+                const bool ok = id >= 0 && id < Mt;
+                if (ok) owner[id] = lane;
+                const bool clash = ok && owner[id] != lane;
+                if (__ballot(clash) == 0ull) {
+                    if (ok) vacc[id] = __fadd_rn(vacc[id], s);
+                } else {
+                    for (int l = 0; l < 64; ++l) {
+                        if (lane == l && ok) vacc[id] = __fadd_rn(vacc[id], s);
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // compact positive entries in id order
+    int P = 0;
+    for (int base = 0; base < Mt; base += 256) {
+        const int m = base + tid;
+        const float a = (m < Mt) ? acc[m] : 0.f;
+        const int pos = (a > 0.f) ? 1 : 0;
+        int tot;
+        const int off = fta_block_scan256(pos, s_tmp, &tot);
+        if (pos) {
+            keys[P + off] = ((unsigned long long)__builtin_bit_cast(uint32_t, a) << 32) |
+                            (unsigned long long)(0xffffffffu - (uint32_t)m);
+        }
+        P += tot;
+    }
+    int S = 1;
+    while (S < P) S <<= 1;
+    for (int i = P + tid; i < S; i += 256) keys[i] = 0ull;
+    __syncthreads();
+    for (int size = 2; size <= S; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < S; i += 256) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool desc = (i & size) == 0;
+                    const unsigned long long a = keys[i], b = keys[j];
+                    if (desc ? (a < b) : (a > b)) {
+                        keys[i] = b;
+                        keys[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    const int keep = P < W ? P : W;
+    int32_t* oi = out_idx + slice * (int64_t)W;
+    float* os = out_scr ? out_scr + slice * (int64_t)W : nullptr;
+    for (int p = tid; p < W; p += 256) {
+        if (p < keep) {
+            const unsigned long long key = keys[p];
+            oi[p] = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+            if (os) os[p] = __builtin_bit_cast(float, (uint32_t)(key >> 32));
+        } else {
+            oi[p] = -1;
+            if (os) os[p] = 0.f;
+        }
+    }
+    if (counts && tid == 0) counts[slice] = keep;
+}
+
+// ----------------------------------------------------------------------------
+// Reverse index (reference: flash_topk_attn_v2/sparse_attn_bwd.py:36-76,
+// csrc/build_reverse_indices_kernel.cu:6-104).
+// Membership bitmap sel[bh][m][qm/32] bit (qm%32) = q-block qm selected KV
+// block m.  Bit-OR is order independent, so the lists derived from it (q-block
+// ids ascending) are deterministic.
+// ----------------------------------------------------------------------------
+__global__ void fta_fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+__global__ void fta_sel_bitmap_kernel(const int32_t* __restrict__ merged, int QM, int W, int M, int QW,
+                                      uint32_t* __restrict__ sel) {
+    const int64_t slice = blockIdx.x;  // bh * QM + qm
+    const int64_t bh = slice / QM;
+    const int qm = (int)(slice - bh * QM);
+    for (int s = threadIdx.x; s < W; s += blockDim.x) {
+        const int m = merged[slice * W + s];
+        if (m >= 0 && m < M) atomicOr(&sel[(bh * M + m) * QW + (qm >> 5)], 1u << (qm & 31));
+    }
+}
+
+// One wave per (bh, m): ascending q-block list, -1 fill, count.
+__global__ __launch_bounds__(64) void fta_reverse_lists_kernel(const uint32_t* __restrict__ sel, int QM, int QW,
+                                                                int32_t* __restrict__ rev_idx,
+                                                                int32_t* __restrict__ rev_cnt) {
+    const int64_t row = blockIdx.x;
+    const int lane = threadIdx.x;
+    const uint32_t* w = sel + row * QW;
+    int32_t* out = rev_idx + row * QM;
+    int base = 0;
+    for (int w0 = 0; w0 < QW; w0 += 64) {
+        const uint32_t bits = (w0 + lane < QW) ? w[w0 + lane] : 0u;
+        const int c = __popc(bits);
+        int x = c;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(x, off, 64);
+            if (lane >= off) x += y;
+        }
+        int pos = base + x - c;
+        uint32_t bb = bits;
+        while (bb) {
+            const int j = __ffs(bb) - 1;
+            bb &= bb - 1;
+            out[pos++] = (w0 + lane) * 32 + j;
+        }
+        base += __shfl(x, 63, 64);
+    }
+    for (int i = base + lane; i < QM; i += 64) out[i] = -1;
+    if (lane == 0) rev_cnt[row] = base;
+}
+
+// Stable descending argsort of counts within each row of length n (one WG per
+// row; rank counting keeps ties in ascending index order).
+__global__ __launch_bounds__(256) void fta_argsort_desc_rows_kernel(const int32_t* __restrict__ cnt, int n,
+                                                                     int32_t* __restrict__ out) {
+    __shared__ int c[4096];
+    const int64_t row = blockIdx.x;
+    const int32_t* in = cnt + row * n;
+    for (int i = threadIdx.x; i < n; i += 256) c[i] = in[i];
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const int ci = c[i];
+        int rank = 0;
+        for (int j = 0; j < n; ++j) {
+            const int cj = c[j];
+            rank += (cj > ci) || (cj == ci && j < i);
+        }
+        out[row * n + rank] = i;
+    }
+}
+
+// Global stable descending sort of counts (reference: sort_by_count_cuda.py:33-67):
+// rank_i = #{j : c_j > c_i} + #{j < i : c_j == c_i}.
+__global__ __launch_bounds__(256) void fta_sort_by_count_kernel(const int32_t* __restrict__ cnt, int n,
+                                                                 int32_t* __restrict__ sorted_cnt,
+                                                                 int32_t* __restrict__ sorted_ids) {
+    __shared__ int tile[2048];
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int ci = (i < n) ? cnt[i] : 0;
+    int rank = 0;
+    for (int t0 = 0; t0 < n; t0 += 2048) {
+        __syncthreads();
+        for (int j = threadIdx.x; j < 2048; j += 256) tile[j] = (t0 + j < n) ? cnt[t0 + j] : -2147483647 - 1;
+        __syncthreads();
+        const int lim = (n - t0 < 2048) ? n - t0 : 2048;
+        for (int j = 0; j < lim; ++j) {
+            const int cj = tile[j];
+            rank += (cj > ci) || (cj == ci && t0 + j < i);
+        }
+    }
+    if (i < n) {
+        sorted_cnt[rank] = ci;
+        sorted_ids[rank] = i;
+    }
+}
+
+// ----------------------------------------------------------------------------
+// delta[bh][n] = sum_d O * dO in fp32 (reference: sparse_attn_bwd.py:12-33).
+// ----------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void fta_delta_kernel(const uint16_t* __restrict__ o, int64_t o_sb, int64_t o_sh,
+                                                        int64_t o_sn, const uint16_t* __restrict__ dout,
+                                                        int64_t d_sb, int64_t d_sh, int64_t d_sn, int B, int H,
+                                                        int N, int D, float* __restrict__ delta) {
+    using E = Elem<DT>;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (b, n, h)
+    if (gid >= (int64_t)B * N * H) return;
+    const int h = (int)(gid % H);
+    const int64_t bn = gid / H;
+    const int n = (int)(bn % N), b = (int)(bn / N);
+    const uint16_t* op = o + b * o_sb + h * o_sh + (int64_t)n * o_sn;
+    const uint16_t* dp = dout + b * d_sb + h * d_sh + (int64_t)n * d_sn;
+    float acc = 0.f;
+    for (int d = 0; d < D; d += 8) {
+        const uint4 a = *reinterpret_cast<const uint4*>(op + d);
+        const uint4 c = *reinterpret_cast<const uint4*>(dp + d);
+        const uint32_t av[4] = {a.x, a.y, a.z, a.w}, cv[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            acc = fmaf(E::to_f32((uint16_t)(av[e] & 0xffffu)), E::to_f32((uint16_t)(cv[e] & 0xffffu)), acc);
+            acc = fmaf(E::to_f32((uint16_t)(av[e] >> 16)), E::to_f32((uint16_t)(cv[e] >> 16)), acc);
+        }
+    }
+    delta[((int64_t)b * H + h) * N + n] = acc;
+}
+
+// ----------------------------------------------------------------------------
+// T layout: out[bh][d][p'] for a token-blocked column space: column p' lies in
+// block m = p' / blk_stride at offset r = p' % blk_stride and holds token
+// t = m * blk_len + r - pad when r < blk_len and 0 <= t < N, else 0.
+// (blk_len = blk_stride gives plain padded coordinates p' = t + pad; a stride
+// rounded up to 64 keeps every KV block 64-aligned for any block size.)
+// d < Dk (zero for d >= Dreal).  64 x 64 tiles through LDS.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fta_transpose_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t sh,
+                                                            int64_t sn, int H, int N, int Dreal, int Dk, int Np,
+                                                            int pad, int blk_len, int blk_stride, int ntp, int ntd,
+                                                            uint16_t* __restrict__ out) {
+    __shared__ uint16_t tile[64][66];
+    const int per = ntp * ntd;
+    const int bh = blockIdx.x / per;
+    const int r = blockIdx.x - bh * per;
+    const int tp = r / ntd, td = r - (r / ntd) * ntd;
+    const int b = bh / H, h = bh - (bh / H) * H;
+    const int p0 = tp * 64, d0 = td * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const uint16_t* xp = x + b * sb + h * sh;
+    for (int pp = ty; pp < 64; pp += 4) {
+        const int pc = p0 + pp;
+        const int m = pc / blk_stride, rr = pc - (pc / blk_stride) * blk_stride;
+        const int t = m * blk_len + rr - pad, d = d0 + tx;
+        uint16_t v = 0;
+        if (rr < blk_len && t >= 0 && t < N && d < Dreal) v = xp[(int64_t)t * sn + d];
+        tile[pp][tx] = v;
+    }
+    __syncthreads();
+    uint16_t* op = out + (int64_t)bh * Dk * Np;
+    for (int dd = ty; dd < 64; dd += 4) {
+        const int d = d0 + dd, pc = p0 + tx;
+        if (d < Dk && pc < Np) op[(int64_t)d * Np + pc] = tile[tx][dd];
+    }
+}
+
+namespace fta {
+int launch_transpose(const void* x, const int64_t* s, int B, int H, int N, int Dreal, int Dk, int Np, int pad,
+                     int blk_len, int blk_stride, void* out, hipStream_t st) {
+    const int ntp = (Np + 63) / 64, ntd = (Dk + 63) / 64;
+    const int64_t grid = (int64_t)B * H * ntp * ntd;
+    if (grid > 0)
+        hipLaunchKernelGGL(fta_transpose_kernel, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)x, s[0],
+                           s[1], s[2], H, N, Dreal, Dk, Np, pad, blk_len, blk_stride, ntp, ntd, (uint16_t*)out);
+    return check_launch("fta_transpose_kernel");
+}
+
+int launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t st) {
+    if (n <= 0) return FTA_OK;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(fta_fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p, n, v);
+    return check_launch("fta_fill_u32_kernel");
+}
+
+int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint32_t* sel, hipStream_t st) {
+    const int QW = (QM + 31) / 32;
+    int rc = launch_fill_u32(sel, (int64_t)BH * M * QW, 0u, st);
+    if (rc != FTA_OK) return rc;
+    if ((int64_t)BH * QM > 0)
+        hipLaunchKernelGGL(fta_sel_bitmap_kernel, dim3((unsigned)((int64_t)BH * QM)), dim3(128), 0, st, merged, QM,
+                           W, M, QW, sel);
+    return check_launch("fta_sel_bitmap_kernel");
+}
+}  // namespace fta
+
+extern "C" {
+
+int fta_qblock_merge(const int32_t* topk_indices, const float* topk_scores, int64_t num_slices, int q_block_size,
+                     int k_per_query, int num_score_blocks, int qblock_topk, int32_t* merged_indices,
+                     float* merged_scores, int32_t* counts, void* stream) {
+    FTA_TRY_BEGIN
+    if (num_slices < 0 || num_slices > 0x7fffffff) return fta::arg_error("qblock_merge: bad slice count");
+    if (q_block_size <= 0 || k_per_query < 0) return fta::arg_error("qblock_merge: bad q_block_size / K");
+    if (num_score_blocks <= 0) return fta::arg_error("num_score_blocks must be positive");
+    if (num_score_blocks > 4096) return fta::unsupported("num_score_blocks exceeds block sort limit 4096");
+    if (qblock_topk <= 0) return fta::arg_error("qblock_topk must be positive");
+    if (num_slices == 0) return FTA_OK;
+    hipLaunchKernelGGL(fta_qblock_merge_kernel, dim3((unsigned)num_slices), dim3(256), 0, (hipStream_t)stream,
+                       topk_indices, topk_scores, q_block_size, k_per_query, num_score_blocks, qblock_topk,
+                       merged_indices, merged_scores, counts);
+    return fta::check_launch("fta_qblock_merge_kernel");
+    FTA_TRY_END
+}
+
+size_t fta_build_reverse_indices_workspace_size(int B, int H, int QM, int M) {
+    return fta::align_up((size_t)B * H * M * ((QM + 31) / 32) * sizeof(uint32_t));
+}
+
+int fta_build_reverse_indices(const int32_t* merged_indices, const int32_t* counts, int B, int H, int QM, int W,
+                              int M, int32_t* reverse_indices, int32_t* reverse_counts, int32_t* sorted_kv_indices,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+    FTA_TRY_BEGIN
+    (void)counts;  // membership is read from the -1 padded lists directly
+    if (B <= 0 || H <= 0 || QM <= 0 || W <= 0 || M <= 0) return fta::arg_error("build_reverse_indices: bad dims");
+    if (M > 4096) return fta::unsupported("build_reverse_indices: M exceeds 4096");
+    if (workspace_bytes < fta_build_reverse_indices_workspace_size(B, H, QM, M))
+        return fta::arg_error("build_reverse_indices: workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    uint32_t* sel = (uint32_t*)workspace;
+    int rc = fta::launch_sel_bitmap(merged_indices, B * H, QM, W, M, sel, st);
+    if (rc != FTA_OK) return rc;
+    const int QW = (QM + 31) / 32;
+    hipLaunchKernelGGL(fta_reverse_lists_kernel, dim3((unsigned)((int64_t)B * H * M)), dim3(64), 0, st, sel, QM, QW,
+                       reverse_indices, reverse_counts);
+    rc = fta::check_launch("fta_reverse_lists_kernel");
+    if (rc != FTA_OK) return rc;
+    if (sorted_kv_indices) {
+        hipLaunchKernelGGL(fta_argsort_desc_rows_kernel, dim3((unsigned)(B * H)), dim3(256), 0, st, reverse_counts,
+                           M, sorted_kv_indices);
+        rc = fta::check_launch("fta_argsort_desc_rows_kernel");
+    }
+    return rc;
+    FTA_TRY_END
+}
+
+int fta_sort_by_count(const int32_t* reverse_counts, int64_t total, int32_t* sorted_counts, int32_t* sorted_ids,
+                      void* stream) {
+    FTA_TRY_BEGIN
+    if (total < 0 || total > 0x7fffffff) return fta::arg_error("sort_by_count: bad size");
+    if (total == 0) return FTA_OK;
+    hipLaunchKernelGGL(fta_sort_by_count_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, reverse_counts, (int)total, sorted_counts, sorted_ids);
+    return fta::check_launch("fta_sort_by_count_kernel");
+    FTA_TRY_END
+}
+
+int fta_preprocess_delta(const void* o, const int64_t* o_strides, const void* dout, const int64_t* do_strides,
+                         int dtype, int B, int H, int N, int D, float* delta, void* stream) {
+    FTA_TRY_BEGIN
+    if (B <= 0 || H <= 0 || N <= 0 || D <= 0 || D % 8) return fta::arg_error("preprocess_delta: bad dims");
+    const int64_t n = (int64_t)B * N * H;
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    hipStream_t st = (hipStream_t)stream;
+    if (dtype == FTA_DTYPE_BF16)
+        hipLaunchKernelGGL((fta_delta_kernel<FTA_DTYPE_BF16>), dim3(grid), dim3(256), 0, st, (const uint16_t*)o,
+                           o_strides[0], o_strides[1], o_strides[2], (const uint16_t*)dout, do_strides[0],
+                           do_strides[1], do_strides[2], B, H, N, D, delta);
+    else if (dtype == FTA_DTYPE_F16)
+        hipLaunchKernelGGL((fta_delta_kernel<FTA_DTYPE_F16>), dim3(grid), dim3(256), 0, st, (const uint16_t*)o,
+                           o_strides[0], o_strides[1], o_strides[2], (const uint16_t*)dout, do_strides[0],
+                           do_strides[1], do_strides[2], B, H, N, D, delta);
+    else
+        return fta::arg_error("preprocess_delta: dtype must be bf16 or fp16");
+    return fta::check_launch("fta_delta_kernel");
+    FTA_TRY_END
+}
+
+}  // extern "C"

@@ -1,0 +1,585 @@
+// Block scoring and top-k selection for gfx950.
+//
+// Block scoring (reference: flash_topk_attn_v2/csrc/block_score_kernel.cu:19-314,
+// flash_topk_attn_v2/block_score.py:295-366) computes, for every query t and
+// virtual score block j of b keys,
+//     score[t, j] = sum_{keys i in block j} softmax(q_t K^T / sqrt(D))_i .
+// Here it is done in two stages:
+//   1. fta_block_score_lse_kernel streams K once per 256-query tile and emits the
+//      per-block log2-sum-exp  lse2[j, t] = log2 sum_{i in j} 2^{c s_i}
+//      (c = scale * log2 e) plus the row total lse2[t]; both fp32.  Layout of
+//      the per-block values is [BH][M][N] so that lanes (= queries) store
+//      contiguously.
+//   2. score = 2^{lse2[j, t] - lse2[t]}, either materialised by
+//      fta_block_normalize_kernel ([BH][N][M], the public block-score tensor) or
+//      consumed directly by the top-k selector (fused path, no [BH][N][M] array).
+//
+// Top-k selection (reference: flash_topk_attn_v2/topk_select.py:128-182 and
+// csrc/topk_select_kernel.cu:7-131) ranks blocks by avg = raw / valid_count,
+// ties to the lower block index, keeps the first max_topk, and truncates after
+// the first position whose sequential fp32 cumulative sum of avg * valid_count
+// reaches the threshold.
+#include "fta_common.h"
+
+// ----------------------------------------------------------------------------
+// Stage 1: per-block log2-sum-exp.
+// WG = 4 waves, each wave owns 64 queries (two 32-column MFMA tiles); the WG
+// stages 64-key chunks of K in LDS (double-buffered).  S^T = K Q^T so that each
+// lane holds 16 keys of one query per 32x32 tile and the reduction over keys is
+// in-lane plus one exchange with lane ^ 32.
+// ----------------------------------------------------------------------------
+template <int DT, int D>
+__global__ __launch_bounds__(256, 2) void fta_block_score_lse_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+    int H, int N, int Dreal, int M, int bsz, int pad_head, float c,
+    float* __restrict__ blk_lse, float* __restrict__ row_lse, int qtiles, int total) {
+    using E = Elem<DT>;
+    constexpr int KS = D / 16;
+    constexpr int ROW = D + 8;  // +16 B per LDS row against bank conflicts
+    constexpr int SEGS = D / 8;
+    constexpr int LOADS = (64 * SEGS) / 256;
+    static_assert((64 * SEGS) % 256 == 0, "D must be a multiple of 32");
+    __shared__ __align__(16) uint16_t sk[2][64 * ROW];
+
+    const int wg = fta_xcd_remap(blockIdx.x, total);
+    const int bh = wg / qtiles;
+    const int qt = wg - bh * qtiles;
+    const int b = bh / H, h = bh - (bh / H) * H;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int qbase = qt * 256 + wave * 64;
+    const uint16_t* qp = q + b * q_sb + h * q_sh;
+    const uint16_t* kp = k + b * k_sb + h * k_sh;
+
+    uint4 qf[2][KS];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int qi = qbase + t * 32 + (lane & 31);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d = ks * 16 + (lane >> 5) * 8;
+            qf[t][ks] = (qi < N && d < Dreal) ? *reinterpret_cast<const uint4*>(qp + (int64_t)qi * q_sn + d)
+                                              : fta_zero4();
+        }
+    }
+
+    const int nchunk = (bsz + 63) >> 6;
+    const int total_it = M * nchunk;
+    uint4 stage[LOADS];
+
+    auto load_chunk = [&](int it) {
+        const int m = it / nchunk, ch = it - (it / nchunk) * nchunk;
+        const int kb = m * bsz - pad_head + ch * 64;
+        const int rem = bsz - ch * 64;
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int s = tid + i * 256;
+            const int row = s / SEGS, seg = s - (s / SEGS) * SEGS;
+            const int t = kb + row;
+            const bool ok = row < rem && t >= 0 && t < N && seg * 8 < Dreal;
+            stage[i] = ok ? *reinterpret_cast<const uint4*>(kp + (int64_t)t * k_sn + seg * 8) : fta_zero4();
+        }
+    };
+    auto store_chunk = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int s = tid + i * 256;
+            const int row = s / SEGS, seg = s - (s / SEGS) * SEGS;
+            *reinterpret_cast<uint4*>(&sk[buf][row * ROW + seg * 8]) = stage[i];
+        }
+    };
+
+    float m_run[2] = {-FTA_INF, -FTA_INF}, L_run[2] = {0.f, 0.f};
+    float mb[2] = {-FTA_INF, -FTA_INF}, lb[2] = {0.f, 0.f};
+
+    load_chunk(0);
+    store_chunk(0);
+    __syncthreads();
+
+    for (int it = 0; it < total_it; ++it) {
+        const int buf = it & 1;
+        if (it + 1 < total_it) load_chunk(it + 1);
+        const int m = it / nchunk, ch = it - (it / nchunk) * nchunk;
+        const int kb = m * bsz - pad_head + ch * 64;
+        const int rem = bsz - ch * 64;
+        const bool two = rem > 32;
+
+        f32x16 acc[2][2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[s][t][i] = 0.f;
+
+        const uint16_t* base = &sk[buf][0];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const uint4 a0 =
+                *reinterpret_cast<const uint4*>(base + (lane & 31) * ROW + ks * 16 + (lane >> 5) * 8);
+            acc[0][0] = E::mma(a0, qf[0][ks], acc[0][0]);
+            acc[0][1] = E::mma(a0, qf[1][ks], acc[0][1]);
+        }
+        if (two) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const uint4 a1 = *reinterpret_cast<const uint4*>(base + (32 + (lane & 31)) * ROW + ks * 16 +
+                                                                 (lane >> 5) * 8);
+                acc[1][0] = E::mma(a1, qf[0][ks], acc[1][0]);
+                acc[1][1] = E::mma(a1, qf[1][ks], acc[1][1]);
+            }
+        }
+
+        const bool need_mask = kb < 0 || kb + 64 > N || rem < 64;
+        if (need_mask) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int rel = s * 32 + c_row(i, lane);
+                    const int t = kb + rel;
+                    if (rel >= rem || t < 0 || t >= N) {
+                        acc[s][0][i] = -FTA_INF;
+                        acc[s][1][i] = -FTA_INF;
+                    }
+                }
+        }
+
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            float mx = acc[0][t][0];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, acc[0][t][i]);
+            if (two) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mx = fmaxf(mx, acc[1][t][i]);
+            }
+            mx = fmaxf(mx, fta_xor32(mx));
+            const float mref = (ch == 0) ? mx : fmaxf(mb[t], mx);
+            const float mr = (mref == -FTA_INF) ? 0.f : mref;
+            const float mc = mr * c;
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sum += fta_exp2(fmaf(acc[0][t][i], c, -mc));
+            if (two) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sum += fta_exp2(fmaf(acc[1][t][i], c, -mc));
+            }
+            sum += fta_xor32(sum);
+            lb[t] = (ch == 0) ? sum : fmaf(lb[t], fta_exp2((mb[t] - mr) * c), sum);
+            mb[t] = mref;
+        }
+
+        if (ch == nchunk - 1) {
+            float lse_b[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                lse_b[t] = (lb[t] > 0.f) ? fmaf(mb[t], c, fta_log2(lb[t])) : -FTA_INF;
+                if (lb[t] > 0.f) {
+                    const float mn = fmaxf(m_run[t], mb[t]);
+                    L_run[t] = L_run[t] * fta_exp2((m_run[t] - mn) * c) + lb[t] * fta_exp2((mb[t] - mn) * c);
+                    m_run[t] = mn;
+                }
+            }
+            const int qi = qbase + lane;
+            if (qi < N) blk_lse[((int64_t)bh * M + m) * N + qi] = (lane < 32) ? lse_b[0] : lse_b[1];
+        }
+
+        if (it + 1 < total_it) store_chunk(buf ^ 1);
+        __syncthreads();
+    }
+
+    const int qi = qbase + lane;
+    if (qi < N) {
+        const int t = lane >> 5;
+        const float mr = (t == 0) ? m_run[0] : m_run[1];
+        const float Lr = (t == 0) ? L_run[0] : L_run[1];
+        row_lse[(int64_t)bh * N + qi] = (Lr > 0.f) ? fmaf(mr, c, fta_log2(Lr)) : -FTA_INF;
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Stage 2a: materialise scores[bh][n][m] = 2^{lse2[bh][m][n] - lse2[bh][n]}.
+// 64 x 64 tiles transposed through LDS.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fta_block_normalize_kernel(const float* __restrict__ blk_lse,
+                                                                  const float* __restrict__ row_lse,
+                                                                  float* __restrict__ scores, int N, int M,
+                                                                  int ntiles_n, int ntiles_m) {
+    __shared__ float tile[64][65];
+    const int bh = blockIdx.x / (ntiles_n * ntiles_m);
+    const int r = blockIdx.x - bh * ntiles_n * ntiles_m;
+    const int tn = r / ntiles_m, tm = r - (r / ntiles_m) * ntiles_m;
+    const int n0 = tn * 64, m0 = tm * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int mm = ty; mm < 64; mm += 4) {
+        const int m = m0 + mm, n = n0 + tx;
+        float v = 0.f;
+        if (m < M && n < N) v = blk_lse[((int64_t)bh * M + m) * N + n] - row_lse[(int64_t)bh * N + n];
+        tile[mm][tx] = v;
+    }
+    __syncthreads();
+    for (int nn = ty; nn < 64; nn += 4) {
+        const int n = n0 + nn, m = m0 + tx;
+        if (m < M && n < N) scores[((int64_t)bh * N + n) * M + m] = fta_exp2(tile[tx][nn]);
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Stage 2b: top-k selection, one lane per query row.
+// Single pass over the M blocks: a block becomes a candidate when it beats the
+// current K-th best (tau); candidates are parked in a per-lane LDS list and
+// merged into a sorted register list (insertion network) whenever some lane's
+// list is full, after which tau tightens.  Exact for any input; deterministic.
+// MODE 0 reads raw scores in[row * stride_row + m * stride_m];
+// MODE 1 reads the lse2 intermediate ([BH][M][N]) and row totals.
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ bool fta_better(float v, int i, float w, int j) {
+    return v > w || (v == w && i < j);
+}
+
+__device__ __forceinline__ int fta_valid_count(int m, int M, int bsz, int pad_head, int pad_tail) {
+    int vc = bsz;
+    if (pad_head > 0 && m == 0) vc -= pad_head;
+    if (pad_tail > 0 && m == M - 1) vc -= pad_tail;
+    return vc;
+}
+
+template <int KB, int MODE>
+__global__ __launch_bounds__(256) void fta_topk_select_kernel(
+    const float* __restrict__ in, int64_t stride_row, int64_t stride_m, const float* __restrict__ row_lse,
+    int N, int rows, int M, int m_out, int bsz, int pad_head, int pad_tail, float threshold,
+    int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg) {
+    constexpr int CAP = 32;
+    __shared__ float cand_v[4][CAP][64];
+    __shared__ int cand_i[4][CAP][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row = blockIdx.x * 256 + tid;
+    const bool active = row < rows;
+
+    float lv[KB];
+    int li[KB];
+#pragma unroll
+    for (int p = 0; p < KB; ++p) {
+        lv[p] = -FTA_INF;
+        li[p] = 0x7fffffff;
+    }
+    float tv = -FTA_INF;
+    int ti = 0x7fffffff;
+    int cnt = 0;
+
+    const float* src = nullptr;
+    float rl = 0.f;
+    int64_t bh = 0, n = 0;
+    if (MODE == 0) {
+        src = in + (int64_t)(active ? row : 0) * stride_row;
+    } else {
+        bh = (active ? row : 0) / N;
+        n = (active ? row : 0) - bh * N;
+        src = in + bh * (int64_t)M * N + n;
+        rl = row_lse[active ? row : 0];
+    }
+
+    auto flush = [&]() {
+        for (int j = 0; j < CAP; ++j) {
+            const bool ok = j < cnt;
+            const float v = ok ? cand_v[wave][j][lane] : -FTA_INF;
+            const int id = ok ? cand_i[wave][j][lane] : 0x7fffffff;
+            bool bt[KB];
+#pragma unroll
+            for (int p = 0; p < KB; ++p) bt[p] = fta_better(v, id, lv[p], li[p]);
+#pragma unroll
+            for (int p = KB - 1; p > 0; --p) {
+                const float nv = bt[p - 1] ? lv[p - 1] : (bt[p] ? v : lv[p]);
+                const int ni = bt[p - 1] ? li[p - 1] : (bt[p] ? id : li[p]);
+                lv[p] = nv;
+                li[p] = ni;
+            }
+            if (bt[0]) {
+                lv[0] = v;
+                li[0] = id;
+            }
+        }
+        cnt = 0;
+#pragma unroll
+        for (int p = 0; p < KB; ++p)
+            if (p == m_out - 1) {
+                tv = lv[p];
+                ti = li[p];
+            }
+    };
+
+    for (int m = 0; m < M; ++m) {
+        float raw;
+        if (MODE == 0) {
+            raw = active ? src[m * stride_m] : 0.f;
+        } else {
+            raw = active ? fta_exp2(src[(int64_t)m * N] - rl) : 0.f;
+        }
+        const float avg = raw / (float)fta_valid_count(m, M, bsz, pad_head, pad_tail);
+        if (active && fta_better(avg, m, tv, ti)) {
+            cand_v[wave][cnt][lane] = avg;
+            cand_i[wave][cnt][lane] = m;
+            ++cnt;
+        }
+        if (__ballot(cnt == CAP) != 0ull) flush();
+    }
+    flush();
+
+    if (!active) return;
+    float cs = 0.f;
+    int cut = m_out;
+    bool found = false;
+#pragma unroll
+    for (int p = 0; p < KB; ++p) {
+        if (p < m_out && !found) {
+            const float rw = __fmul_rn(lv[p], (float)fta_valid_count(li[p], M, bsz, pad_head, pad_tail));
+            cs = __fadd_rn(cs, rw);
+            if (cs >= threshold) {
+                cut = p + 1;
+                found = true;
+            }
+        }
+    }
+    const int64_t o = (int64_t)row * m_out;
+#pragma unroll
+    for (int p = 0; p < KB; ++p) {
+        if (p < m_out) {
+            const bool keep = p < cut;
+            out_idx[o + p] = keep ? li[p] : -1;
+            out_avg[o + p] = keep ? lv[p] : 0.f;
+            out_raw[o + p] =
+                keep ? __fmul_rn(lv[p], (float)fta_valid_count(li[p], M, bsz, pad_head, pad_tail)) : 0.f;
+        }
+    }
+}
+
+// Slow general path for m_out > 64: one workgroup per row, bitonic sort of the
+// M (<= 4096) 64-bit keys (orderable avg bits, ~index) in LDS.
+__device__ __forceinline__ uint32_t fta_orderable(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float fta_unorderable(uint32_t u) {
+    return __builtin_bit_cast(float, (u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void fta_topk_select_sort_kernel(
+    const float* __restrict__ in, int64_t stride_row, int64_t stride_m, const float* __restrict__ row_lse,
+    int N, int M, int m_out, int bsz, int pad_head, int pad_tail, float threshold,
+    int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg) {
+    __shared__ unsigned long long keys[4096];
+    __shared__ int s_cut;
+    const int row = blockIdx.x;
+    int S = 1;
+    while (S < M) S <<= 1;
+    int64_t bh = row / N, n = row - (row / N) * N;
+    for (int m = threadIdx.x; m < S; m += 256) {
+        unsigned long long key = 0ull;
+        if (m < M) {
+            float raw;
+            if (MODE == 0)
+                raw = in[(int64_t)row * stride_row + m * stride_m];
+            else
+                raw = fta_exp2(in[(bh * M + m) * (int64_t)N + n] - row_lse[row]);
+            const float avg = raw / (float)fta_valid_count(m, M, bsz, pad_head, pad_tail);
+            key = ((unsigned long long)fta_orderable(avg) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)m);
+        }
+        keys[m] = key;
+    }
+    __syncthreads();
+    for (int size = 2; size <= S; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < S; i += 256) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool desc = (i & size) == 0;
+                    const unsigned long long a = keys[i], bb = keys[j];
+                    if (desc ? (a < bb) : (a > bb)) {
+                        keys[i] = bb;
+                        keys[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (threadIdx.x == 0) {
+        float cs = 0.f;
+        int cut = m_out;
+        for (int p = 0; p < m_out; ++p) {
+            const unsigned long long key = keys[p];
+            const int id = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+            const float avg = fta_unorderable((uint32_t)(key >> 32));
+            cs = __fadd_rn(cs, __fmul_rn(avg, (float)fta_valid_count(id, M, bsz, pad_head, pad_tail)));
+            if (cs >= threshold) {
+                cut = p + 1;
+                break;
+            }
+        }
+        s_cut = cut;
+    }
+    __syncthreads();
+    const int cut = s_cut;
+    for (int p = threadIdx.x; p < m_out; p += 256) {
+        const unsigned long long key = keys[p];
+        const int id = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+        const float avg = fta_unorderable((uint32_t)(key >> 32));
+        const bool keep = p < cut;
+        const int64_t o = (int64_t)row * m_out + p;
+        out_idx[o] = keep ? id : -1;
+        out_avg[o] = keep ? avg : 0.f;
+        out_raw[o] = keep ? __fmul_rn(avg, (float)fta_valid_count(id, M, bsz, pad_head, pad_tail)) : 0.f;
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Host launchers (extern "C" ABI, declared in include/fta.h)
+// ----------------------------------------------------------------------------
+#include "fta_host.h"
+
+namespace {
+
+template <int DT>
+int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D, int Dk, const int64_t* qs,
+                        const int64_t* ks, int M, int bsz, int pad_head, float scale, float* blk_lse,
+                        float* row_lse, hipStream_t st) {
+    const int qtiles = (N + 255) / 256;
+    const int total = qtiles * B * H;
+    const float c = scale * 1.4426950408889634f;
+#define FTA_LAUNCH_SCORE(DK)                                                                               \
+    hipLaunchKernelGGL((fta_block_score_lse_kernel<DT, DK>), dim3(total), dim3(256), 0, st,                \
+                       (const uint16_t*)q, (const uint16_t*)k, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], H, N, \
+                       D, M, bsz, pad_head, c, blk_lse, row_lse, qtiles, total)
+    switch (Dk) {
+        case 32: FTA_LAUNCH_SCORE(32); break;
+        case 64: FTA_LAUNCH_SCORE(64); break;
+        case 96: FTA_LAUNCH_SCORE(96); break;
+        case 128: FTA_LAUNCH_SCORE(128); break;
+        case 160: FTA_LAUNCH_SCORE(160); break;
+        case 256: FTA_LAUNCH_SCORE(256); break;
+        default: return fta::arg_error("block_score: unsupported head dim");
+    }
+#undef FTA_LAUNCH_SCORE
+    return fta::check_launch("fta_block_score_lse_kernel");
+}
+
+int launch_score_lse(const void* q, const void* k, int dtype, int B, int H, int N, int D, const int64_t* qs,
+                     const int64_t* ks, int M, int bsz, int pad_head, float scale, float* blk_lse, float* row_lse,
+                     hipStream_t st) {
+    const int Dk = fta::kernel_head_dim(D);
+    if (Dk < 0) return fta::arg_error("block_score: head dim must be <= 256");
+    if (D % 8 != 0) return fta::arg_error("block_score: head dim must be a multiple of 8");
+    if (dtype == FTA_DTYPE_BF16)
+        return launch_score_lse_dt<FTA_DTYPE_BF16>(q, k, B, H, N, D, Dk, qs, ks, M, bsz, pad_head, scale, blk_lse,
+                                                   row_lse, st);
+    if (dtype == FTA_DTYPE_F16)
+        return launch_score_lse_dt<FTA_DTYPE_F16>(q, k, B, H, N, D, Dk, qs, ks, M, bsz, pad_head, scale, blk_lse,
+                                                  row_lse, st);
+    return fta::arg_error("block_score: dtype must be bf16 or fp16");
+}
+
+template <int MODE>
+int launch_topk(const float* in, int64_t stride_row, int64_t stride_m, const float* row_lse, int N, int rows,
+                int M, int m_out, int bsz, int pad_head, int pad_tail, float threshold, int32_t* idx, float* raw,
+                float* avg, hipStream_t st) {
+    if (rows == 0) return FTA_OK;
+    if (m_out <= 64) {
+        const int grid = (rows + 255) / 256;
+#define FTA_LAUNCH_TOPK(KB)                                                                                \
+    hipLaunchKernelGGL((fta_topk_select_kernel<KB, MODE>), dim3(grid), dim3(256), 0, st, in, stride_row,   \
+                       stride_m, row_lse, N, rows, M, m_out, bsz, pad_head, pad_tail, threshold, idx, raw, avg)
+        if (m_out <= 8)
+            FTA_LAUNCH_TOPK(8);
+        else if (m_out <= 16)
+            FTA_LAUNCH_TOPK(16);
+        else if (m_out <= 32)
+            FTA_LAUNCH_TOPK(32);
+        else
+            FTA_LAUNCH_TOPK(64);
+#undef FTA_LAUNCH_TOPK
+    } else {
+        hipLaunchKernelGGL((fta_topk_select_sort_kernel<MODE>), dim3(rows), dim3(256), 0, st, in, stride_row,
+                           stride_m, row_lse, N, M, m_out, bsz, pad_head, pad_tail, threshold, idx, raw, avg);
+    }
+    return fta::check_launch("fta_topk_select_kernel");
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fta_block_score_workspace_size(int B, int H, int N, int M) {
+    return fta::align_up((size_t)B * H * M * N * sizeof(float)) + fta::align_up((size_t)B * H * N * sizeof(float));
+}
+
+int fta_block_score(const void* q, const void* k, int dtype, int B, int H, int N, int D, const int64_t* q_strides,
+                    const int64_t* k_strides, int score_block_size, int pad_head, int pad_tail, float scale,
+                    float* scores, void* workspace, size_t workspace_bytes, void* stream) {
+    FTA_TRY_BEGIN
+    int M = 0;
+    int st = fta::check_score_args(B, H, N, D, score_block_size, pad_head, pad_tail, &M);
+    if (st != FTA_OK) return st;
+    if (!q || !k || !scores) return fta::arg_error("block_score: null pointer");
+    if (workspace_bytes < fta_block_score_workspace_size(B, H, N, M))
+        return fta::arg_error("block_score: workspace too small");
+    float* blk_lse = (float*)workspace;
+    float* row_lse = (float*)((char*)workspace + fta::align_up((size_t)B * H * M * N * sizeof(float)));
+    hipStream_t s = (hipStream_t)stream;
+    st = launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, scale,
+                          blk_lse, row_lse, s);
+    if (st != FTA_OK) return st;
+    const int tn = (N + 63) / 64, tm = (M + 63) / 64;
+    if ((int64_t)B * H * tn * tm > 0) {
+        hipLaunchKernelGGL(fta_block_normalize_kernel, dim3(B * H * tn * tm), dim3(256), 0, s, blk_lse, row_lse,
+                           scores, N, M, tn, tm);
+    }
+    return fta::check_launch("fta_block_normalize_kernel");
+    FTA_TRY_END
+}
+
+int fta_topk_select(const float* block_scores, int64_t rows, int M, int64_t stride_row, int64_t stride_m,
+                    int max_topk, int score_block_size, int pad_head, int pad_tail, float threshold,
+                    int32_t* topk_indices, float* topk_raw, float* topk_avg, void* stream) {
+    FTA_TRY_BEGIN
+    if (M <= 0) return fta::arg_error("topk_select: M must be positive");
+    if (M > 4096) return fta::unsupported("topk_select: M exceeds 4096");
+    if (score_block_size <= 0) return fta::arg_error("topk_select: score_block_size must be positive");
+    if (pad_head < 0 || pad_tail < 0 || pad_head >= score_block_size || pad_tail >= score_block_size)
+        return fta::arg_error("topk_select: bad padding");
+    if (max_topk < 0) return fta::arg_error("topk_select: max_topk must be >= 0");
+    if (rows < 0 || rows > 0x7fffffff) return fta::arg_error("topk_select: bad row count");
+    const int m_out = (max_topk > 0 && max_topk < M) ? max_topk : M;
+    return launch_topk<0>(block_scores, stride_row, stride_m, nullptr, 1, (int)rows, M, m_out, score_block_size,
+                          pad_head, pad_tail, threshold, topk_indices, topk_raw, topk_avg, (hipStream_t)stream);
+    FTA_TRY_END
+}
+
+size_t fta_topk_score_workspace_size(int B, int H, int N, int M) { return fta_block_score_workspace_size(B, H, N, M); }
+
+int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N, int D, const int64_t* q_strides,
+                   const int64_t* k_strides, int score_block_size, int pad_head, int pad_tail, float scale,
+                   int max_topk, float threshold, int32_t* topk_indices, float* topk_raw, float* topk_avg,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+    FTA_TRY_BEGIN
+    int M = 0;
+    int st = fta::check_score_args(B, H, N, D, score_block_size, pad_head, pad_tail, &M);
+    if (st != FTA_OK) return st;
+    if (M > 4096) return fta::unsupported("topk_score: M exceeds 4096");
+    if (max_topk < 0) return fta::arg_error("topk_score: max_topk must be >= 0");
+    if (workspace_bytes < fta_topk_score_workspace_size(B, H, N, M))
+        return fta::arg_error("topk_score: workspace too small");
+    float* blk_lse = (float*)workspace;
+    float* row_lse = (float*)((char*)workspace + fta::align_up((size_t)B * H * M * N * sizeof(float)));
+    hipStream_t s = (hipStream_t)stream;
+    st = launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, scale,
+                          blk_lse, row_lse, s);
+    if (st != FTA_OK) return st;
+    const int m_out = (max_topk > 0 && max_topk < M) ? max_topk : M;
+    return launch_topk<1>(blk_lse, 0, 0, row_lse, N, B * H * N, M, m_out, score_block_size, pad_head, pad_tail,
+                          threshold, topk_indices, topk_raw, topk_avg, s);
+    FTA_TRY_END
+}
+
+}  // extern "C"

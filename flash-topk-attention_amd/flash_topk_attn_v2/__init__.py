@@ -1,0 +1,190 @@
+"""MI355X (gfx950) flash-topk-attention V2 hot path.
+
+Drop-in for the public API of the reference package ``flash_topk_attn_v2``
+(flash_topk_attn_v2/__init__.py:16-176): ``flash_topk_score``,
+``build_qblock_topk_indices`` and ``flash_topk_attn`` (differentiable), with
+the same signatures, argument checks and return conventions.  All compute runs
+in hand-written HIP kernels (libfta_gfx950.so, C ABI in include/fta.h).
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from .block_score import _parse_block_score_args, _prepare_qk, flash_block_score
+from .qblock_merge import flash_qblock_merge
+from .sparse_attn import FlashSparseAttnFunc, flash_sparse_attn
+from .sparse_attn_bwd import flash_build_reverse_indices, flash_sort_by_count, preprocess_delta
+from .topk_select import flash_topk_select
+
+
+def flash_topk_score(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    num_heads: Optional[int] = None,
+    score_block_size: int = 64,
+    topk: int = 16,
+    padding: Tuple[int, int] = (0, 0),
+    threshold: float = 1.0,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Block-level top-k scoring (reference: flash_topk_attn_v2/__init__.py:16-54).
+
+    Returns ``(topk_indices int32, topk_raw_scores f32, topk_avg_scores f32)``,
+    each ``[B, H, N, min(topk, M)]`` (``M`` when ``topk == 0``).  Scoring and
+    selection run fused: the ``[B, H, N, M]`` score tensor is never
+    materialised.
+    """
+    input_4d = q.ndim == 4
+    if input_4d:
+        _, head_count, _, _ = q.shape
+        if num_heads is not None and num_heads != head_count:
+            raise ValueError(f"num_heads ({num_heads}) != q.shape[1] ({head_count})")
+        num_heads = head_count
+    else:
+        if q.ndim != 3:
+            raise ValueError("q must be 3D [B, N, C] or 4D [B, H, N, D]")
+        if num_heads is None:
+            raise ValueError("num_heads is required for 3D [B, N, C] input")
+
+    parsed = _parse_block_score_args(q, k, num_heads, score_block_size, padding)
+    input_4d, B, H, N, D, C, n_padded, pad_head, pad_tail = parsed
+    M = n_padded // score_block_size
+    if topk < 0:
+        raise ValueError("max_topk must be >= 0")
+    if M > 4096:
+        raise NotImplementedError(f"M={M} exceeds block sort limit 4096")
+    m_out = min(topk, M) if topk > 0 else M
+    qq, kk, qs, ks, Dp = _prepare_qk(q, k, input_4d, H, D)
+    dev = q.device
+    idx = torch.empty(B, H, N, m_out, device=dev, dtype=torch.int32)
+    raw = torch.empty(B, H, N, m_out, device=dev, dtype=torch.float32)
+    avg = torch.empty(B, H, N, m_out, device=dev, dtype=torch.float32)
+    L = _lib.lib()
+    ws = _lib.workspace(L.fta_topk_score_workspace_size(B, H, N, M), dev)
+    rc = L.fta_topk_score(
+        _lib.ptr(qq), _lib.ptr(kk), _lib.dtype_code(qq.dtype), B, H, N, Dp, _lib.i64arr(qs), _lib.i64arr(ks),
+        score_block_size, pad_head, pad_tail, float(D ** -0.5), topk, float(threshold),
+        _lib.ptr(idx), _lib.ptr(raw), _lib.ptr(avg), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev),
+    )
+    _lib.check(rc, "flash_topk_score")
+    return idx, raw, avg
+
+
+def build_qblock_topk_indices(
+    topk_indices: torch.Tensor,
+    q_block_size: int,
+    q_padding: Tuple[int, int] = (0, 0),
+    topk_scores: Optional[torch.Tensor] = None,
+    qblock_topk: Optional[int] = None,
+) -> Tuple[torch.Tensor, torch.Tensor, int]:
+    """Per-q-block merged indices (reference: flash_topk_attn_v2/__init__.py:57-133).
+
+    Returns ``(merged_indices [B, H, QM, W] int32, counts [B, H, QM] int32, W)``.
+    """
+    if topk_indices.ndim != 4:
+        raise ValueError("topk_indices must be [B, H, N, K]")
+
+    _, _, sequence_length, topk_width = topk_indices.shape
+    q_pad_head, q_pad_tail = q_padding
+    device = topk_indices.device
+
+    if q_pad_head < 0 or q_pad_tail < 0:
+        raise ValueError("q_padding must be non-negative")
+    if q_pad_head >= q_block_size:
+        raise ValueError(f"q_pad_head={q_pad_head} must be < q_block_size={q_block_size}")
+    if q_pad_tail >= q_block_size:
+        raise ValueError(f"q_pad_tail={q_pad_tail} must be < q_block_size={q_block_size}")
+
+    padded_sequence_length = q_pad_head + sequence_length + q_pad_tail
+    if padded_sequence_length % q_block_size != 0:
+        raise ValueError(
+            f"q_pad_head + N + q_pad_tail = {padded_sequence_length} must be divisible "
+            f"by q_block_size ({q_block_size})"
+        )
+
+    indices_int = topk_indices.to(torch.int32).contiguous()
+    if q_pad_head > 0 or q_pad_tail > 0:
+        indices_int = F.pad(indices_int, (0, 0, q_pad_head, q_pad_tail), value=-1)
+
+    if qblock_topk is None:
+        qblock_topk = q_block_size * topk_width
+
+    # num_score_blocks = max id + 1 (host sync, as in the reference :101-105)
+    mx = int(indices_int.max().item()) if indices_int.numel() > 0 else -1
+    num_score_blocks = mx + 1 if mx >= 0 else 1
+
+    if topk_scores is not None:
+        scores_float = topk_scores.float().contiguous()
+        if q_pad_head > 0 or q_pad_tail > 0:
+            scores_float = F.pad(scores_float, (0, 0, q_pad_head, q_pad_tail), value=0.0)
+    else:
+        scores_float = (indices_int >= 0).to(torch.float32)
+
+    B, H = indices_int.shape[:2]
+    QM = padded_sequence_length // q_block_size
+    counts = torch.empty(B, H, QM, device=device, dtype=torch.int32)
+    merged_indices, _merged_scores = flash_qblock_merge(
+        indices_int,
+        scores_float,
+        q_block_size=q_block_size,
+        qblock_topk=qblock_topk,
+        num_score_blocks=num_score_blocks,
+        counts_out=counts,
+    )
+    max_merged_width = merged_indices.shape[-1]
+    return merged_indices, counts, max_merged_width
+
+
+def flash_topk_attn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    merged_indices: torch.Tensor,
+    counts: torch.Tensor,
+    num_heads: int,
+    q_block_size: int,
+    kv_block_size: int,
+    scale: Optional[float] = None,
+    num_kv_heads: Optional[int] = None,
+    kv_padding: Tuple[int, int] = (0, 0),
+    q_padding: Tuple[int, int] = (0, 0),
+    S_MAX: Optional[int] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Sparse attention over merged KV block indices
+    (reference: flash_topk_attn_v2/__init__.py:136-169).  ``counts`` and
+    ``S_MAX`` are accepted and ignored, as in the reference."""
+    del counts, S_MAX
+    if num_kv_heads is not None and num_kv_heads != num_heads:
+        raise NotImplementedError("GQA (num_kv_heads != num_heads) is not supported")
+
+    return flash_sparse_attn(
+        q,
+        k,
+        v,
+        merged_indices,
+        num_heads=num_heads,
+        q_block_size=q_block_size,
+        kv_block_size=kv_block_size,
+        scale=scale,
+        q_padding=q_padding,
+        kv_padding=kv_padding,
+    )
+
+
+__all__ = [
+    "flash_topk_score",
+    "build_qblock_topk_indices",
+    "flash_topk_attn",
+    "flash_block_score",
+    "flash_topk_select",
+    "flash_qblock_merge",
+    "flash_sparse_attn",
+    "FlashSparseAttnFunc",
+    "preprocess_delta",
+    "flash_build_reverse_indices",
+    "flash_sort_by_count",
+]

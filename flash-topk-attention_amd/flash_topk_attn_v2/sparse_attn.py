@@ -1,0 +1,179 @@
+"""Block-sparse attention over merged KV-block indices (HIP, gfx950).
+
+Mirrors flash_topk_attn_v2/sparse_attn.py (reference): ``flash_sparse_attn``
+(:227-392) with the same signature, validation and outputs, and the autograd
+function ``FlashSparseAttnFunc`` (:130-224).  The kernels handle any N, head
+dim up to 256 (multiple of 16) and virtual padding directly, so the reference's
+physical N / D padding copies are not needed.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from .sparse_attn_bwd import preprocess_delta, sparse_attn_bwd
+
+
+def _sparse_attn_fwd(q, k, v, merged, H, g, kvb, scale, q_padding, kv_padding):
+    B, N, C = q.shape
+    D = C // H
+    dev = q.device
+    qq, qs = _lib.token_view(q, "bnc", H)
+    kk, ks = _lib.token_view(k, "bnc", H)
+    vv, vs = _lib.token_view(v, "bnc", H)
+    o = torch.empty(B, N, C, device=dev, dtype=q.dtype)
+    lse = torch.empty(B, H, N, device=dev, dtype=torch.float32)
+    QM, W = merged.shape[2], merged.shape[3]
+    L = _lib.lib()
+    geo = (B, H, N, D, g, kvb, q_padding[0], q_padding[1], kv_padding[0], kv_padding[1])
+    ws = _lib.workspace(L.fta_sparse_attn_fwd_workspace_size(*geo), dev)
+    rc = L.fta_sparse_attn_fwd(
+        _lib.ptr(qq), _lib.i64arr(qs), _lib.ptr(kk), _lib.i64arr(ks), _lib.ptr(vv), _lib.i64arr(vs),
+        _lib.dtype_code(q.dtype), B, H, N, D, _lib.ptr(merged), QM, W, g, kvb,
+        q_padding[0], q_padding[1], kv_padding[0], kv_padding[1], float(scale),
+        _lib.ptr(o), _lib.i64arr([N * C, D, C]), _lib.ptr(lse), _lib.ptr(ws), ws.numel(),
+        _lib.stream_ptr(dev),
+    )
+    _lib.check(rc, "flash_sparse_attn")
+    return o, lse
+
+
+class FlashSparseAttnFunc(torch.autograd.Function):
+    """Autograd function: HIP forward, HIP dQ / dK / dV backward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, merged_indices, num_heads, q_block_size, kv_block_size,
+                softmax_scale, q_padding, kv_padding):
+        o, lse = _sparse_attn_fwd(q, k, v, merged_indices, num_heads, q_block_size, kv_block_size,
+                                  softmax_scale, q_padding, kv_padding)
+        ctx.save_for_backward(q, k, v, o, merged_indices, lse)
+        ctx.num_heads = num_heads
+        ctx.q_block_size = q_block_size
+        ctx.kv_block_size = kv_block_size
+        ctx.softmax_scale = softmax_scale
+        ctx.q_padding = q_padding
+        ctx.kv_padding = kv_padding
+        ctx.mark_non_differentiable(lse)
+        return o, lse
+
+    @staticmethod
+    def backward(ctx, grad_output, _grad_lse):
+        q, k, v, o, merged, lse = ctx.saved_tensors
+        delta = preprocess_delta(o, grad_output, ctx.num_heads)
+        dq, dk, dv = sparse_attn_bwd(
+            q, k, v, o, grad_output, lse, merged, ctx.num_heads, ctx.q_block_size, ctx.kv_block_size,
+            ctx.softmax_scale, ctx.q_padding, ctx.kv_padding, delta=delta,
+        )
+        return dq, dk, dv, None, None, None, None, None, None, None
+
+
+def flash_sparse_attn(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    merged_indices: torch.Tensor,
+    num_heads: int,
+    q_block_size: int,
+    kv_block_size: int,
+    scale: Optional[float] = None,
+    q_padding: Tuple[int, int] = (0, 0),
+    kv_padding: Tuple[int, int] = (0, 0),
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Block-sparse attention forward (differentiable in q, k, v).
+
+    Args:
+        q, k, v: ``[B, N, C]``, ``C = num_heads * D`` (float16, bfloat16, float32).
+        merged_indices: ``[B, H, QM, qblock_topk]`` int32, ``-1`` padding,
+            ``QM = (q_pad_head + N + q_pad_tail) // q_block_size``.
+        num_heads: Number of attention heads.
+        q_block_size: Query block size (1 to 64).
+        kv_block_size: KV block size (any positive integer).
+        scale: Softmax scale, default ``1 / sqrt(D)``.
+        q_padding, kv_padding: virtual ``(pad_head, pad_tail)``.
+
+    Returns:
+        ``(output [B, N, C] same dtype as q, lse [B, H, N] float32 natural log)``.
+    """
+    if q.ndim != 3:
+        raise ValueError("q must be [B, N, C]")
+    if q.device.type != "cuda":
+        raise ValueError("flash_sparse_attn requires CUDA tensors")
+    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError("q must be float16, bfloat16, or float32")
+
+    orig_dtype = q.dtype
+    if orig_dtype == torch.float32:
+        q = q.bfloat16()
+        k = k.bfloat16()
+        v = v.bfloat16()
+
+    B, N, C = q.shape
+    H = num_heads
+    D = C // H
+
+    if C != H * D:
+        raise ValueError(f"C ({C}) must be divisible by num_heads ({H})")
+    if q_block_size <= 0 or q_block_size > 64:
+        raise ValueError(f"q_block_size must be in (0, 64], got {q_block_size}")
+    if kv_block_size <= 0:
+        raise ValueError(f"kv_block_size must be positive, got {kv_block_size}")
+    if merged_indices.ndim != 4:
+        raise ValueError("merged_indices must be [B, H, QM, qblock_topk]")
+    if merged_indices.dtype != torch.int32:
+        raise ValueError("merged_indices must be int32")
+
+    q_pad_head, q_pad_tail = q_padding
+    kv_pad_head, kv_pad_tail = kv_padding
+    if q_pad_head < 0 or q_pad_tail < 0:
+        raise ValueError("q_padding values must be non-negative")
+    if kv_pad_head < 0 or kv_pad_tail < 0:
+        raise ValueError("kv_padding values must be non-negative")
+    if q_pad_head >= q_block_size:
+        raise ValueError(f"q_pad_head={q_pad_head} must be < q_block_size={q_block_size}")
+    if q_pad_tail >= q_block_size:
+        raise ValueError(f"q_pad_tail={q_pad_tail} must be < q_block_size={q_block_size}")
+    if kv_pad_head >= kv_block_size:
+        raise ValueError(f"kv_pad_head={kv_pad_head} must be < kv_block_size={kv_block_size}")
+    if kv_pad_tail >= kv_block_size:
+        raise ValueError(f"kv_pad_tail={kv_pad_tail} must be < kv_block_size={kv_block_size}")
+
+    n_q_padded = q_pad_head + N + q_pad_tail
+    n_kv_padded = kv_pad_head + N + kv_pad_tail
+    if n_q_padded % q_block_size != 0:
+        raise ValueError(
+            f"q_pad_head + N + q_pad_tail = {n_q_padded} must be divisible "
+            f"by q_block_size={q_block_size}"
+        )
+    if n_kv_padded % kv_block_size != 0:
+        raise ValueError(
+            f"kv_pad_head + N + kv_pad_tail = {n_kv_padded} must be "
+            f"divisible by kv_block_size={kv_block_size}"
+        )
+    QM = n_q_padded // q_block_size
+    if merged_indices.shape[2] != QM:
+        raise ValueError(
+            f"merged_indices dim 2 ({merged_indices.shape[2]}) must match "
+            f"QM = (q_pad_head + N + q_pad_tail) // q_block_size = {QM}"
+        )
+    if D <= 0 or D % 16 != 0:
+        raise ValueError(f"D ({D}) must be a positive multiple of 16")
+    if D > 256:
+        raise ValueError(f"D ({D}) must be <= 256")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+
+    merged = merged_indices.contiguous()
+    output, lse = FlashSparseAttnFunc.apply(
+        q, k, v, merged, H, q_block_size, kv_block_size, float(scale),
+        (q_pad_head, q_pad_tail), (kv_pad_head, kv_pad_tail),
+    )
+    if orig_dtype == torch.float32:
+        output = output.float()
+    return output, lse
+
+
+__all__ = ["flash_sparse_attn", "FlashSparseAttnFunc"]

@@ -1,0 +1,200 @@
+/*
+ * fta.h -- C ABI of libfta_gfx950.so, the MI355X (gfx950) implementation of the
+ * flash-topk-attention V2 hot path:
+ *     block score -> top-k select -> q-block merge -> sparse attention fwd/bwd.
+ *
+ * Conventions
+ *  - Every function returns an int status: FTA_OK (0), FTA_ERR_ARG (1, bad
+ *    argument), FTA_ERR_UNSUPPORTED (2, outside the supported envelope) or
+ *    FTA_ERR_HIP (3, launch error).  fta_last_error() returns the message of
+ *    the last failure on the calling thread.  No C++ exception crosses the ABI.
+ *  - All pointers are device pointers owned by the caller.  Functions that need
+ *    scratch take (workspace, workspace_bytes); the matching *_workspace_size()
+ *    returns the required size (0 for invalid geometry).
+ *  - Work is enqueued on `stream` (a hipStream_t) and is asynchronous.
+ *  - dtype: FTA_DTYPE_BF16 (0) or FTA_DTYPE_F16 (1); 16-bit tensors are passed
+ *    as raw pointers.  Token tensors are addressed as [B][N][H][D] with element
+ *    strides {stride_b, stride_h, stride_n} and unit stride along D; D-rows must
+ *    be 16-byte aligned (strides and base pointer multiples of 8 elements).
+ *    This covers both the reference's [B, N, H*D] and [B, H, N, D] layouts.
+ *  - Index conventions follow the reference: -1 marks an empty slot; merged
+ *    lists are [B][H][QM][W]; per-row outputs are [B][H][N].
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *  each entry point below names the pybind launcher (flash_topk_attn_v2/csrc/
+ *  *.cpp) and Python wrapper it stands in for.
+ */
+#ifndef FTA_H_
+#define FTA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FTA_OK 0
+#define FTA_ERR_ARG 1
+#define FTA_ERR_UNSUPPORTED 2
+#define FTA_ERR_HIP 3
+
+#define FTA_DTYPE_BF16 0
+#define FTA_DTYPE_F16 1
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* fta_last_error(void);
+/* ABI version (1). */
+int fta_version(void);
+
+/* ---------------------------------------------------------------- scoring */
+
+/* Workspace for fta_block_score: per-block log2-sum-exp [B*H][M][N] f32 plus
+ * row totals [B*H][N] f32. */
+size_t fta_block_score_workspace_size(int B, int H, int N, int M);
+
+/*
+ * Dense per-query block mass: scores[b][h][n][m] = sum over keys of block m of
+ * softmax(q k^T * scale) (fp32, rows sum to 1), M = (pad_head+N+pad_tail)/b.
+ * Replaces block_score_launch (flash_topk_attn_v2/csrc/block_score.cpp:3-15,
+ * csrc/block_score_kernel.cu:414-438) behind flash_block_score_cuda
+ * (flash_topk_attn_v2/block_score_cuda.py:45-161) and the Triton path of
+ * flash_block_score (flash_topk_attn_v2/block_score.py:417-451).
+ * q_strides/k_strides: {stride_b, stride_h, stride_n} in elements.
+ */
+int fta_block_score(const void* q, const void* k, int dtype, int B, int H, int N, int D,
+                    const int64_t* q_strides, const int64_t* k_strides, int score_block_size,
+                    int pad_head, int pad_tail, float scale, float* scores, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/*
+ * Top-k block selection with threshold truncation over `rows` rows of M fp32
+ * scores (element (r, m) at block_scores[r*stride_row + m*stride_m]).
+ * Outputs [rows][M_OUT], M_OUT = min(max_topk, M) (M if max_topk == 0):
+ * indices (-1 past the cut), raw = avg*valid_count (0 past the cut), avg.
+ * Ties go to the lower block index; the cumulative sum is sequential fp32.
+ * Replaces topk_select_launch (flash_topk_attn_v2/csrc/topk_select.cpp:3-15,
+ * csrc/topk_select_kernel.cu:142-177) behind flash_topk_select
+ * (flash_topk_attn_v2/topk_select.py:185-311, topk_select_cuda.py:27-114).
+ */
+int fta_topk_select(const float* block_scores, int64_t rows, int M, int64_t stride_row,
+                    int64_t stride_m, int max_topk, int score_block_size, int pad_head, int pad_tail,
+                    float threshold, int32_t* topk_indices, float* topk_raw, float* topk_avg,
+                    void* stream);
+
+size_t fta_topk_score_workspace_size(int B, int H, int N, int M);
+
+/*
+ * Fused scoring + selection: the result of fta_block_score followed by
+ * fta_topk_select without materialising the [B][H][N][M] score tensor.
+ * Replaces the composition in flash_topk_score (flash_topk_attn_v2/__init__.py:16-54).
+ * Outputs are [B][H][N][M_OUT].
+ */
+int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N, int D,
+                   const int64_t* q_strides, const int64_t* k_strides, int score_block_size,
+                   int pad_head, int pad_tail, float scale, int max_topk, float threshold,
+                   int32_t* topk_indices, float* topk_raw, float* topk_avg, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- indices */
+
+/*
+ * Per-(b, h, q-block) merge of g*K (index, score) pairs: sequential fp32
+ * scatter-add in (row, slot) order, positive entries sorted by (score desc,
+ * index asc), first qblock_topk kept, -1 / 0 padding; counts[slice] = #kept
+ * (counts may be NULL, merged_scores may be NULL).
+ * Replaces qblock_merge_launch (flash_topk_attn_v2/csrc/qblock_merge.cpp:3-14,
+ * csrc/qblock_merge_kernel.cu:100-131) behind flash_qblock_merge
+ * (flash_topk_attn_v2/qblock_merge.py:85-155).
+ */
+int fta_qblock_merge(const int32_t* topk_indices, const float* topk_scores, int64_t num_slices,
+                     int q_block_size, int k_per_query, int num_score_blocks, int qblock_topk,
+                     int32_t* merged_indices, float* merged_scores, int32_t* counts, void* stream);
+
+size_t fta_build_reverse_indices_workspace_size(int B, int H, int QM, int M);
+
+/*
+ * Reverse index: reverse_indices[b][h][m][:] = ascending q-block ids whose
+ * merged list holds m (-1 padded to QM), reverse_counts[b][h][m], and
+ * sorted_kv_indices[b][h][:] = stable descending argsort of the counts
+ * (may be NULL).  Replaces build_reverse_indices_launch
+ * (flash_topk_attn_v2/csrc/build_reverse_indices.cpp:3-14,
+ * csrc/build_reverse_indices_kernel.cu:71-104) behind
+ * flash_build_reverse_indices_cuda (flash_topk_attn_v2/build_reverse_indices_cuda.py:32-78).
+ */
+int fta_build_reverse_indices(const int32_t* merged_indices, const int32_t* counts, int B, int H,
+                              int QM, int W, int M, int32_t* reverse_indices,
+                              int32_t* reverse_counts, int32_t* sorted_kv_indices, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/*
+ * Stable descending sort of `total` int32 counts: sorted_counts and the
+ * original positions sorted_ids.  Replaces sort_by_count_launch
+ * (flash_topk_attn_v2/csrc/sort_by_count.cpp:3-13, csrc/sort_by_count_kernel.cu:6-51)
+ * behind flash_sort_by_count_cuda (flash_topk_attn_v2/sort_by_count_cuda.py:33-67).
+ */
+int fta_sort_by_count(const int32_t* reverse_counts, int64_t total, int32_t* sorted_counts,
+                      int32_t* sorted_ids, void* stream);
+
+/* ---------------------------------------------------------------- attention */
+
+size_t fta_sparse_attn_fwd_workspace_size(int B, int H, int N, int D, int q_block_size,
+                                          int kv_block_size, int q_pad_head, int q_pad_tail,
+                                          int kv_pad_head, int kv_pad_tail);
+
+/*
+ * Block-sparse attention forward over the merged KV-block lists
+ * (merged_indices [B][H][QM][W], -1 entries ignored, order irrelevant):
+ * o [B][N][H][D] (strided, same dtype) and lse [B][H][N] (natural log,
+ * -inf and o = 0 for rows without candidate tokens).
+ * Replaces sparse_attn_fwd_launch (flash_topk_attn_v2/csrc/sparse_attn.cpp:3-16,
+ * csrc/sparse_attn_kernel.cu:368-457) behind flash_sparse_attn_cuda
+ * (flash_topk_attn_v2/sparse_attn_cuda.py:42-110); lse = softmax_max + softmax_lse
+ * of the reference (flash_topk_attn_v2/sparse_attn.py:391).
+ */
+int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k,
+                        const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                        int dtype, int B, int H, int N, int D, const int32_t* merged_indices,
+                        int QM, int W, int q_block_size, int kv_block_size, int q_pad_head,
+                        int q_pad_tail, int kv_pad_head, int kv_pad_tail, float scale, void* o,
+                        const int64_t* o_strides, float* lse, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/*
+ * delta[b][h][n] = sum_d o * dout (fp32).  Replaces preprocess_delta
+ * (flash_topk_attn_v2/sparse_attn_bwd.py:12-33).
+ */
+int fta_preprocess_delta(const void* o, const int64_t* o_strides, const void* dout,
+                         const int64_t* do_strides, int dtype, int B, int H, int N, int D,
+                         float* delta, void* stream);
+
+size_t fta_sparse_attn_bwd_workspace_size(int B, int H, int N, int D, int q_block_size,
+                                          int kv_block_size, int q_pad_head, int q_pad_tail,
+                                          int kv_pad_head, int kv_pad_tail);
+
+/*
+ * Backward: dq, dk, dv ([B][N][H][D] strided, same dtype as q) from the
+ * forward's lse and delta.  dQ walks the merged lists; dK/dV walk the
+ * transposed membership (built internally in the workspace) without atomics.
+ * Replaces sparse_attn_bwd_dq_launch and sparse_attn_bwd_dkv_launch
+ * (flash_topk_attn_v2/csrc/sparse_attn_bwd_dq.cpp:3-19, sparse_attn_bwd_dkv.cpp:3-20)
+ * behind flash_sparse_attn_bwd_dq_cuda / flash_sparse_attn_bwd_dkv_cuda
+ * (flash_topk_attn_v2/sparse_attn_bwd_dq_cuda.py:44-108,
+ * sparse_attn_bwd_dkv_cuda.py:44-118) as called from
+ * FlashSparseAttnFunc.backward (flash_topk_attn_v2/sparse_attn.py:163-224).
+ */
+int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k,
+                        const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                        const void* dout, const int64_t* do_strides, int dtype, int B, int H, int N,
+                        int D, const int32_t* merged_indices, int QM, int W, int q_block_size,
+                        int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head,
+                        int kv_pad_tail, float scale, const float* lse, const float* delta, void* dq,
+                        const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                        const int64_t* dv_strides, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FTA_H_ */

@@ -1,0 +1,419 @@
+"""CPU oracle for the flash-topk-attention V2 hot path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product package imports this
+module; only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
+``cpu_baseline`` leg may use it, and only as the checker / CPU baseline.
+
+This is a numpy restatement of the reference's naive semantics (paths are
+relative to the reference repository root, ``v2/`` = ``flash_topk_attn_v2/``):
+
+* ``block_score``          v2/block_score.py:295-366
+* ``topk_select``          v2/topk_select.py:128-182, cut and valid-count rules
+                           of v2/topk_select.py:66-123 and
+                           v2/csrc/topk_select_kernel.cu:50-110
+* ``qblock_merge``         v2/qblock_merge.py:27-82, pad/<=0 rules of
+                           v2/csrc/qblock_merge_kernel.cu:36-89
+* ``build_qblock_topk_indices``  v2/__init__.py:57-133
+* ``sparse_attn``          v2/sparse_attn.py:24-127 (empty q-block semantics of
+                           v2/csrc/sparse_attn_kernel.cu:39-54)
+* ``preprocess_delta``     v2/sparse_attn_bwd.py:12-33
+* ``build_reverse_indices`` v2/sparse_attn_bwd.py:36-76 (+ the argsort of
+                           v2/csrc/build_reverse_indices_kernel.cu:29-62)
+* ``sort_by_count``        v2/sparse_attn_bwd.py:79-108
+* ``sparse_attn_bwd``      v2/sparse_attn_bwd.py:111-294
+
+Orders that the reference leaves implementation-defined are fixed here, and
+the HIP kernels follow the same rules:
+
+* top-k ties: descending average score, ties broken by the LOWER block index
+  (CUB BlockRadixSort is stable, v2/csrc/topk_select_kernel.cu:62);
+* top-k cumulative sum: sequential fp32 sum in sorted order of
+  ``raw' = avg * valid_count`` (both reference kernels re-derive raw from avg:
+  v2/topk_select.py:101, v2/csrc/topk_select_kernel.cu:80);
+* merge sums: sequential fp32 sum in (query row, slot) order (the reference
+  uses shared-memory float atomics, whose order is undefined);
+* merge ties: descending merged score, ties broken by the lower block index;
+* reverse lists: q-block ids in ascending order (the reference's atomic slot
+  order is undefined).
+
+Floating-point attention maths (block scores, o, lse, gradients) is computed
+in float64 from the caller's (already bf16/fp16-rounded) inputs.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Iterable, Optional, Sequence, Tuple
+
+import numpy as np
+
+# --------------------------------------------------------------------------
+# helpers
+# --------------------------------------------------------------------------
+
+
+def _to_bhnd(x: np.ndarray, num_heads: int) -> np.ndarray:
+    """[B, N, C] -> [B, H, N, D] (float64 view/copy)."""
+    B, N, C = x.shape
+    D = C // num_heads
+    return x.reshape(B, N, num_heads, D).transpose(0, 2, 1, 3).astype(np.float64)
+
+
+def _from_bhnd(x: np.ndarray) -> np.ndarray:
+    B, H, N, D = x.shape
+    return x.transpose(0, 2, 1, 3).reshape(B, N, H * D)
+
+
+def _logsumexp(s: np.ndarray, axis: int = -1) -> np.ndarray:
+    m = np.max(s, axis=axis, keepdims=True)
+    m_safe = np.where(np.isfinite(m), m, 0.0)
+    with np.errstate(divide="ignore"):
+        out = np.log(np.sum(np.exp(s - m_safe), axis=axis, keepdims=True)) + m_safe
+    return np.squeeze(out, axis=axis)
+
+
+# --------------------------------------------------------------------------
+# scoring: v2/block_score.py:295-366
+# --------------------------------------------------------------------------
+
+
+def block_score(
+    q: np.ndarray,
+    k: np.ndarray,
+    num_heads: Optional[int],
+    score_block_size: int,
+    padding: Tuple[int, int] = (0, 0),
+    rows: Optional[np.ndarray] = None,
+    chunk: int = 1024,
+) -> np.ndarray:
+    """Per-query softmax mass per virtual score block (float64).
+
+    Follows v2/block_score.py:295-366: softmax over all N keys with scale
+    D**-0.5, then sums over keys ``[max(0, m*b - pad_head), min(N, (m+1)*b - pad_head))``.
+
+    ``q``/``k`` are ``[B, N, C]`` (needs ``num_heads``) or ``[B, H, N, D]``.
+    ``rows`` optionally restricts the computation to those query indices
+    (the maths is row-independent); the result is then ``[B, H, len(rows), M]``.
+    """
+    if q.ndim == 4:
+        B, H, N, D = q.shape
+        q4 = q.astype(np.float64)
+        k4 = k.astype(np.float64)
+    else:
+        B, N, C = q.shape
+        H = num_heads
+        D = C // H
+        q4 = _to_bhnd(q, H)
+        k4 = _to_bhnd(k, H)
+    pad_head, pad_tail = padding
+    n_padded = pad_head + N + pad_tail
+    assert n_padded % score_block_size == 0
+    M = n_padded // score_block_size
+    scale = D ** -0.5
+    if rows is None:
+        rows = np.arange(N)
+    rows = np.asarray(rows)
+    out = np.zeros((B, H, len(rows), M), dtype=np.float64)
+    for b in range(B):
+        for h in range(H):
+            kk = k4[b, h]
+            for c0 in range(0, len(rows), chunk):
+                r = rows[c0 : c0 + chunk]
+                s = (q4[b, h, r] * scale) @ kk.T
+                s = s - s.max(axis=-1, keepdims=True)
+                p = np.exp(s)
+                p /= p.sum(axis=-1, keepdims=True)
+                # keys live at padded coordinates p = t + pad_head; padded slots hold 0
+                p_pad = np.zeros((len(r), n_padded), dtype=np.float64)
+                p_pad[:, pad_head : pad_head + N] = p
+                out[b, h, c0 : c0 + chunk] = p_pad.reshape(len(r), M, score_block_size).sum(-1)
+    return out
+
+
+def valid_counts(M: int, score_block_size: int, padding: Tuple[int, int]) -> np.ndarray:
+    """Valid tokens per score block (v2/topk_select.py:152-156)."""
+    pad_head, pad_tail = padding
+    vc = np.full((M,), float(score_block_size), dtype=np.float32)
+    if pad_head > 0:
+        vc[0] = float(score_block_size - pad_head)
+    if pad_tail > 0:
+        vc[-1] = float(score_block_size - pad_tail)
+    return vc
+
+
+# --------------------------------------------------------------------------
+# top-k select: v2/topk_select.py:128-182 (+ kernel rules)
+# --------------------------------------------------------------------------
+
+
+def topk_select(
+    block_scores: np.ndarray,
+    threshold: float,
+    max_topk: int,
+    score_block_size: int,
+    padding: Tuple[int, int] = (0, 0),
+) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Sort by avg = raw / valid_count (desc, ties -> lower index), cumulative
+    fp32 sum of raw' = avg * valid_count in sorted order, keep through the first
+    position whose cumsum >= threshold (else all), cap at M_OUT.
+
+    All arithmetic is fp32 so that a kernel fed the same fp32 block scores must
+    agree bit for bit.  Returns (indices int32, raw f32, avg f32), ``[..., M_OUT]``.
+    """
+    raw = np.asarray(block_scores, dtype=np.float32)
+    M = raw.shape[-1]
+    vc = valid_counts(M, score_block_size, padding)
+    avg = (raw / vc).astype(np.float32)
+    m_out = min(max_topk, M) if max_topk > 0 else M
+    order = np.argsort(-avg, axis=-1, kind="stable")[..., :m_out]
+    sorted_avg = np.take_along_axis(avg, order, axis=-1)
+    sorted_raw = (sorted_avg * vc[order]).astype(np.float32)
+    cs = np.cumsum(sorted_raw, axis=-1, dtype=np.float32)
+    exceed = cs >= np.float32(threshold)
+    has = exceed.any(axis=-1)
+    first = np.argmax(exceed, axis=-1)
+    cut = np.where(has, first + 1, m_out)
+    keep = np.arange(m_out) < cut[..., None]
+    idx = np.where(keep, order, -1).astype(np.int32)
+    raw_o = np.where(keep, sorted_raw, np.float32(0)).astype(np.float32)
+    avg_o = np.where(keep, sorted_avg, np.float32(0)).astype(np.float32)
+    return idx, raw_o, avg_o
+
+
+# --------------------------------------------------------------------------
+# q-block merge: v2/qblock_merge.py:27-82, v2/__init__.py:57-133
+# --------------------------------------------------------------------------
+
+
+def qblock_merge(
+    topk_indices: np.ndarray,
+    topk_scores: np.ndarray,
+    q_block_size: int,
+    qblock_topk: int,
+    num_score_blocks: int,
+) -> Tuple[np.ndarray, np.ndarray]:
+    """Scatter-add (sequential fp32, (row, slot) order), keep positive entries
+    sorted by score desc (ties -> lower id), truncate to ``qblock_topk``."""
+    B, H, N, K = topk_indices.shape
+    assert N % q_block_size == 0
+    QM = N // q_block_size
+    S = B * H * QM
+    idx = topk_indices.reshape(S, q_block_size * K).astype(np.int64)
+    scr = np.asarray(topk_scores, dtype=np.float32).reshape(S, q_block_size * K)
+    Mt = num_score_blocks
+    valid = (idx >= 0) & (idx < Mt)
+    acc = np.zeros((S, Mt), dtype=np.float32)
+    sl = np.broadcast_to(np.arange(S)[:, None], idx.shape)
+    flat = (sl * Mt + np.where(valid, idx, 0))[valid]
+    np.add.at(acc.reshape(-1), flat, scr[valid])  # sequential, in (row, slot) order
+    order = np.argsort(-acc, axis=-1, kind="stable")
+    vals = np.take_along_axis(acc, order, axis=-1)
+    W = qblock_topk
+    out_idx = np.full((S, W), -1, dtype=np.int32)
+    out_scr = np.zeros((S, W), dtype=np.float32)
+    w = min(W, Mt)
+    pos = vals[:, :w] > 0
+    out_idx[:, :w] = np.where(pos, order[:, :w], -1)
+    out_scr[:, :w] = np.where(pos, vals[:, :w], 0)
+    return out_idx.reshape(B, H, QM, W), out_scr.reshape(B, H, QM, W)
+
+
+def build_qblock_topk_indices(
+    topk_indices: np.ndarray,
+    q_block_size: int,
+    q_padding: Tuple[int, int] = (0, 0),
+    topk_scores: Optional[np.ndarray] = None,
+    qblock_topk: Optional[int] = None,
+) -> Tuple[np.ndarray, np.ndarray, int]:
+    """v2/__init__.py:57-133: q padding with -1 / 0, default W = g*K, ones
+    scores for valid ids, num_score_blocks = max id + 1, counts = #valid."""
+    B, H, N, K = topk_indices.shape
+    ph, pt = q_padding
+    idx = np.asarray(topk_indices).astype(np.int32)
+    idx = np.pad(idx, ((0, 0), (0, 0), (ph, pt), (0, 0)), constant_values=-1)
+    if qblock_topk is None:
+        qblock_topk = q_block_size * K
+    valid = idx >= 0
+    nsb = int(idx[valid].max()) + 1 if valid.any() else 1
+    if topk_scores is not None:
+        scr = np.pad(np.asarray(topk_scores, dtype=np.float32),
+                     ((0, 0), (0, 0), (ph, pt), (0, 0)), constant_values=0.0)
+    else:
+        scr = valid.astype(np.float32)
+    merged, _ = qblock_merge(idx, scr, q_block_size, qblock_topk, nsb)
+    counts = (merged >= 0).sum(-1).astype(np.int32)
+    return merged, counts, merged.shape[-1]
+
+
+# --------------------------------------------------------------------------
+# sparse attention forward: v2/sparse_attn.py:24-127
+# --------------------------------------------------------------------------
+
+
+def _valid_tokens(blocks: Iterable[int], N: int, kv_block_size: int, kv_pad_head: int) -> np.ndarray:
+    valid = np.zeros(N, dtype=bool)
+    for bid in blocks:
+        s = int(bid) * kv_block_size - kv_pad_head
+        e = s + kv_block_size
+        s, e = max(0, s), min(N, e)
+        if s < e:
+            valid[s:e] = True
+    return valid
+
+
+def sparse_attn(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    merged_indices: np.ndarray,
+    num_heads: int,
+    q_block_size: int,
+    kv_block_size: int,
+    scale: Optional[float] = None,
+    q_padding: Tuple[int, int] = (0, 0),
+    kv_padding: Tuple[int, int] = (0, 0),
+    qblocks: Optional[Sequence[Tuple[int, int, int]]] = None,
+) -> Tuple[np.ndarray, np.ndarray]:
+    """o [B, N, C] float64 and natural-log lse [B, H, N] (−inf and o = 0 for
+    rows with no candidate token).  ``qblocks`` restricts the computation to the
+    listed (b, h, qm) triples; other rows are left at o = 0 / lse = NaN."""
+    B, N, C = q.shape
+    H = num_heads
+    D = C // H
+    q4, k4, v4 = _to_bhnd(q, H), _to_bhnd(k, H), _to_bhnd(v, H)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    ph = q_padding[0]
+    kph = kv_padding[0]
+    QM = merged_indices.shape[2]
+    o = np.zeros((B, H, N, D), dtype=np.float64)
+    lse = np.full((B, H, N), -np.inf if qblocks is None else np.nan, dtype=np.float64)
+    if qblocks is None:
+        qblocks = [(b, h, qm) for b in range(B) for h in range(H) for qm in range(QM)]
+    for b, h, qm in qblocks:
+        r0 = qm * q_block_size - ph
+        rs, re = max(0, r0), min(N, r0 + q_block_size)
+        if rs >= re:
+            continue
+        lse[b, h, rs:re] = -np.inf
+        ids = merged_indices[b, h, qm]
+        valid = _valid_tokens(ids[ids >= 0], N, kv_block_size, kph)
+        if not valid.any():
+            continue
+        s = (q4[b, h, rs:re] * scale) @ k4[b, h, valid].T
+        row_lse = _logsumexp(s)
+        p = np.exp(s - row_lse[:, None])
+        o[b, h, rs:re] = p @ v4[b, h, valid]
+        lse[b, h, rs:re] = row_lse
+    return _from_bhnd(o), lse
+
+
+# --------------------------------------------------------------------------
+# backward: v2/sparse_attn_bwd.py:12-294
+# --------------------------------------------------------------------------
+
+
+def preprocess_delta(o: np.ndarray, do: np.ndarray, num_heads: int) -> np.ndarray:
+    """delta[b, h, n] = sum_d O * dO (v2/sparse_attn_bwd.py:12-33)."""
+    return (_to_bhnd(o, num_heads) * _to_bhnd(do, num_heads)).sum(-1)
+
+
+def build_reverse_indices(
+    merged_indices: np.ndarray, counts: np.ndarray, num_kv_blocks: int
+) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """KV block -> ascending list of q-blocks that selected it
+    (v2/sparse_attn_bwd.py:36-76), plus the per-(b, h) stable descending
+    argsort of the reverse counts (v2/csrc/build_reverse_indices_kernel.cu:29-62)."""
+    B, H, QM, W = merged_indices.shape
+    M = num_kv_blocks
+    rev = np.full((B, H, M, QM), -1, dtype=np.int32)
+    cnt = np.zeros((B, H, M), dtype=np.int32)
+    for b in range(B):
+        for h in range(H):
+            sel = np.zeros((M, QM), dtype=bool)
+            for qm in range(QM):
+                ids = merged_indices[b, h, qm, : int(counts[b, h, qm])]
+                ids = ids[(ids >= 0) & (ids < M)]
+                sel[ids, qm] = True
+            for m in range(M):
+                qs = np.nonzero(sel[m])[0]
+                rev[b, h, m, : len(qs)] = qs
+                cnt[b, h, m] = len(qs)
+    sorted_kv = np.argsort(-cnt, axis=-1, kind="stable").astype(np.int32)
+    return rev, cnt, sorted_kv
+
+
+def sort_by_count(reverse_counts: np.ndarray, num_heads: int, num_kv_blocks: int) -> Tuple[np.ndarray, np.ndarray]:
+    """Global stable descending sort of reverse counts (v2/sparse_attn_bwd.py:79-108)."""
+    flat = np.asarray(reverse_counts).reshape(-1)
+    order = np.argsort(-flat.astype(np.int64), kind="stable")
+    return flat[order].astype(np.int32), order.astype(np.int32)
+
+
+def sparse_attn_bwd(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    do: np.ndarray,
+    merged_indices: np.ndarray,
+    num_heads: int,
+    q_block_size: int,
+    kv_block_size: int,
+    scale: Optional[float] = None,
+    q_padding: Tuple[int, int] = (0, 0),
+    kv_padding: Tuple[int, int] = (0, 0),
+    qblocks: Optional[Sequence[Tuple[int, int, int]]] = None,
+) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """dQ, dK, dV (float64, [B, N, C]) following bwd_dq_naive / bwd_dkv_naive
+    (v2/sparse_attn_bwd.py:111-294): P = softmax over the q-block's candidate
+    tokens, dP = dO V^T, delta = rowsum(dO * (P V)), dS = P (dP - delta),
+    dQ = scale dS K, dK = scale dS^T Q, dV = P^T dO.  ``qblocks`` restricts the
+    sum to the listed (b, h, qm) triples (dK/dV then hold partial sums)."""
+    B, N, C = q.shape
+    H = num_heads
+    D = C // H
+    q4, k4, v4, do4 = _to_bhnd(q, H), _to_bhnd(k, H), _to_bhnd(v, H), _to_bhnd(do, H)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    ph = q_padding[0]
+    kph = kv_padding[0]
+    QM = merged_indices.shape[2]
+    dq = np.zeros_like(q4)
+    dk = np.zeros_like(k4)
+    dv = np.zeros_like(v4)
+    if qblocks is None:
+        qblocks = [(b, h, qm) for b in range(B) for h in range(H) for qm in range(QM)]
+    for b, h, qm in qblocks:
+        r0 = qm * q_block_size - ph
+        rs, re = max(0, r0), min(N, r0 + q_block_size)
+        if rs >= re:
+            continue
+        ids = merged_indices[b, h, qm]
+        valid = _valid_tokens(ids[ids >= 0], N, kv_block_size, kph)
+        if not valid.any():
+            continue
+        qq, dd = q4[b, h, rs:re], do4[b, h, rs:re]
+        kk, vv = k4[b, h, valid], v4[b, h, valid]
+        s = (qq * scale) @ kk.T
+        p = np.exp(s - _logsumexp(s)[:, None])
+        dp = dd @ vv.T
+        delta = (dd * (p @ vv)).sum(-1, keepdims=True)
+        ds = p * (dp - delta)
+        dq[b, h, rs:re] += scale * ds @ kk
+        dk[b, h, valid] += scale * ds.T @ qq
+        dv[b, h, valid] += p.T @ dd
+    return _from_bhnd(dq), _from_bhnd(dk), _from_bhnd(dv)
+
+
+__all__ = [
+    "block_score",
+    "valid_counts",
+    "topk_select",
+    "qblock_merge",
+    "build_qblock_topk_indices",
+    "sparse_attn",
+    "preprocess_delta",
+    "build_reverse_indices",
+    "sort_by_count",
+    "sparse_attn_bwd",
+]

@@ -1,0 +1,62 @@
+"""CPU-side checks of the boundary: the C-ABI library loads and exports every
+symbol declared in include/fta.h; argument validation raises the reference's
+exception types without touching the GPU."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fta.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fta_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from flash_topk_attn_v2 import _lib
+
+    so = ctypes.CDLL(_lib.LIB_PATH)
+    names = _declared()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(so, n), n
+    assert set(names) == set(_lib._SIGNATURES)
+
+
+def test_error_path_returns_status_without_gpu():
+    from flash_topk_attn_v2 import _lib
+
+    L = _lib.lib()
+    # invalid geometry is rejected before any launch
+    rc = L.fta_topk_select(None, 1, 0, 0, 1, 16, 64, 0, 0, 1.0, None, None, None, None)
+    assert rc == _lib.FTA_ERR_ARG
+    assert b"M must be positive" in L.fta_last_error()
+    rc = L.fta_qblock_merge(None, None, 1, 32, 16, 5000, 16, None, None, None, None)
+    assert rc == _lib.FTA_ERR_UNSUPPORTED
+    assert L.fta_sparse_attn_fwd_workspace_size(1, 1, 100, 64, 32, 64, 0, 0, 0, 0) == 0  # 100 % 32 != 0
+    assert L.fta_sparse_attn_fwd_workspace_size(1, 2, 128, 64, 32, 64, 0, 0, 0, 0) > 0
+
+
+def test_api_validation_matches_reference_errors():
+    import flash_topk_attn_v2 as fta
+
+    q = torch.zeros(1, 10, 4)
+    with pytest.raises(ValueError, match="num_heads is required"):
+        fta.flash_topk_score(q, q)
+    with pytest.raises(ValueError, match="topk_indices must be"):
+        fta.build_qblock_topk_indices(torch.zeros(2, 2, dtype=torch.int32), 4)
+    with pytest.raises(ValueError, match="q_pad_head=4 must be < q_block_size=4"):
+        fta.build_qblock_topk_indices(torch.zeros(1, 1, 8, 2, dtype=torch.int32), 4, (4, 0))
+    with pytest.raises(NotImplementedError, match="GQA"):
+        fta.flash_topk_attn(q, q, q, None, None, 2, 4, 4, num_kv_heads=1)
+    with pytest.raises(ValueError, match="requires CUDA"):
+        fta.flash_sparse_attn(q, q, q, torch.zeros(1, 1, 1, 1, dtype=torch.int32), 1, 4, 4)
+    with pytest.raises(ValueError, match="requires CUDA"):
+        fta.flash_block_score(q, q, 1, 5)

@@ -1,0 +1,236 @@
+"""GPU parity: HIP kernels (through the C ABI via the Python API) vs the CPU oracle.
+
+Tolerances (from the task's north star): top-k indices identical except where
+the oracle's average scores of the swapped blocks differ by < 1e-6; merged
+indices / counts / reverse lists bit-exact given identical inputs; o, dQ, dK,
+dV within atol 2e-3 + rtol 1e-2 (fp16/bf16 outputs), lse rtol 1e-4.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import fta_oracle as O
+from _helpers import check_topk_gap, np32, rand, say
+
+pytestmark = pytest.mark.gpu
+
+fta = pytest.importorskip("flash_topk_attn_v2")
+
+SCORE_CASES = [
+    # B, N, H, D, b, padding, dtype, layout
+    (1, 1024, 2, 64, 64, (0, 0), torch.float16, "bnc"),
+    (1, 1000, 2, 128, 64, (24, 0), torch.bfloat16, "bnc"),
+    (2, 640, 3, 128, 32, (0, 0), torch.bfloat16, "bhnd"),
+    (1, 300, 2, 64, 48, (12, 0), torch.float16, "bnc"),
+    (1, 520, 1, 96, 128, (0, 120), torch.bfloat16, "bnc"),
+    (1, 256, 2, 40, 64, (0, 0), torch.float32, "bnc"),
+    (1, 200, 2, 256, 64, (30, 26), torch.bfloat16, "bnc"),
+]
+
+
+def _qk(case, seed):
+    B, N, H, D, b, pad, dt, layout = case
+    shape = (B, H, N, D) if layout == "bhnd" else (B, N, H * D)
+    q = rand(shape, seed, dt, "cuda")
+    k = rand(shape, seed + 1, dt, "cuda")
+    return q, k
+
+
+def _oracle_inputs(q, k):
+    # the kernels compute in bf16 for fp32 inputs (as the reference)
+    if q.dtype == torch.float32:
+        q, k = q.bfloat16(), k.bfloat16()
+    return np32(q), np32(k)
+
+
+@pytest.mark.parametrize("case", SCORE_CASES, ids=lambda c: f"B{c[0]}N{c[1]}H{c[2]}D{c[3]}b{c[4]}p{c[5]}")
+def test_block_score_vs_oracle(case):
+    B, N, H, D, b, pad, dt, layout = case
+    say(f"[block_score] {case}")
+    q, k = _qk(case, 10)
+    got = fta.flash_block_score(q, k, H, b, pad)
+    torch.cuda.synchronize()
+    qn, kn = _oracle_inputs(q, k)
+    ref = O.block_score(qn, kn, H, b, pad)
+    g = got.cpu().numpy()
+    assert g.shape == ref.shape
+    np.testing.assert_allclose(g, ref, rtol=2e-4, atol=2e-7)
+    np.testing.assert_allclose(g.sum(-1), 1.0, rtol=1e-5)
+
+
+@pytest.mark.parametrize("case", SCORE_CASES[:5], ids=lambda c: f"N{c[1]}D{c[3]}b{c[4]}p{c[5]}")
+@pytest.mark.parametrize("thr,topk", [(1.0, 16), (0.9, 8), (0.5, 0)])
+def test_topk_select_bit_exact_and_fused(case, thr, topk):
+    B, N, H, D, b, pad, dt, layout = case
+    say(f"[topk] {case} thr={thr} topk={topk}")
+    q, k = _qk(case, 20)
+    scores = fta.flash_block_score(q, k, H, b, pad)
+    idx, raw, avg = fta.flash_topk_select(scores, thr, topk, b, pad)
+    fi, fr, fa = fta.flash_topk_score(q, k, H, b, topk, pad, thr)
+    torch.cuda.synchronize()
+    ri, rr, ra = O.topk_select(scores.cpu().numpy(), thr, topk, b, pad)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ri)
+    np.testing.assert_array_equal(raw.cpu().numpy(), rr)
+    np.testing.assert_array_equal(avg.cpu().numpy(), ra)
+    # fused path evaluates the same fp32 expressions -> identical
+    np.testing.assert_array_equal(fi.cpu().numpy(), ri)
+    np.testing.assert_array_equal(fr.cpu().numpy(), rr)
+    np.testing.assert_array_equal(fa.cpu().numpy(), ra)
+
+
+@pytest.mark.parametrize("case", SCORE_CASES[:4], ids=lambda c: f"N{c[1]}D{c[3]}b{c[4]}")
+def test_topk_score_vs_float64_oracle(case):
+    B, N, H, D, b, pad, dt, layout = case
+    say(f"[topk_score64] {case}")
+    q, k = _qk(case, 30)
+    fi, _, _ = fta.flash_topk_score(q, k, H, b, 16, pad, 1.0)
+    torch.cuda.synchronize()
+    qn, kn = _oracle_inputs(q, k)
+    s64 = O.block_score(qn, kn, H, b, pad)
+    M = s64.shape[-1]
+    vc = O.valid_counts(M, b, pad).astype(np.float64)
+    avg64 = s64 / vc
+    ri, _, _ = O.topk_select(s64.astype(np.float32), 1.0, 16, b, pad)
+    bad, ndiff = check_topk_gap(fi.cpu().numpy(), avg64, ri)
+    assert bad == 0, f"{bad} of {ndiff} differing indices have score gap >= 1e-6"
+
+
+@pytest.mark.parametrize("g,K,Mt,W,pad", [(32, 16, 128, None, (0, 0)), (1, 16, 128, None, (0, 0)),
+                                          (16, 8, 157, 128, (3, 13)), (32, 16, 512, 256, (0, 0)),
+                                          (4, 64, 4096, 300, (1, 3))])
+@pytest.mark.parametrize("with_scores", [False, True])
+def test_merge_bit_exact(g, K, Mt, W, pad, with_scores):
+    say(f"[merge] g={g} K={K} Mt={Mt} W={W} pad={pad} scores={with_scores}")
+    rng = np.random.default_rng(5)
+    B, H = 1, 2
+    N = 64 * g - pad[0] - pad[1]
+    idx = np.stack([rng.permutation(Mt)[:K] for _ in range(B * H * N)]).reshape(B, H, N, K).astype(np.int32)
+    idx[..., K - 2:][rng.random((B, H, N, 2)) < 0.3] = -1  # ragged rows
+    scr = rng.random((B, H, N, K)).astype(np.float32) if with_scores else None
+    ti = torch.from_numpy(idx).cuda()
+    ts = torch.from_numpy(scr).cuda() if with_scores else None
+    m, c, w = fta.build_qblock_topk_indices(ti, g, pad, ts, W)
+    torch.cuda.synchronize()
+    rm, rc, rw = O.build_qblock_topk_indices(idx, g, pad, scr, W)
+    assert w == rw
+    np.testing.assert_array_equal(m.cpu().numpy(), rm)
+    np.testing.assert_array_equal(c.cpu().numpy(), rc)
+
+
+ATTN_CASES = [
+    # B, N, H, D, g, b, qpad, kvpad, W, dtype
+    (1, 1024, 2, 64, 32, 64, (0, 0), (0, 0), 12, torch.float16),
+    (1, 1024, 2, 128, 32, 64, (0, 0), (0, 0), 20, torch.bfloat16),
+    (2, 1000, 2, 64, 16, 64, (8, 8), (24, 24), 10, torch.bfloat16),
+    (1, 777, 2, 128, 64, 96, (13, 2), (5, 82), 6, torch.float16),
+    (1, 512, 2, 32, 1, 64, (0, 0), (0, 0), 4, torch.bfloat16),
+    (1, 600, 1, 256, 48, 40, (0, 24), (0, 0), 7, torch.bfloat16),
+    (1, 500, 2, 160, 20, 128, (0, 0), (12, 116), 3, torch.float16),
+    (1, 256, 2, 64, 32, 64, (0, 0), (0, 0), 4, torch.float32),
+]
+
+
+def _random_merged(B, H, QM, W, M, seed, empty_frac=0.1):
+    rng = np.random.default_rng(seed)
+    merged = np.full((B, H, QM, W), -1, dtype=np.int32)
+    for bb in range(B):
+        for h in range(H):
+            for qm in range(QM):
+                if rng.random() < empty_frac:
+                    continue
+                n = int(rng.integers(1, min(W, M) + 1))
+                merged[bb, h, qm, :n] = rng.permutation(M)[:n]
+    return merged
+
+
+def _attn_inputs(case, seed):
+    B, N, H, D, g, b, qpad, kvpad, W, dt = case
+    QM = (qpad[0] + N + qpad[1]) // g
+    M = (kvpad[0] + N + kvpad[1]) // b
+    merged = _random_merged(B, H, QM, W, M, seed)
+    q = rand((B, N, H * D), seed + 1, dt, "cuda")
+    k = rand((B, N, H * D), seed + 2, dt, "cuda")
+    v = rand((B, N, H * D), seed + 3, dt, "cuda")
+    return q, k, v, merged
+
+
+def _rounded(x):
+    return np32(x.bfloat16() if x.dtype == torch.float32 else x)
+
+
+@pytest.mark.parametrize("case", ATTN_CASES, ids=lambda c: f"N{c[1]}D{c[3]}g{c[4]}b{c[5]}q{c[6]}kv{c[7]}")
+def test_sparse_attn_fwd_bwd_vs_oracle(case):
+    B, N, H, D, g, b, qpad, kvpad, W, dt = case
+    say(f"[attn] {case}")
+    q, k, v, merged = _attn_inputs(case, 40)
+    q.requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+    tm = torch.from_numpy(merged).cuda()
+    counts = (tm >= 0).sum(-1).int()
+    o, lse = fta.flash_topk_attn(q, k, v, tm, counts, H, g, b, None, None, kvpad, qpad)
+    do = rand((B, N, H * D), 99, o.dtype, "cuda")
+    o.backward(do)
+    torch.cuda.synchronize()
+    qn, kn, vn = _rounded(q), _rounded(k), _rounded(v)
+    ro, rl = O.sparse_attn(qn, kn, vn, merged, H, g, b, None, qpad, kvpad)
+    assert o.dtype == dt
+    np.testing.assert_allclose(np32(o), ro, atol=2e-3, rtol=1e-2)
+    l = lse.cpu().numpy()
+    np.testing.assert_array_equal(np.isneginf(l), np.isneginf(rl))
+    fin = np.isfinite(rl)
+    np.testing.assert_allclose(l[fin], rl[fin], rtol=1e-4, atol=1e-4)
+    dq, dk, dv = O.sparse_attn_bwd(qn, kn, vn, np32(do), merged, H, g, b, None, qpad, kvpad)
+    for name, got, ref in (("dq", q.grad, dq), ("dk", k.grad, dk), ("dv", v.grad, dv)):
+        np.testing.assert_allclose(np32(got), ref, atol=2e-3 * max(1.0, np.abs(ref).max() / 4), rtol=1e-2,
+                                   err_msg=name)
+
+
+def test_reverse_indices_and_sort_by_count():
+    say("[reverse]")
+    B, H, QM, W, M = 2, 3, 70, 9, 40
+    merged = _random_merged(B, H, QM, W, M, 7)
+    counts = (merged >= 0).sum(-1).astype(np.int32)
+    tm = torch.from_numpy(merged).cuda()
+    tc = torch.from_numpy(counts).cuda()
+    rev, cnt, skv = fta.flash_build_reverse_indices(tm, tc, M)
+    sc, sid = fta.flash_sort_by_count(cnt, H, M)
+    torch.cuda.synchronize()
+    rrev, rcnt, rskv = O.build_reverse_indices(merged, counts, M)
+    np.testing.assert_array_equal(rev.cpu().numpy(), rrev)
+    np.testing.assert_array_equal(cnt.cpu().numpy(), rcnt)
+    np.testing.assert_array_equal(skv.cpu().numpy(), rskv)
+    rsc, rsid = O.sort_by_count(rcnt, H, M)
+    np.testing.assert_array_equal(sc.cpu().numpy(), rsc)
+    np.testing.assert_array_equal(sid.cpu().numpy(), rsid)
+
+
+def test_preprocess_delta():
+    say("[delta]")
+    o = rand((2, 100, 3 * 64), 1, torch.bfloat16, "cuda")
+    do = rand((2, 100, 3 * 64), 2, torch.bfloat16, "cuda")
+    d = fta.preprocess_delta(o, do, 3)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(d.cpu().numpy(), O.preprocess_delta(np32(o), np32(do), 3), rtol=1e-5, atol=1e-5)
+
+
+def test_pipeline_config1():
+    """BASELINE config 1 end to end: score -> merge -> sparse attention."""
+    say("[pipeline C1]")
+    B, N, H, D = 1, 1024, 8, 64
+    q = rand((B, N, H * D), 0, torch.float16, "cuda")
+    k = rand((B, N, H * D), 1, torch.float16, "cuda")
+    v = rand((B, N, H * D), 2, torch.float16, "cuda")
+    idx, raw, avg = fta.flash_topk_score(q, k, H, 64, 16, (0, 0), 1.0)
+    merged, counts, W = fta.build_qblock_topk_indices(idx, 32, (0, 0), avg, None)
+    o, lse = fta.flash_topk_attn(q, k, v, merged, counts, H, 32, 64)
+    torch.cuda.synchronize()
+    assert W == 512 and merged.shape == (B, H, 32, 512)
+    # topk=16=M keeps every block -> every q-block attends to all 16 blocks -> dense attention
+    assert (counts == 16).all()
+    qt, kt, vt = (x.double().view(B, N, H, D).transpose(1, 2) for x in (q, k, v))
+    ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt).transpose(1, 2).reshape(B, N, H * D)
+    np.testing.assert_allclose(np32(o), ref.cpu().numpy(), atol=2e-3, rtol=1e-2)

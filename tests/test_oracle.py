@@ -1,0 +1,295 @@
+"""Pins the CPU oracle (oracle/fta_oracle.py) against independent checks.
+
+The reference ships no tests, fixtures or golden vectors, so every oracle
+function is pinned here by brute force on tiny inputs, by special cases that
+reduce to a library routine (torch softmax / SDPA / autograd), and by
+invariants.  Each check is chosen so that a plausible slip (wrong tie
+direction, dropped padding term, transposed operand, off-by-one cut) fails.
+"""
+
+import math
+from collections import Counter
+
+import numpy as np
+import pytest
+import torch
+
+import fta_oracle as O
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------- block score
+
+
+def _brute_block_score(q, k, H, b, padding):
+    B, N, C = q.shape
+    D = C // H
+    ph, pt = padding
+    M = (ph + N + pt) // b
+    out = np.zeros((B, H, N, M))
+    for bb in range(B):
+        for h in range(H):
+            for n in range(N):
+                s = [sum(q[bb, n, h * D + d] * k[bb, t, h * D + d] for d in range(D)) / math.sqrt(D)
+                     for t in range(N)]
+                mx = max(s)
+                e = [math.exp(x - mx) for x in s]
+                tot = sum(e)
+                for t in range(N):
+                    out[bb, h, n, (t + ph) // b] += e[t] / tot
+    return out
+
+
+@pytest.mark.parametrize("padding", [(0, 2), (1, 1), (2, 0)])
+def test_block_score_brute_force(padding):
+    r = _rng(0)
+    B, N, H, D, b = 1, 7, 2, 4, 3
+    if (padding[0] + N + padding[1]) % b:
+        pytest.skip("not divisible")
+    q = r.standard_normal((B, N, H * D))
+    k = r.standard_normal((B, N, H * D))
+    got = O.block_score(q, k, H, b, padding)
+    ref = _brute_block_score(q, k, H, b, padding)
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(got.sum(-1), 1.0, rtol=1e-12)
+
+
+def test_block_score_b1_is_softmax_and_4d_layout():
+    r = _rng(1)
+    B, N, H, D = 2, 16, 3, 8
+    q = r.standard_normal((B, N, H * D)).astype(np.float32)
+    k = r.standard_normal((B, N, H * D)).astype(np.float32)
+    got = O.block_score(q, k, H, 1)
+    qt = torch.from_numpy(q).double().view(B, N, H, D).transpose(1, 2)
+    kt = torch.from_numpy(k).double().view(B, N, H, D).transpose(1, 2)
+    ref = torch.softmax(qt @ kt.transpose(-1, -2) / math.sqrt(D), dim=-1).numpy()
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-15)
+    # 4D input [B, H, N, D] gives the same result
+    got4 = O.block_score(qt.numpy(), kt.numpy(), None, 1)
+    np.testing.assert_allclose(got4, got, rtol=1e-12)
+    # row subset
+    rows = np.array([3, 0, 15])
+    np.testing.assert_allclose(O.block_score(q, k, H, 1, rows=rows), got[:, :, rows], rtol=1e-12)
+
+
+# ---------------------------------------------------------------- top-k select
+
+
+def _brute_topk(scores, thr, topk, b, padding):
+    M = len(scores)
+    ph, pt = padding
+    vc = [float(b)] * M
+    if ph:
+        vc[0] = float(b - ph)
+    if pt:
+        vc[-1] = float(b - pt)
+    avg = [np.float32(np.float32(s) / np.float32(c)) for s, c in zip(scores, vc)]
+    order = sorted(range(M), key=lambda j: (-float(avg[j]), j))
+    m_out = min(topk, M) if topk > 0 else M
+    cs = np.float32(0)
+    cut = m_out
+    for p in range(m_out):
+        cs = np.float32(cs + np.float32(avg[order[p]] * np.float32(vc[order[p]])))
+        if cs >= np.float32(thr):
+            cut = p + 1
+            break
+    idx = [order[p] if p < cut else -1 for p in range(m_out)]
+    avg_o = [float(avg[order[p]]) if p < cut else 0.0 for p in range(m_out)]
+    return idx, avg_o
+
+
+@pytest.mark.parametrize("thr,topk,padding", [(1.0, 0, (0, 0)), (0.5, 4, (0, 0)), (0.9, 8, (3, 5)),
+                                              (2.0, 6, (7, 0)), (0.0, 5, (0, 0))])
+def test_topk_select_brute_force(thr, topk, padding):
+    r = _rng(2)
+    b, M = 8, 12
+    raw = r.dirichlet(np.ones(M), size=(1, 2, 5)).astype(np.float32)
+    idx, rw, av = O.topk_select(raw, thr, topk, b, padding)
+    for h in range(2):
+        for n in range(5):
+            bi, ba = _brute_topk(raw[0, h, n], thr, topk, b, padding)
+            assert list(idx[0, h, n]) == bi
+            np.testing.assert_array_equal(av[0, h, n], np.float32(ba))
+
+
+def test_topk_select_ties_go_to_lower_index():
+    raw = np.array([[[[0.1, 0.3, 0.3, 0.1, 0.2]]]], dtype=np.float32)
+    idx, _, _ = O.topk_select(raw, 2.0, 0, 4)
+    assert idx[0, 0, 0].tolist() == [1, 2, 4, 0, 3]
+
+
+def test_topk_select_partial_block_normalisation():
+    # block 0 only holds 2 valid tokens: its average beats a larger raw score
+    raw = np.array([[[[0.3, 0.4, 0.3]]]], dtype=np.float32)
+    idx, rw, av = O.topk_select(raw, 0.5, 3, 4, (2, 0))
+    assert idx[0, 0, 0].tolist() == [0, 1, -1]
+    np.testing.assert_allclose(av[0, 0, 0, :2], [0.15, 0.1], rtol=1e-6)
+    np.testing.assert_allclose(rw[0, 0, 0, :2], [0.3, 0.4], rtol=1e-6)
+
+
+def test_topk_select_threshold_one_and_full_sort():
+    r = _rng(3)
+    raw = r.random((1, 1, 4, 9)).astype(np.float32)
+    idx, _, av = O.topk_select(raw, 1e9, 0, 2)
+    for n in range(4):
+        assert idx[0, 0, n].tolist() == sorted(range(9), key=lambda j: (-raw[0, 0, n, j], j))
+        assert np.all(np.diff(av[0, 0, n]) <= 0)
+
+
+# ---------------------------------------------------------------- merge
+
+
+def test_merge_ones_is_count_union():
+    r = _rng(4)
+    B, H, N, K, g, M = 1, 2, 16, 3, 4, 10
+    idx = np.stack([r.permutation(M)[:K] for _ in range(B * H * N)]).reshape(B, H, N, K).astype(np.int32)
+    idx[0, 0, 3, 2] = -1
+    merged, counts, W = O.build_qblock_topk_indices(idx, g)
+    assert W == g * K
+    for h in range(H):
+        for qm in range(N // g):
+            c = Counter(int(x) for x in idx[0, h, qm * g:(qm + 1) * g].ravel() if x >= 0)
+            exp = sorted(c, key=lambda j: (-c[j], j))
+            got = merged[0, h, qm]
+            assert got[: len(exp)].tolist() == exp
+            assert np.all(got[len(exp):] == -1)
+            assert counts[0, h, qm] == len(exp)
+
+
+def test_merge_scores_truncation_and_padding():
+    idx = np.array([[[[2, 0], [0, -1], [5, 2], [1, 3]]]], dtype=np.int32)
+    scr = np.array([[[[0.5, 0.25], [0.25, 9.0], [0.125, 0.5], [0.0, 0.75]]]], dtype=np.float32)
+    # q_padding=(1,1) with g=3: rows -> [-1, r0, r1 | r2, r3, -1]
+    merged, counts, W = O.build_qblock_topk_indices(idx, 3, (1, 1), scr, qblock_topk=3)
+    # q-block 0: {2:.5, 0:.25+.25=.5} -> tie -> 0 then 2 ; q-block 1: {5:.125, 2:.5, 1:0, 3:.75}
+    assert merged[0, 0, 0].tolist() == [0, 2, -1]
+    assert merged[0, 0, 1].tolist() == [3, 2, 5]
+    assert counts[0, 0].tolist() == [2, 3]
+
+
+def test_merge_sequential_fp32_order():
+    # 1 + 1e-8 + 1e-8 ... in (row, slot) order loses the small terms in fp32
+    idx = np.zeros((1, 1, 4, 1), dtype=np.int32)
+    scr = np.array([1.0, 1e-8, 1e-8, 1e-8], dtype=np.float32).reshape(1, 1, 4, 1)
+    _, ms = O.qblock_merge(idx, scr, 4, 1, 1)
+    assert ms[0, 0, 0, 0] == np.float32(1.0)
+
+
+# ---------------------------------------------------------------- attention fwd/bwd
+
+
+def _torch_masked_dense(q, k, v, merged, H, g, b, scale, qpad, kvpad):
+    """Independent torch restatement (v2/sparse_attn.py:395-485) with autograd."""
+    B, N, C = q.shape
+    D = C // H
+    QM = merged.shape[2]
+    mask = torch.zeros(B, H, N, N, dtype=torch.bool)
+    for bb in range(B):
+        for h in range(H):
+            for qm in range(QM):
+                r0 = qm * g - qpad[0]
+                rs, re = max(0, r0), min(N, r0 + g)
+                for bid in merged[bb, h, qm]:
+                    if bid < 0:
+                        continue
+                    ks, ke = max(0, bid * b - kvpad[0]), min(N, bid * b - kvpad[0] + b)
+                    if rs < re and ks < ke:
+                        mask[bb, h, rs:re, ks:ke] = True
+    qh = q.view(B, N, H, D).transpose(1, 2)
+    kh = k.view(B, N, H, D).transpose(1, 2)
+    vh = v.view(B, N, H, D).transpose(1, 2)
+    s = (qh * scale) @ kh.transpose(-1, -2)
+    s = s.masked_fill(~mask, float("-inf"))
+    lse = torch.logsumexp(s, -1)
+    p = torch.softmax(s, -1).nan_to_num(0.0)
+    o = (p @ vh).transpose(1, 2).reshape(B, N, C)
+    return o, lse
+
+
+@pytest.mark.parametrize("g,b,qpad,kvpad", [(3, 6, (0, 0), (0, 0)), (4, 5, (1, 1), (2, 0)), (5, 4, (3, 4), (1, 1))])
+def test_sparse_attn_fwd_bwd_vs_torch_autograd(g, b, qpad, kvpad):
+    r = _rng(5)
+    B, N, H, D = 2, 18, 2, 8
+    if (qpad[0] + N + qpad[1]) % g or (kvpad[0] + N + kvpad[1]) % b:
+        pytest.skip("bad padding")
+    QM = (qpad[0] + N + qpad[1]) // g
+    M = (kvpad[0] + N + kvpad[1]) // b
+    merged = np.full((B, H, QM, 3), -1, dtype=np.int32)
+    for bb in range(B):
+        for h in range(H):
+            for qm in range(QM):
+                n = r.integers(0, 4)
+                merged[bb, h, qm, :n] = r.permutation(M)[:n]
+    q, k, v, do = (r.standard_normal((B, N, H * D)) for _ in range(4))
+    scale = 0.3
+    o, lse = O.sparse_attn(q, k, v, merged, H, g, b, scale, qpad, kvpad)
+    qt, kt, vt = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    ot, lset = _torch_masked_dense(qt, kt, vt, merged, H, g, b, scale, qpad, kvpad)
+    np.testing.assert_allclose(o, ot.detach().numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_array_equal(np.isinf(lse), torch.isinf(lset).numpy())
+    fin = np.isfinite(lse)
+    np.testing.assert_allclose(lse[fin], lset.detach().numpy()[fin], rtol=1e-10)
+    ot.backward(torch.tensor(do))
+    dq, dk, dv = O.sparse_attn_bwd(q, k, v, do, merged, H, g, b, scale, qpad, kvpad)
+    np.testing.assert_allclose(dq, qt.grad.numpy(), rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(dk, kt.grad.numpy(), rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(dv, vt.grad.numpy(), rtol=1e-9, atol=1e-11)
+    # delta = rowsum(O * dO)
+    dl = O.preprocess_delta(o, do, H)
+    np.testing.assert_allclose(dl, (ot.detach().numpy() * do).reshape(B, N, H, D).sum(-1).transpose(0, 2, 1))
+
+
+def test_sparse_attn_all_blocks_is_dense_sdpa():
+    r = _rng(6)
+    B, N, H, D, g, b = 1, 32, 2, 16, 8, 8
+    M, QM = N // b, N // g
+    merged = np.tile(np.arange(M, dtype=np.int32)[::-1], (B, H, QM, 1))
+    q, k, v = (r.standard_normal((B, N, H * D)).astype(np.float32) for _ in range(3))
+    o, lse = O.sparse_attn(q, k, v, merged, H, g, b)
+    th = [torch.from_numpy(x).double().view(B, N, H, D).transpose(1, 2) for x in (q, k, v)]
+    ref = torch.nn.functional.scaled_dot_product_attention(*th).transpose(1, 2).reshape(B, N, H * D)
+    np.testing.assert_allclose(o, ref.numpy(), rtol=1e-10, atol=1e-12)
+    ref_lse = torch.logsumexp(th[0] @ th[1].transpose(-1, -2) / math.sqrt(D), -1)
+    np.testing.assert_allclose(lse, ref_lse.numpy(), rtol=1e-12)
+
+
+def test_empty_qblock_gives_zero_and_neg_inf():
+    r = _rng(7)
+    q, k, v = (r.standard_normal((1, 8, 4)) for _ in range(3))
+    merged = np.full((1, 1, 2, 2), -1, dtype=np.int32)
+    merged[0, 0, 1, 0] = 1
+    o, lse = O.sparse_attn(q, k, v, merged, 1, 4, 4)
+    assert np.all(o[0, :4] == 0) and np.all(np.isneginf(lse[0, 0, :4]))
+    assert np.all(np.isfinite(lse[0, 0, 4:]))
+
+
+# ---------------------------------------------------------------- reverse index / sort
+
+
+def test_reverse_indices_brute_force():
+    r = _rng(8)
+    B, H, QM, W, M = 1, 3, 9, 4, 7
+    merged = np.full((B, H, QM, W), -1, dtype=np.int32)
+    counts = np.zeros((B, H, QM), dtype=np.int32)
+    for h in range(H):
+        for qm in range(QM):
+            n = r.integers(0, W + 1)
+            merged[0, h, qm, :n] = r.permutation(M)[:n]
+            counts[0, h, qm] = n
+    rev, cnt, skv = O.build_reverse_indices(merged, counts, M)
+    for h in range(H):
+        lists = {m: [] for m in range(M)}
+        for qm in range(QM):
+            for s in range(counts[0, h, qm]):
+                lists[int(merged[0, h, qm, s])].append(qm)
+        for m in range(M):
+            assert rev[0, h, m, : cnt[0, h, m]].tolist() == sorted(lists[m])
+            assert np.all(rev[0, h, m, cnt[0, h, m]:] == -1)
+        assert skv[0, h].tolist() == sorted(range(M), key=lambda m: (-len(lists[m]), m))
+    sc, sid = O.sort_by_count(cnt, H, M)
+    flat = cnt.ravel().tolist()
+    assert sid.tolist() == sorted(range(len(flat)), key=lambda i: (-flat[i], i))
+    assert sc.tolist() == [flat[i] for i in sid]
