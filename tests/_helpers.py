@@ -38,3 +38,18 @@ def check_topk_gap(gpu_idx, ref_scores_avg, ref_idx, atol_gap=1e-6):
         if gap > atol_gap:
             bad += 1
     return bad, len(diff[0])
+
+
+def assert_close_frac(got, ref, atol, rtol, min_frac=0.9999, hard_atol=1e-2, name=""):
+    """bf16/fp16 tolerance: |got - ref| <= atol + rtol*|ref| on at least
+    ``min_frac`` of the elements (P is rounded to 16 bits before the P.V / dS.K
+    products, as in the reference kernels, so isolated elements can exceed the
+    per-element bound), and never more than ``hard_atol`` + rtol*|ref|."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, name
+    err = np.abs(got - ref)
+    ok = err <= atol + rtol * np.abs(ref)
+    frac = ok.mean() if ok.size else 1.0
+    assert frac >= min_frac, f"{name}: only {frac:.6f} of elements within atol={atol}, rtol={rtol}; max err {err.max()}"
+    assert np.all(err <= hard_atol + rtol * np.abs(ref)), f"{name}: max err {err.max()} beyond hard bound"
