@@ -1,0 +1,227 @@
+"""Benchmark: flash-topk-attention V2 hot path on one MI355X.
+
+One step = flash_topk_score -> build_qblock_topk_indices -> flash_topk_attn
+forward -> backward, on BASELINE config 3 (B=1, N=32768, H=32, D=128 bf16,
+peaked synthetic attention, b=64, topk=16, threshold=0.9, g=32, W=256).
+Prints one JSON line (driver contract).  Extra fields: per-stage ms, the
+C3-iid variant's forward/backward throughput, the scoring kernel's roofline
+(measured with HIP events on the stream it runs on) and a CPU baseline (the
+numpy oracle on a bounded sample, host cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "flash-topk-attention_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def make_inputs(B, N, H, D, peaked, seed, dev):
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    C = H * D
+    if not peaked:
+        q, k, v = (torch.randn(B, N, C, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+        return q, k, v
+    b = 64
+    M = N // b
+    cent = torch.randn(B, M, C, generator=g, device=dev)
+    k = 0.3 * torch.randn(B, N, C, generator=g, device=dev) + cent.repeat_interleave(b, dim=1)
+    nseg = N // 1024
+    choice = torch.stack([torch.randperm(M, generator=g, device=dev)[:8] for _ in range(B * nseg)]).view(B, nseg, 8)
+    pick_slot = torch.randint(0, 8, (B, N), generator=g, device=dev)
+    seg = torch.arange(N, device=dev) // 1024
+    pick = torch.gather(choice[:, seg, :], 2, pick_slot.unsqueeze(-1)).squeeze(-1)  # [B, N]
+    q = 0.3 * torch.randn(B, N, C, generator=g, device=dev) + torch.gather(
+        cent, 1, pick.unsqueeze(-1).expand(B, N, C))
+    v = torch.randn(B, N, C, generator=g, device=dev)
+    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+def cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, rows):
+    """Numpy oracle (oracle/fta_oracle.py) on head 0, first `rows` queries."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import fta_oracle as O
+
+    N = q.shape[1]
+    f = lambda t: t[:, :, :D].float().cpu().numpy()  # head 0
+    qn, kn, vn, dn = f(q), f(k), f(v), f(do)
+    t0 = time.perf_counter()
+    sc = O.block_score(qn, kn, 1, b, rows=np.arange(rows))
+    idx, raw, avg = O.topk_select(sc.astype(np.float32), thr, topk, b)
+    merged, counts, _ = O.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
+    qbl = [(0, 0, qm) for qm in range(rows // g)]
+    full = np.full((1, 1, N // g, W), -1, dtype=np.int32)
+    full[:, :, : rows // g] = merged
+    O.sparse_attn(qn, kn, vn, full, 1, g, b, None, qblocks=qbl)
+    O.sparse_attn_bwd(qn, kn, vn, dn, full, 1, g, b, None, qblocks=qbl)
+    secs = time.perf_counter() - t0
+    P = g * b * int(counts.sum())
+    flops = 2.0 * rows * N * D + 14.0 * D * P
+    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": os.cpu_count(), "kind": "port",
+            "seconds": secs,
+            "sample": f"numpy oracle, 1 head x {rows} queries of the C3 workload "
+                      f"(score+select+merge+fwd+bwd), float64 BLAS"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-iid", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=8192)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); every stage is per (b, h) "
+              "and shards over heads with no communication, so N>1 is not measured here.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import flash_topk_attn_v2 as fta
+    from flash_topk_attn_v2 import _lib
+
+    dev = torch.device("cuda:0")
+    B, N, H, D, b, topk, thr, g, W = 1, 32768, 32, 128, 64, 16, 0.9, 32, 256
+    q, k, v = make_inputs(B, N, H, D, True, 2, dev)
+    gd = torch.Generator(device=dev).manual_seed(7)
+    do = torch.randn(B, N, H * D, generator=gd, device=dev).to(torch.bfloat16)
+    ql, kl, vl = (t.detach().requires_grad_(True) for t in (q, k, v))
+
+    stream = torch.cuda.current_stream(dev)
+
+    def step(record=None):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)] if record is not None else None
+        ql.grad = kl.grad = vl.grad = None
+        if ev: ev[0].record(stream)
+        idx, raw, avg = fta.flash_topk_score(ql.detach(), kl.detach(), H, b, topk, (0, 0), thr)
+        if ev: ev[1].record(stream)
+        merged, counts, Wd = fta.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
+        if ev: ev[2].record(stream)
+        o, lse = fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, b)
+        if ev: ev[3].record(stream)
+        o.backward(do)
+        if ev:
+            ev[4].record(stream)
+            record.append(ev)
+        return counts
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        counts = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    recs = []
+    for _ in range(3):
+        counts = step(recs)
+    torch.cuda.synchronize()
+    names = ["score", "merge", "fwd", "bwd"]
+    stage = {n: sorted(r[i].elapsed_time(r[i + 1]) for r in recs)[1] for i, n in enumerate(names)}
+
+    P = g * b * float(counts.sum().item())
+    f_score = 2.0 * B * H * N * N * D
+    f_fwd, f_bwd = 4.0 * D * P, 10.0 * D * P
+    flops = f_score + f_fwd + f_bwd
+    value = flops / (ms * 1e-3) / 1e12
+
+    # dominant kernel: scoring stage 1 (fta_block_score_lse_kernel), timed alone
+    M = N // b
+    blk = torch.empty(B * H * M * N, device=dev, dtype=torch.float32)
+    row = torch.empty(B * H * N, device=dev, dtype=torch.float32)
+    qs = _lib.i64arr([N * H * D, D, H * D])
+    L = _lib.lib()
+
+    def score_lse():
+        rc = L.fta_block_score_lse(q.data_ptr(), k.data_ptr(), 0, B, H, N, D, qs, qs, b, 0, 0, D ** -0.5,
+                                   blk.data_ptr(), row.data_ptr(), stream.cuda_stream)
+        _lib.check(rc, "fta_block_score_lse")
+
+    score_lse()
+    reps = 10
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        score_lse()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    k_ms = e0.elapsed_time(e1) / reps
+    achieved = f_score / (k_ms * 1e-3) / 1e12
+    del blk, row
+
+    out = {
+        "metric": "score+attn fwd+bwd ms and TFLOP/s at N=32K,D=128 bf16; % of MFMA peak",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (BASELINE config 3: peaked block-centred q/k, iid v, seed 2)",
+        "config": {"workload": "C3 threshold: B1 N32768 H32 D128, b64 topk16 thr0.9 g32 W256; "
+                               "score+merge+sparse fwd+bwd",
+                   "global_batch": B, "seq_len": N, "heads": H, "head_dim": D, "parallelism": "none"},
+        "stage_ms": {k2: round(v2, 3) for k2, v2 in stage.items()},
+        "flops": {"score": f_score, "fwd": f_fwd, "bwd_10DP": f_bwd, "P_pairs": P},
+        "roofline": {"bound": "mfma", "kernel": "fta_block_score_lse_kernel", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "kernel_ms": round(k_ms, 3), "traffic": None},
+    }
+
+    if not args.no_iid:
+        # C3-iid variant (the MFMA gate for the sparse forward/backward)
+        del ql, kl, vl
+        torch.cuda.empty_cache()
+        qi, ki, vi = make_inputs(B, N, H, D, False, 3, dev)
+        idx, raw, avg = fta.flash_topk_score(qi, ki, H, b, topk, (0, 0), 1.0)
+        merged, counts_i, _ = fta.build_qblock_topk_indices(idx, g, (0, 0), avg, 512)
+        qi.requires_grad_(True)
+        ki.requires_grad_(True)
+        vi.requires_grad_(True)
+        fw, bw = [], []
+        for it in range(4):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            e[0].record(stream)
+            o, lse = fta.flash_topk_attn(qi, ki, vi, merged, counts_i, H, g, b)
+            e[1].record(stream)
+            o.backward(do)
+            e[2].record(stream)
+            torch.cuda.synchronize()
+            if it:
+                fw.append(e[0].elapsed_time(e[1]))
+                bw.append(e[1].elapsed_time(e[2]))
+        Pi = g * b * float(counts_i.sum().item())
+        fms, bms = sorted(fw)[1], sorted(bw)[1]
+        out["c3_iid"] = {"fwd_ms": round(fms, 3), "bwd_ms": round(bms, 3),
+                         "fwd_tflops": round(4 * D * Pi / fms / 1e9, 2),
+                         "bwd_tflops_10DP": round(10 * D * Pi / bms / 1e9, 2),
+                         "mean_count": Pi / (g * b * B * H * (N // g))}
+
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, args.cpu_rows)
+
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -510,6 +510,19 @@ int launch_topk(const float* in, int64_t stride_row, int64_t stride_m, const flo
 
 extern "C" {
 
+int fta_block_score_lse(const void* q, const void* k, int dtype, int B, int H, int N, int D,
+                        const int64_t* q_strides, const int64_t* k_strides, int score_block_size, int pad_head,
+                        int pad_tail, float scale, float* blk_lse, float* row_lse, void* stream) {
+    FTA_TRY_BEGIN
+    int M = 0;
+    int st = fta::check_score_args(B, H, N, D, score_block_size, pad_head, pad_tail, &M);
+    if (st != FTA_OK) return st;
+    if (!q || !k || !blk_lse || !row_lse) return fta::arg_error("block_score_lse: null pointer");
+    return launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, scale,
+                            blk_lse, row_lse, (hipStream_t)stream);
+    FTA_TRY_END
+}
+
 size_t fta_block_score_workspace_size(int B, int H, int N, int M) {
     return fta::align_up((size_t)B * H * M * N * sizeof(float)) + fta::align_up((size_t)B * H * N * sizeof(float));
 }

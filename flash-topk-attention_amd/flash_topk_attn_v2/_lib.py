@@ -35,6 +35,7 @@ _SIGNATURES = {
     "fta_version": (_i, []),
     "fta_block_score_workspace_size": (_sz, [_i, _i, _i, _i]),
     "fta_block_score": (_i, [_p, _p, _i, _i, _i, _i, _i, _i64p, _i64p, _i, _i, _i, _f, _p, _p, _sz, _p]),
+    "fta_block_score_lse": (_i, [_p, _p, _i, _i, _i, _i, _i, _i64p, _i64p, _i, _i, _i, _f, _p, _p, _p]),
     "fta_topk_select": (_i, [_p, _i64, _i, _i64, _i64, _i, _i, _i, _i, _f, _p, _p, _p, _p]),
     "fta_topk_score_workspace_size": (_sz, [_i, _i, _i, _i]),
     "fta_topk_score": (_i, [_p, _p, _i, _i, _i, _i, _i, _i64p, _i64p, _i, _i, _i, _f, _i, _f, _p, _p, _p, _p,

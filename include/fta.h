@@ -49,6 +49,18 @@ int fta_version(void);
 
 /* ---------------------------------------------------------------- scoring */
 
+/*
+ * Scoring stage 1 alone: blk_lse[b*H+h][m][n] = log2 sum_{keys of block m}
+ * 2^(scale*log2(e) * q.k) and row_lse[b*H+h][n] = log2 of the row total (fp32).
+ * score[n][m] = 2^(blk_lse - row_lse).  This is the MFMA-bound half of
+ * block_score_launch (flash_topk_attn_v2/csrc/block_score_kernel.cu:19-227,
+ * m_locals / l_locals) with the per-block state folded into one log value.
+ */
+int fta_block_score_lse(const void* q, const void* k, int dtype, int B, int H, int N, int D,
+                        const int64_t* q_strides, const int64_t* k_strides, int score_block_size,
+                        int pad_head, int pad_tail, float scale, float* blk_lse, float* row_lse,
+                        void* stream);
+
 /* Workspace for fta_block_score: per-block log2-sum-exp [B*H][M][N] f32 plus
  * row totals [B*H][N] f32. */
 size_t fta_block_score_workspace_size(int B, int H, int N, int M);
