@@ -97,14 +97,14 @@ __device__ int fta_build_q_masks(const AttnArgs& a, int bh, int p0, int seg0, in
     }
     __syncthreads();
     int U = 0;
-    for (int base = 0; base < segn; base += 256) {
+    for (int base = 0; base < segn; base += blockDim.x) {
         const int ml = base + tid;
         int any = 0;
-        if (tid < 256 && ml < segn) {
+        if (ml < segn) {
 #pragma unroll
             for (int t = 0; t < T; ++t) any |= (sMask[t][ml] != 0u);
         }
-        // 256-wide scan (threads >= 256, if any, contribute 0)
+        // block-wide exclusive scan of `any`
         const int lane = tid & 63, wave = tid >> 6;
         int x = any;
 #pragma unroll
@@ -135,17 +135,18 @@ __device__ int fta_build_q_masks(const AttnArgs& a, int bh, int p0, int seg0, in
 // lazily rescaled running max (rescale only when the max grows by > 2^8),
 // O^T += V^T P^T.
 // ----------------------------------------------------------------------------
-template <int DT, int D, int TPW>
-__global__ __launch_bounds__(256, 1) void fta_sparse_fwd_kernel(AttnArgs a) {
+template <int DT, int D, int TPW, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) {
     using E = Elem<DT>;
-    constexpr int T = 4 * TPW;
+    constexpr int NTHR = NW * 64;
+    constexpr int T = NW * TPW;
     constexpr int KS = D / 16;
     constexpr int DT32 = D / 32;
     constexpr int KROW = D + 8;
     constexpr int VROW = 64 + 8;
     constexpr int KSEG = D / 8;
-    constexpr int KLOADS = 64 * KSEG / 256;
-    constexpr int VLOADS = D * 8 / 256;
+    constexpr int KLOADS = (64 * KSEG + NTHR - 1) / NTHR;
+    constexpr int VLOADS = (D * 8 + NTHR - 1) / NTHR;
     __shared__ __align__(16) uint16_t sK[2][64 * KROW];
     __shared__ __align__(16) uint16_t sV[2][D * VROW];
     __shared__ uint32_t sMask[T][kSeg];
@@ -207,32 +208,33 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_fwd_kernel(AttnArgs a) {
             const int rem = a.kvb - ch * 64;
 #pragma unroll
             for (int i = 0; i < KLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int row = s / KSEG, sg = s - (s / KSEG) * KSEG;
                 const int t = kb + row;
-                const bool ok = row < rem && t >= 0 && t < a.N && sg * 8 < a.Dreal;
+                const bool ok = s < 64 * KSEG && row < rem && t >= 0 && t < a.N && sg * 8 < a.Dreal;
                 kst[i] = ok ? *reinterpret_cast<const uint4*>(kp + (int64_t)t * a.k_sn + sg * 8) : fta_zero4();
             }
             const int pb = m * a.sbk + ch * 64;
 #pragma unroll
             for (int i = 0; i < VLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int dr = s >> 3, sg = s & 7;
-                vst[i] = *reinterpret_cast<const uint4*>(vtp + (int64_t)dr * a.Npk + pb + sg * 8);
+                vst[i] = (s < D * 8) ? *reinterpret_cast<const uint4*>(vtp + (int64_t)dr * a.Npk + pb + sg * 8)
+                                     : fta_zero4();
             }
         };
         auto store = [&](int buf) {
 #pragma unroll
             for (int i = 0; i < KLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int row = s / KSEG, sg = s - (s / KSEG) * KSEG;
-                *reinterpret_cast<uint4*>(&sK[buf][row * KROW + sg * 8]) = kst[i];
+                if (s < 64 * KSEG) *reinterpret_cast<uint4*>(&sK[buf][row * KROW + sg * 8]) = kst[i];
             }
 #pragma unroll
             for (int i = 0; i < VLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int dr = s >> 3, sg = s & 7;
-                *reinterpret_cast<uint4*>(&sV[buf][dr * VROW + sg * 8]) = vst[i];
+                if (s < D * 8) *reinterpret_cast<uint4*>(&sV[buf][dr * VROW + sg * 8]) = vst[i];
             }
         };
 
@@ -328,7 +330,9 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_fwd_kernel(AttnArgs a) {
                     l_run[tt] += ls;
                     const uint16_t* vbase = &sV[buf][0];
                     const int nks = two ? 4 : 2;
-                    for (int ks = 0; ks < nks; ++ks) {
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) {
+                        if (ks >= nks) break;
 #pragma unroll
                         for (int dt = 0; dt < DT32; ++dt) {
                             const uint16_t* vr = vbase + (dt * 32 + (lane & 31)) * VROW + ks * 16 + hf * 4;
@@ -375,18 +379,19 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_fwd_kernel(AttnArgs a) {
 //   S^T = K Q^T, P^T = 2^{c S^T - lse2}, dP^T = V dO^T, dS^T = P^T (dP^T - delta),
 //   dQ^T += K^T dS^T  (K^T from the T layout).
 // ----------------------------------------------------------------------------
-template <int DT, int D>
-__global__ __launch_bounds__(256, 1) void fta_sparse_dq_kernel(AttnArgs a) {
+template <int DT, int D, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
     using E = Elem<DT>;
     constexpr int NB = (D <= 160) ? 2 : 1;  // LDS buffers (D = 256 single-buffers to fit 160 KB)
-    constexpr int T = 4;
+    constexpr int NTHR = NW * 64;
+    constexpr int T = NW;
     constexpr int KS = D / 16;
     constexpr int DT32 = D / 32;
     constexpr int KROW = D + 8;
     constexpr int VROW = 64 + 8;
     constexpr int KSEG = D / 8;
-    constexpr int KLOADS = 64 * KSEG / 256;
-    constexpr int TLOADS = D * 8 / 256;
+    constexpr int KLOADS = (64 * KSEG + NTHR - 1) / NTHR;
+    constexpr int TLOADS = (D * 8 + NTHR - 1) / NTHR;
     __shared__ __align__(16) uint16_t sK[NB][64 * KROW];
     __shared__ __align__(16) uint16_t sV[NB][64 * KROW];
     __shared__ __align__(16) uint16_t sKt[NB][D * VROW];
@@ -446,34 +451,37 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_dq_kernel(AttnArgs a) {
             const int rem = a.kvb - ch * 64;
 #pragma unroll
             for (int i = 0; i < KLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int row = s / KSEG, sg = s - (s / KSEG) * KSEG;
                 const int t = kb + row;
-                const bool ok = row < rem && t >= 0 && t < a.N && sg * 8 < a.Dreal;
+                const bool ok = s < 64 * KSEG && row < rem && t >= 0 && t < a.N && sg * 8 < a.Dreal;
                 kst[i] = ok ? *reinterpret_cast<const uint4*>(kp + (int64_t)t * a.k_sn + sg * 8) : fta_zero4();
                 vst[i] = ok ? *reinterpret_cast<const uint4*>(vp + (int64_t)t * a.v_sn + sg * 8) : fta_zero4();
             }
             const int pb = m * a.sbk + ch * 64;
 #pragma unroll
             for (int i = 0; i < TLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int dr = s >> 3, sg = s & 7;
-                tst[i] = *reinterpret_cast<const uint4*>(ktp + (int64_t)dr * a.Npk + pb + sg * 8);
+                tst[i] = (s < D * 8) ? *reinterpret_cast<const uint4*>(ktp + (int64_t)dr * a.Npk + pb + sg * 8)
+                                     : fta_zero4();
             }
         };
         auto store = [&](int buf) {
 #pragma unroll
             for (int i = 0; i < KLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int row = s / KSEG, sg = s - (s / KSEG) * KSEG;
-                *reinterpret_cast<uint4*>(&sK[buf][row * KROW + sg * 8]) = kst[i];
-                *reinterpret_cast<uint4*>(&sV[buf][row * KROW + sg * 8]) = vst[i];
+                if (s < 64 * KSEG) {
+                    *reinterpret_cast<uint4*>(&sK[buf][row * KROW + sg * 8]) = kst[i];
+                    *reinterpret_cast<uint4*>(&sV[buf][row * KROW + sg * 8]) = vst[i];
+                }
             }
 #pragma unroll
             for (int i = 0; i < TLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int dr = s >> 3, sg = s & 7;
-                *reinterpret_cast<uint4*>(&sKt[buf][dr * VROW + sg * 8]) = tst[i];
+                if (s < D * 8) *reinterpret_cast<uint4*>(&sKt[buf][dr * VROW + sg * 8]) = tst[i];
             }
         };
 
@@ -502,7 +510,9 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_dq_kernel(AttnArgs a) {
                 const uint16_t* kbase = &sK[buf][0];
                 const uint16_t* vbase = &sV[buf][0];
                 const int nsb = two ? 2 : 1;
-                for (int sb = 0; sb < nsb; ++sb) {
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    if (sb >= nsb) break;
 #pragma unroll
                     for (int ks = 0; ks < KS; ++ks) {
                         const int off = (sb * 32 + (lane & 31)) * KROW + ks * 16 + hf * 8;
@@ -530,7 +540,9 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_dq_kernel(AttnArgs a) {
                 }
                 const uint16_t* tbase = &sKt[buf][0];
                 const int nks = two ? 4 : 2;
-                for (int ks = 0; ks < nks; ++ks) {
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    if (ks >= nks) break;
 #pragma unroll
                     for (int dt = 0; dt < DT32; ++dt) {
                         const uint16_t* tr = tbase + (dt * 32 + (lane & 31)) * VROW + ks * 16 + hf * 4;
@@ -569,17 +581,18 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_dq_kernel(AttnArgs a) {
 //   S = Q K^T, P = 2^{c S - lse2}, dP = dO V^T, dS = P (dP - delta),
 //   dV += P^T dO, dK += dS^T Q.  No atomics.
 // ----------------------------------------------------------------------------
-template <int DT, int D>
-__global__ __launch_bounds__(256, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
+template <int DT, int D, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
     using E = Elem<DT>;
-    constexpr int T = 4;
+    constexpr int NTHR = NW * 64;
+    constexpr int T = NW;
     constexpr int KS = D / 16;
     constexpr int DT32 = D / 32;
     constexpr int QROW = D + 8;
     constexpr int TROW = 32 + 8;
     constexpr int QSEG = D / 8;
-    constexpr int QLOADS = (32 * QSEG + 255) / 256;
-    constexpr int TLOADS = (D * 4 + 255) / 256;
+    constexpr int QLOADS = (32 * QSEG + NTHR - 1) / NTHR;
+    constexpr int TLOADS = (D * 4 + NTHR - 1) / NTHR;
     __shared__ __align__(16) uint16_t sQ[2][32 * QROW];
     __shared__ __align__(16) uint16_t sO[2][32 * QROW];
     __shared__ __align__(16) uint16_t sQt[2][D * TROW];
@@ -638,9 +651,9 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
     for (int seg0 = 0; seg0 < a.NC; seg0 += kSeg) {
         const int segn = min(kSeg, a.NC - seg0);
         // masks: tile tau x chunk (seg0 + cl) -> bits over the chunk's 32 queries
-        for (int i = tid; i < T * kSeg; i += 256) sMask[i / kSeg][i % kSeg] = 0u;
+        for (int i = tid; i < T * kSeg; i += NTHR) sMask[i / kSeg][i % kSeg] = 0u;
         __syncthreads();
-        for (int pi = tid; pi < T * segn; pi += 256) {
+        for (int pi = tid; pi < T * segn; pi += NTHR) {
             const int tau = pi / segn, cl = pi - (pi / segn) * segn;
             const int Gt = wk * T + tau;
             const int mt = Gt / Tb;
@@ -661,7 +674,7 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
         }
         __syncthreads();
         int U = 0;
-        for (int base = 0; base < segn; base += 256) {
+        for (int base = 0; base < segn; base += NTHR) {
             const int cl = base + tid;
             int any = 0;
             if (cl < segn) {
@@ -678,7 +691,7 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
             __syncthreads();
             int wbase = 0, tot = 0;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
+            for (int w = 0; w < NW; ++w) {
                 const int t = s_tmp[w];
                 if (w < wave) wbase += t;
                 tot += t;
@@ -693,7 +706,7 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
             const int c = seg0 + sList[u];
 #pragma unroll
             for (int i = 0; i < QLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int row = s / QSEG, sg = s - (s / QSEG) * QSEG;
                 const int t = 32 * c + row - a.q_pad;
                 const bool ok = s < 32 * QSEG && t >= 0 && t < a.N && sg * 8 < a.Dreal;
@@ -702,7 +715,7 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
             }
 #pragma unroll
             for (int i = 0; i < TLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int dr = s >> 2, sg = s & 3;
                 const bool ok = s < D * 4;
                 const int64_t off = (int64_t)dr * a.Npq + 32 * c + sg * 8;
@@ -719,7 +732,7 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
         auto store = [&](int buf) {
 #pragma unroll
             for (int i = 0; i < QLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 if (s < 32 * QSEG) {
                     const int row = s / QSEG, sg = s - (s / QSEG) * QSEG;
                     *reinterpret_cast<uint4*>(&sQ[buf][row * QROW + sg * 8]) = qst[i];
@@ -728,7 +741,7 @@ __global__ __launch_bounds__(256, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
             }
 #pragma unroll
             for (int i = 0; i < TLOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 if (s < D * 4) {
                     const int dr = s >> 2, sg = s & 3;
                     *reinterpret_cast<uint4*>(&sQt[buf][dr * TROW + sg * 8]) = qtst[i];
@@ -879,16 +892,16 @@ void fill_common(AttnArgs& a, int H, int N, int D, int g, int kvb, int qph, int 
 template <int DT>
 int launch_fwd_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
     switch (Dk) {
-#define FTA_FWD(DK, TPW)                                                                                  \
+#define FTA_FWD(DK, TPW, NW)                                                                              \
     case DK:                                                                                              \
-        hipLaunchKernelGGL((fta_sparse_fwd_kernel<DT, DK, TPW>), dim3(grid), dim3(256), 0, st, a);       \
+        hipLaunchKernelGGL((fta_sparse_fwd_kernel<DT, DK, TPW, NW>), dim3(grid), dim3(NW * 64), 0, st, a); \
         break;
-        FTA_FWD(32, 2)
-        FTA_FWD(64, 2)
-        FTA_FWD(96, 2)
-        FTA_FWD(128, 2)
-        FTA_FWD(160, 1)
-        FTA_FWD(256, 1)
+        FTA_FWD(32, 1, 8)
+        FTA_FWD(64, 1, 8)
+        FTA_FWD(96, 1, 8)
+        FTA_FWD(128, 1, 8)
+        FTA_FWD(160, 1, 8)
+        FTA_FWD(256, 1, 4)
 #undef FTA_FWD
         default:
             return fta::arg_error("sparse_attn: unsupported head dim");
@@ -899,16 +912,16 @@ int launch_fwd_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
 template <int DT>
 int launch_dq_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
     switch (Dk) {
-#define FTA_DQ(DK)                                                                                       \
+#define FTA_DQ(DK, NW)                                                                                  \
     case DK:                                                                                             \
-        hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, DK>), dim3(grid), dim3(256), 0, st, a);           \
+        hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, DK, NW>), dim3(grid), dim3(NW * 64), 0, st, a);     \
         break;
-        FTA_DQ(32)
-        FTA_DQ(64)
-        FTA_DQ(96)
-        FTA_DQ(128)
-        FTA_DQ(160)
-        FTA_DQ(256)
+        FTA_DQ(32, 8)
+        FTA_DQ(64, 8)
+        FTA_DQ(96, 8)
+        FTA_DQ(128, 8)
+        FTA_DQ(160, 4)
+        FTA_DQ(256, 4)
 #undef FTA_DQ
         default:
             return fta::arg_error("sparse_attn_bwd: unsupported head dim");
@@ -919,16 +932,16 @@ int launch_dq_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
 template <int DT>
 int launch_dkv_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
     switch (Dk) {
-#define FTA_DKV(DK)                                                                                      \
+#define FTA_DKV(DK, NW)                                                                                  \
     case DK:                                                                                             \
-        hipLaunchKernelGGL((fta_sparse_dkv_kernel<DT, DK>), dim3(grid), dim3(256), 0, st, a);          \
+        hipLaunchKernelGGL((fta_sparse_dkv_kernel<DT, DK, NW>), dim3(grid), dim3(NW * 64), 0, st, a);     \
         break;
-        FTA_DKV(32)
-        FTA_DKV(64)
-        FTA_DKV(96)
-        FTA_DKV(128)
-        FTA_DKV(160)
-        FTA_DKV(256)
+        FTA_DKV(32, 8)
+        FTA_DKV(64, 8)
+        FTA_DKV(96, 8)
+        FTA_DKV(128, 4)
+        FTA_DKV(160, 4)
+        FTA_DKV(256, 4)
 #undef FTA_DKV
         default:
             return fta::arg_error("sparse_attn_bwd: unsupported head dim");
@@ -988,7 +1001,7 @@ int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k, 
     a.o0_sn = o_strides[2];
     a.lse = lse;
     fill_common(a, H, N, D, q_block_size, kv_block_size, q_pad_head, kv_pad_head, scale, G);
-    const int T = (G.Dk <= 128) ? 8 : 4;
+    const int T = (G.Dk <= 160) ? 8 : 4;  // query tiles per workgroup
     a.wg_per_bh = (G.Npq + 32 * T - 1) / (32 * T);
     a.total = a.wg_per_bh * B * H;
     if (dtype == FTA_DTYPE_BF16) return launch_fwd_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);
@@ -1079,7 +1092,8 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, 
     a.o0_sb = dq_strides[0];
     a.o0_sh = dq_strides[1];
     a.o0_sn = dq_strides[2];
-    a.wg_per_bh = (G.Npq + 127) / 128;
+    const int Tq = (G.Dk <= 128) ? 8 : 4;  // query tiles per dQ workgroup
+    a.wg_per_bh = (G.Npq + 32 * Tq - 1) / (32 * Tq);
     a.total = a.wg_per_bh * B * H;
     if (dtype == FTA_DTYPE_BF16)
         rc = launch_dq_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);
@@ -1099,7 +1113,8 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, 
     a.o1_sh = dv_strides[1];
     a.o1_sn = dv_strides[2];
     const int ntiles = G.Mkv * ((kv_block_size + 31) / 32);
-    a.wg_per_bh = (ntiles + 3) / 4;
+    const int Tk = (G.Dk <= 96) ? 8 : 4;  // key tiles per dK/dV workgroup
+    a.wg_per_bh = (ntiles + Tk - 1) / Tk;
     a.total = a.wg_per_bh * B * H;
     if (dtype == FTA_DTYPE_BF16) return launch_dkv_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);
     return launch_dkv_dt<FTA_DTYPE_F16>(a, G.Dk, a.total, st);
