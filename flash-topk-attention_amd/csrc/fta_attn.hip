@@ -17,14 +17,13 @@
 //  * dK/dV walk the transposed membership (KV block -> q-blocks) directly, so no
 //    atomics are needed on the gradient path.
 //  * Operands that are contracted over tokens (V in P.V, K in dS.K, Q and dO in
-//    the dK/dV products) are read from token-transposed copies ("T layout"),
-//    keeping every MFMA operand load a contiguous 8/16-byte LDS read.
+//    the dK/dV products) are read from the same row-major LDS tiles with the
+//    gfx950 LDS transpose load (fta_tr_frag), so each token tile is gathered
+//    from HBM once and no transposed copies exist.
 #include "fta_common.h"
 #include "fta_host.h"
 
 namespace fta {
-int launch_transpose(const void* x, const int64_t* s, int B, int H, int N, int Dreal, int Dk, int Np, int pad,
-                     int blk_len, int blk_stride, void* out, hipStream_t st);
 int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint32_t* sel, hipStream_t st);
 }  // namespace fta
 
@@ -39,11 +38,6 @@ struct AttnArgs {
     int64_t v_sb, v_sh, v_sn;
     const uint16_t* dout;
     int64_t d_sb, d_sh, d_sn;
-    const uint16_t* kvT;  // T layout of V (forward) or K (dQ): [BH][Dk][Npk], block stride sbk
-    int Npk, sbk;
-    const uint16_t* qT;   // T layout of Q (dK/dV): [BH][Dk][Npq]
-    const uint16_t* doT;  // T layout of dO (dK/dV)
-    int Npq;
     const int32_t* merged;  // [BH][QM][W]
     const uint32_t* sel;    // [BH][Mkv][QW] membership bitmap (dK/dV)
     int QM, W, QW;
@@ -130,7 +124,8 @@ __device__ int fta_build_q_masks(const AttnArgs& a, int bh, int p0, int seg0, in
 
 // ----------------------------------------------------------------------------
 // Forward.  WG = 4 waves x TPW tiles x 32 queries.  For every union KV block,
-// 64-key chunks of K (row layout) and V (T layout) are double-buffered in LDS.
+// 64-key chunks of K and V (row layout) are double-buffered in LDS; V^T operands
+// come from LDS transpose reads.
 // Per tile: S^T = K Q^T (32 keys x 32 queries per MFMA), online softmax with a
 // lazily rescaled running max (rescale only when the max grows by > 2^8),
 // O^T += V^T P^T.
@@ -143,12 +138,10 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
     constexpr int KS = D / 16;
     constexpr int DT32 = D / 32;
     constexpr int KROW = D + 8;
-    constexpr int VROW = 64 + 8;
     constexpr int KSEG = D / 8;
     constexpr int KLOADS = (64 * KSEG + NTHR - 1) / NTHR;
-    constexpr int VLOADS = (D * 8 + NTHR - 1) / NTHR;
     __shared__ __align__(16) uint16_t sK[2][64 * KROW];
-    __shared__ __align__(16) uint16_t sV[2][D * VROW];
+    __shared__ __align__(16) uint16_t sV[2][64 * KROW];
     __shared__ uint32_t sMask[T][kSeg];
     __shared__ int sList[kSeg];
     __shared__ int s_tmp[8];
@@ -163,7 +156,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
 
     const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
     const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
-    const uint16_t* vtp = a.kvT + (int64_t)bh * D * a.Npk;
+    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
 
     uint4 qf[TPW][KS];
 #pragma unroll
@@ -193,7 +186,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
     }
 
     const int nch = (a.kvb + 63) >> 6;
-    uint4 kst[KLOADS], vst[VLOADS];
+    uint4 kst[KLOADS], vst[KLOADS];
 
     for (int seg0 = 0; seg0 < a.Mkv; seg0 += kSeg) {
         const int segn = min(kSeg, a.Mkv - seg0);
@@ -213,14 +206,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
                 const int t = kb + row;
                 const bool ok = s < 64 * KSEG && row < rem && t >= 0 && t < a.N && sg * 8 < a.Dreal;
                 kst[i] = ok ? *reinterpret_cast<const uint4*>(kp + (int64_t)t * a.k_sn + sg * 8) : fta_zero4();
-            }
-            const int pb = m * a.sbk + ch * 64;
-#pragma unroll
-            for (int i = 0; i < VLOADS; ++i) {
-                const int s = tid + i * NTHR;
-                const int dr = s >> 3, sg = s & 7;
-                vst[i] = (s < D * 8) ? *reinterpret_cast<const uint4*>(vtp + (int64_t)dr * a.Npk + pb + sg * 8)
-                                     : fta_zero4();
+                vst[i] = ok ? *reinterpret_cast<const uint4*>(vp + (int64_t)t * a.v_sn + sg * 8) : fta_zero4();
             }
         };
         auto store = [&](int buf) {
@@ -228,13 +214,10 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
             for (int i = 0; i < KLOADS; ++i) {
                 const int s = tid + i * NTHR;
                 const int row = s / KSEG, sg = s - (s / KSEG) * KSEG;
-                if (s < 64 * KSEG) *reinterpret_cast<uint4*>(&sK[buf][row * KROW + sg * 8]) = kst[i];
-            }
-#pragma unroll
-            for (int i = 0; i < VLOADS; ++i) {
-                const int s = tid + i * NTHR;
-                const int dr = s >> 3, sg = s & 7;
-                if (s < D * 8) *reinterpret_cast<uint4*>(&sV[buf][dr * VROW + sg * 8]) = vst[i];
+                if (s < 64 * KSEG) {
+                    *reinterpret_cast<uint4*>(&sK[buf][row * KROW + sg * 8]) = kst[i];
+                    *reinterpret_cast<uint4*>(&sV[buf][row * KROW + sg * 8]) = vst[i];
+                }
             }
         };
 
@@ -335,10 +318,8 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
                         if (ks >= nks) break;
 #pragma unroll
                         for (int dt = 0; dt < DT32; ++dt) {
-                            const uint16_t* vr = vbase + (dt * 32 + (lane & 31)) * VROW + ks * 16 + hf * 4;
-                            const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-                            const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
-                            oacc[tt][dt] = E::mma(make_uint4(lo.x, lo.y, hi.x, hi.y), pf[ks], oacc[tt][dt]);
+                            const uint4 vf = fta_tr_frag(vbase, KROW, ks * 16, dt * 32, lane);
+                            oacc[tt][dt] = E::mma(vf, pf[ks], oacc[tt][dt]);
                         }
                     }
                 }
@@ -388,13 +369,10 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
     constexpr int KS = D / 16;
     constexpr int DT32 = D / 32;
     constexpr int KROW = D + 8;
-    constexpr int VROW = 64 + 8;
     constexpr int KSEG = D / 8;
     constexpr int KLOADS = (64 * KSEG + NTHR - 1) / NTHR;
-    constexpr int TLOADS = (D * 8 + NTHR - 1) / NTHR;
     __shared__ __align__(16) uint16_t sK[NB][64 * KROW];
     __shared__ __align__(16) uint16_t sV[NB][64 * KROW];
-    __shared__ __align__(16) uint16_t sKt[NB][D * VROW];
     __shared__ uint32_t sMask[T][kSeg];
     __shared__ int sList[kSeg];
     __shared__ int s_tmp[8];
@@ -411,7 +389,6 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
     const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
     const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
     const uint16_t* dp = a.dout + b * a.d_sb + h * a.d_sh;
-    const uint16_t* ktp = a.kvT + (int64_t)bh * D * a.Npk;
 
     const int tq = p0 + 32 * wave + (lane & 31) - a.q_pad;
     const bool qok = tq >= 0 && tq < a.N;
@@ -437,7 +414,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
         for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
 
     const int nch = (a.kvb + 63) >> 6;
-    uint4 kst[KLOADS], vst[KLOADS], tst[TLOADS];
+    uint4 kst[KLOADS], vst[KLOADS];
 
     for (int seg0 = 0; seg0 < a.Mkv; seg0 += kSeg) {
         const int segn = min(kSeg, a.Mkv - seg0);
@@ -458,14 +435,6 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
                 kst[i] = ok ? *reinterpret_cast<const uint4*>(kp + (int64_t)t * a.k_sn + sg * 8) : fta_zero4();
                 vst[i] = ok ? *reinterpret_cast<const uint4*>(vp + (int64_t)t * a.v_sn + sg * 8) : fta_zero4();
             }
-            const int pb = m * a.sbk + ch * 64;
-#pragma unroll
-            for (int i = 0; i < TLOADS; ++i) {
-                const int s = tid + i * NTHR;
-                const int dr = s >> 3, sg = s & 7;
-                tst[i] = (s < D * 8) ? *reinterpret_cast<const uint4*>(ktp + (int64_t)dr * a.Npk + pb + sg * 8)
-                                     : fta_zero4();
-            }
         };
         auto store = [&](int buf) {
 #pragma unroll
@@ -476,12 +445,6 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
                     *reinterpret_cast<uint4*>(&sK[buf][row * KROW + sg * 8]) = kst[i];
                     *reinterpret_cast<uint4*>(&sV[buf][row * KROW + sg * 8]) = vst[i];
                 }
-            }
-#pragma unroll
-            for (int i = 0; i < TLOADS; ++i) {
-                const int s = tid + i * NTHR;
-                const int dr = s >> 3, sg = s & 7;
-                if (s < D * 8) *reinterpret_cast<uint4*>(&sKt[buf][dr * VROW + sg * 8]) = tst[i];
             }
         };
 
@@ -538,17 +501,14 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
                     dsf[ks] = make_uint4(E::pack2(dsv[0], dsv[1]), E::pack2(dsv[2], dsv[3]),
                                          E::pack2(dsv[4], dsv[5]), E::pack2(dsv[6], dsv[7]));
                 }
-                const uint16_t* tbase = &sKt[buf][0];
+                const uint16_t* tbase = &sK[buf][0];
                 const int nks = two ? 4 : 2;
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
                     if (ks >= nks) break;
 #pragma unroll
                     for (int dt = 0; dt < DT32; ++dt) {
-                        const uint16_t* tr = tbase + (dt * 32 + (lane & 31)) * VROW + ks * 16 + hf * 4;
-                        const uint2 lo = *reinterpret_cast<const uint2*>(tr);
-                        const uint2 hi = *reinterpret_cast<const uint2*>(tr + 8);
-                        acc[dt] = E::mma(make_uint4(lo.x, lo.y, hi.x, hi.y), dsf[ks], acc[dt]);
+                        acc[dt] = E::mma(fta_tr_frag(tbase, KROW, ks * 16, dt * 32, lane), dsf[ks], acc[dt]);
                     }
                 }
             }
@@ -589,14 +549,10 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
     constexpr int KS = D / 16;
     constexpr int DT32 = D / 32;
     constexpr int QROW = D + 8;
-    constexpr int TROW = 32 + 8;
     constexpr int QSEG = D / 8;
     constexpr int QLOADS = (32 * QSEG + NTHR - 1) / NTHR;
-    constexpr int TLOADS = (D * 4 + NTHR - 1) / NTHR;
     __shared__ __align__(16) uint16_t sQ[2][32 * QROW];
     __shared__ __align__(16) uint16_t sO[2][32 * QROW];
-    __shared__ __align__(16) uint16_t sQt[2][D * TROW];
-    __shared__ __align__(16) uint16_t sOt[2][D * TROW];
     __shared__ float sL[2][32];
     __shared__ float sDl[2][32];
     __shared__ uint32_t sMask[T][kSeg];
@@ -624,8 +580,6 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
     const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
     const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
     const uint16_t* dp = a.dout + b * a.d_sb + h * a.d_sh;
-    const uint16_t* qtp = a.qT + (int64_t)bh * D * a.Npq;
-    const uint16_t* dtp = a.doT + (int64_t)bh * D * a.Npq;
 
     uint4 kf[KS], vf[KS];
 #pragma unroll
@@ -644,7 +598,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
             dva[dt][i] = 0.f;
         }
 
-    uint4 qst[QLOADS], ost[QLOADS], qtst[TLOADS], otst[TLOADS];
+    uint4 qst[QLOADS], ost[QLOADS];
     float lst = 0.f, dst = 0.f;
     const int qw = a.QW;
 
@@ -713,15 +667,6 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
                 qst[i] = ok ? *reinterpret_cast<const uint4*>(qp + (int64_t)t * a.q_sn + sg * 8) : fta_zero4();
                 ost[i] = ok ? *reinterpret_cast<const uint4*>(dp + (int64_t)t * a.d_sn + sg * 8) : fta_zero4();
             }
-#pragma unroll
-            for (int i = 0; i < TLOADS; ++i) {
-                const int s = tid + i * NTHR;
-                const int dr = s >> 2, sg = s & 3;
-                const bool ok = s < D * 4;
-                const int64_t off = (int64_t)dr * a.Npq + 32 * c + sg * 8;
-                qtst[i] = ok ? *reinterpret_cast<const uint4*>(qtp + off) : fta_zero4();
-                otst[i] = ok ? *reinterpret_cast<const uint4*>(dtp + off) : fta_zero4();
-            }
             if (tid < 32) {
                 const int t = 32 * c + tid - a.q_pad;
                 const bool ok = t >= 0 && t < a.N;
@@ -737,15 +682,6 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
                     const int row = s / QSEG, sg = s - (s / QSEG) * QSEG;
                     *reinterpret_cast<uint4*>(&sQ[buf][row * QROW + sg * 8]) = qst[i];
                     *reinterpret_cast<uint4*>(&sO[buf][row * QROW + sg * 8]) = ost[i];
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < TLOADS; ++i) {
-                const int s = tid + i * NTHR;
-                if (s < D * 4) {
-                    const int dr = s >> 2, sg = s & 3;
-                    *reinterpret_cast<uint4*>(&sQt[buf][dr * TROW + sg * 8]) = qtst[i];
-                    *reinterpret_cast<uint4*>(&sOt[buf][dr * TROW + sg * 8]) = otst[i];
                 }
             }
             if (tid < 32) {
@@ -796,19 +732,12 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
                     dsf[ks] = make_uint4(E::pack2(dv8[0], dv8[1]), E::pack2(dv8[2], dv8[3]),
                                          E::pack2(dv8[4], dv8[5]), E::pack2(dv8[6], dv8[7]));
                 }
-                const uint16_t* qtb = &sQt[buf][0];
-                const uint16_t* otb = &sOt[buf][0];
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
                     for (int dt = 0; dt < DT32; ++dt) {
-                        const int off = (dt * 32 + (lane & 31)) * TROW + ks * 16 + hf * 4;
-                        const uint2 olo = *reinterpret_cast<const uint2*>(otb + off);
-                        const uint2 ohi = *reinterpret_cast<const uint2*>(otb + off + 8);
-                        dva[dt] = E::mma(pf[ks], make_uint4(olo.x, olo.y, ohi.x, ohi.y), dva[dt]);
-                        const uint2 qlo = *reinterpret_cast<const uint2*>(qtb + off);
-                        const uint2 qhi = *reinterpret_cast<const uint2*>(qtb + off + 8);
-                        dka[dt] = E::mma(dsf[ks], make_uint4(qlo.x, qlo.y, qhi.x, qhi.y), dka[dt]);
+                        dva[dt] = E::mma(pf[ks], fta_tr_frag(ob, QROW, ks * 16, dt * 32, lane), dva[dt]);
+                        dka[dt] = E::mma(dsf[ks], fta_tr_frag(qb, QROW, ks * 16, dt * 32, lane), dka[dt]);
                     }
                 }
             }
@@ -881,9 +810,6 @@ void fill_common(AttnArgs& a, int H, int N, int D, int g, int kvb, int qph, int 
     a.Mkv = G.Mkv;
     a.NC = G.NC;
     a.QM = G.QM;
-    a.Npk = G.Npk;
-    a.sbk = G.sbk;
-    a.Npq = G.Npq;
     a.QW = (G.QM + 31) / 32;
     a.scale = scale;
     a.c = scale * 1.4426950408889634f;
@@ -938,7 +864,7 @@ int launch_dkv_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
         break;
         FTA_DKV(32, 8)
         FTA_DKV(64, 8)
-        FTA_DKV(96, 8)
+        FTA_DKV(96, 4)
         FTA_DKV(128, 4)
         FTA_DKV(160, 4)
         FTA_DKV(256, 4)
@@ -949,7 +875,9 @@ int launch_dkv_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
     return fta::check_launch("fta_sparse_dkv_kernel");
 }
 
-size_t t_bytes(int B, int H, int Dk, int Np) { return fta::align_up((size_t)B * H * Dk * Np * sizeof(uint16_t)); }
+size_t sel_bytes(int B, int H, const Geo& G) {
+    return fta::align_up((size_t)B * H * G.Mkv * ((G.QM + 31) / 32) * sizeof(uint32_t));
+}
 
 }  // namespace
 
@@ -963,7 +891,7 @@ size_t fta_sparse_attn_fwd_workspace_size(int B, int H, int N, int D, int q_bloc
     if (geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
                  &G) != FTA_OK)
         return 0;
-    return t_bytes(B, H, G.Dk, G.Npk);
+    return 0;  // the forward needs no scratch
 }
 
 int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -978,11 +906,9 @@ int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k, 
                       &G);
     if (rc != FTA_OK) return rc;
     if (W <= 0) return fta::arg_error("sparse_attn: qblock_topk must be positive");
-    if (workspace_bytes < t_bytes(B, H, G.Dk, G.Npk)) return fta::arg_error("sparse_attn: workspace too small");
+    (void)workspace;
+    (void)workspace_bytes;
     hipStream_t st = (hipStream_t)stream;
-    rc = fta::launch_transpose(v, v_strides, B, H, N, D, G.Dk, G.Npk, kv_pad_head, kv_block_size, G.sbk, workspace,
-                               st);
-    if (rc != FTA_OK) return rc;
     AttnArgs a = {};
     a.q = (const uint16_t*)q;
     a.q_sb = q_strides[0];
@@ -992,7 +918,10 @@ int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k, 
     a.k_sb = k_strides[0];
     a.k_sh = k_strides[1];
     a.k_sn = k_strides[2];
-    a.kvT = (const uint16_t*)workspace;
+    a.v = (const uint16_t*)v;
+    a.v_sb = v_strides[0];
+    a.v_sh = v_strides[1];
+    a.v_sn = v_strides[2];
     a.merged = merged_indices;
     a.W = W;
     a.out0 = (uint16_t*)o;
@@ -1018,10 +947,7 @@ size_t fta_sparse_attn_bwd_workspace_size(int B, int H, int N, int D, int q_bloc
     if (geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
                  &G) != FTA_OK)
         return 0;
-    const size_t kt = t_bytes(B, H, G.Dk, G.Npk);
-    const size_t qt = t_bytes(B, H, G.Dk, G.Npq);
-    const size_t sel = fta::align_up((size_t)B * H * G.Mkv * ((QM + 31) / 32) * sizeof(uint32_t));
-    return kt + 2 * qt + sel;
+    return sel_bytes(B, H, G);  // membership bitmap KV block -> q-blocks
 }
 
 int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -1038,26 +964,9 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, 
     if (rc != FTA_OK) return rc;
     if (W <= 0) return fta::arg_error("sparse_attn_bwd: qblock_topk must be positive");
     if (G.Mkv > 0x3fffffff / 32) return fta::unsupported("sparse_attn_bwd: too many KV blocks");
-    const size_t kt = t_bytes(B, H, G.Dk, G.Npk);
-    const size_t qt = t_bytes(B, H, G.Dk, G.Npq);
-    if (workspace_bytes < fta_sparse_attn_bwd_workspace_size(B, H, N, D, q_block_size, kv_block_size, q_pad_head,
-                                                              q_pad_tail, kv_pad_head, kv_pad_tail))
-        return fta::arg_error("sparse_attn_bwd: workspace too small");
+    if (workspace_bytes < sel_bytes(B, H, G)) return fta::arg_error("sparse_attn_bwd: workspace too small");
     hipStream_t st = (hipStream_t)stream;
-    char* ws = (char*)workspace;
-    void* ktb = ws;
-    void* qtb = ws + kt;
-    void* dotb = ws + kt + qt;
-    uint32_t* sel = (uint32_t*)(ws + kt + 2 * qt);
-    if ((rc = fta::launch_transpose(k, k_strides, B, H, N, D, G.Dk, G.Npk, kv_pad_head, kv_block_size, G.sbk, ktb,
-                                    st)) != FTA_OK)
-        return rc;
-    if ((rc = fta::launch_transpose(q, q_strides, B, H, N, D, G.Dk, G.Npq, q_pad_head, G.Npq, G.Npq, qtb, st)) !=
-        FTA_OK)
-        return rc;
-    if ((rc = fta::launch_transpose(dout, do_strides, B, H, N, D, G.Dk, G.Npq, q_pad_head, G.Npq, G.Npq, dotb,
-                                    st)) != FTA_OK)
-        return rc;
+    uint32_t* sel = (uint32_t*)workspace;
     if ((rc = fta::launch_sel_bitmap(merged_indices, B * H, QM, W, G.Mkv, sel, st)) != FTA_OK) return rc;
 
     AttnArgs a = {};
@@ -1077,9 +986,6 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, 
     a.d_sb = do_strides[0];
     a.d_sh = do_strides[1];
     a.d_sn = do_strides[2];
-    a.kvT = (const uint16_t*)ktb;
-    a.qT = (const uint16_t*)qtb;
-    a.doT = (const uint16_t*)dotb;
     a.merged = merged_indices;
     a.sel = sel;
     a.W = W;
@@ -1113,7 +1019,7 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, 
     a.o1_sh = dv_strides[1];
     a.o1_sn = dv_strides[2];
     const int ntiles = G.Mkv * ((kv_block_size + 31) / 32);
-    const int Tk = (G.Dk <= 96) ? 8 : 4;  // key tiles per dK/dV workgroup
+    const int Tk = (G.Dk <= 64) ? 8 : 4;  // key tiles per dK/dV workgroup
     a.wg_per_bh = (ntiles + Tk - 1) / Tk;
     a.total = a.wg_per_bh * B * H;
     if (dtype == FTA_DTYPE_BF16) return launch_dkv_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);

@@ -8,10 +8,9 @@
 //                           (i >> 2) * 8 + (l >> 5) * 4 + (i & 3), i = 0..15
 //    Any permutation of k that is applied identically to A and B is harmless,
 //    which the P.V and dS.K products use to consume C-layout registers directly.
-//  * Attention operands are laid out so that both MFMA operands are contiguous
-//    along the contraction dimension: row-major [token][d] for QK^T-type
-//    products and transposed [d][token] copies ("T layout", padded token
-//    coordinates) for products that contract over tokens.
+//  * Token tiles are staged row-major ([token][d]) in LDS.  QK^T-type products
+//    read them with plain 16-byte LDS loads; products that contract over tokens
+//    read the same tiles transposed with fta_tr_frag (ds_read_b64_tr_b16).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -83,6 +82,32 @@ __device__ __forceinline__ int fta_xcd_remap(int hw_id, int total) {
 }
 
 __device__ __forceinline__ uint4 fta_zero4() { return make_uint4(0u, 0u, 0u, 0u); }
+
+// MFMA operand (A or B format) whose k index runs down the ROWS of a row-major
+// LDS tile, read with the gfx950 LDS transpose load ds_read_b64_tr_b16:
+//   element e of lane l = tile[(k0 + kperm(l, e)) * row + n0 + (l & 31)],
+//   kperm(l, e) = 8 * (e >> 2) + 4 * (l >> 5) + (e & 3)
+// (the same k permutation as the rows of the 32x32 C layout, so C-layout
+// registers can be contracted against it directly).
+// ds_read_b64_tr_b16 semantics (per 16-lane group, measured on gfx950): lane j
+// receives element (j & 3) of the 64-bit words addressed by lanes
+// 4e + (j >> 2), e = 0..3.  Lane i of a group therefore addresses row
+// (i >> 2) and columns 4 * (i & 3) .. +3 of a 4 x 16 sub-block.
+typedef short fta_s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) fta_s16x4 fta_lds_s16x4;
+__device__ __forceinline__ uint4 fta_tr_frag(const uint16_t* tile, int row, int k0, int n0, int lane) {
+    const int g = lane >> 4, i = lane & 15;
+    const int r = k0 + 4 * (g >> 1) + (i >> 2);
+    const int col = n0 + 16 * (g & 1) + 4 * (i & 3);
+    const uint16_t* p0 = tile + r * row + col;
+    const uint16_t* p1 = p0 + 8 * row;
+    const fta_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (fta_lds_s16x4*)(__attribute__((address_space(3))) uint16_t*)p0);
+    const fta_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (fta_lds_s16x4*)(__attribute__((address_space(3))) uint16_t*)p1);
+    const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+    return make_uint4(l2.x, l2.y, h2.x, h2.y);
+}
 
 // Status codes returned by every extern "C" entry point (see include/fta.h).
 #define FTA_OK 0

@@ -1,5 +1,4 @@
-// Index kernels: q-block merge, reverse index, count sorts, delta and the
-// token-transposed ("T layout") copies used by the attention kernels.
+// Index kernels: q-block merge, reverse index, count sorts and delta.
 //
 // All of them are deterministic: sums run in a fixed order and no result
 // depends on atomic ordering (the reference's merge and reverse-index kernels,
@@ -261,54 +260,7 @@ __global__ __launch_bounds__(256) void fta_delta_kernel(const uint16_t* __restri
     delta[((int64_t)b * H + h) * N + n] = acc;
 }
 
-// ----------------------------------------------------------------------------
-// T layout: out[bh][d][p'] for a token-blocked column space: column p' lies in
-// block m = p' / blk_stride at offset r = p' % blk_stride and holds token
-// t = m * blk_len + r - pad when r < blk_len and 0 <= t < N, else 0.
-// (blk_len = blk_stride gives plain padded coordinates p' = t + pad; a stride
-// rounded up to 64 keeps every KV block 64-aligned for any block size.)
-// d < Dk (zero for d >= Dreal).  64 x 64 tiles through LDS.
-// ----------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void fta_transpose_kernel(const uint16_t* __restrict__ x, int64_t sb, int64_t sh,
-                                                            int64_t sn, int H, int N, int Dreal, int Dk, int Np,
-                                                            int pad, int blk_len, int blk_stride, int ntp, int ntd,
-                                                            uint16_t* __restrict__ out) {
-    __shared__ uint16_t tile[64][66];
-    const int per = ntp * ntd;
-    const int bh = blockIdx.x / per;
-    const int r = blockIdx.x - bh * per;
-    const int tp = r / ntd, td = r - (r / ntd) * ntd;
-    const int b = bh / H, h = bh - (bh / H) * H;
-    const int p0 = tp * 64, d0 = td * 64;
-    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-    const uint16_t* xp = x + b * sb + h * sh;
-    for (int pp = ty; pp < 64; pp += 4) {
-        const int pc = p0 + pp;
-        const int m = pc / blk_stride, rr = pc - (pc / blk_stride) * blk_stride;
-        const int t = m * blk_len + rr - pad, d = d0 + tx;
-        uint16_t v = 0;
-        if (rr < blk_len && t >= 0 && t < N && d < Dreal) v = xp[(int64_t)t * sn + d];
-        tile[pp][tx] = v;
-    }
-    __syncthreads();
-    uint16_t* op = out + (int64_t)bh * Dk * Np;
-    for (int dd = ty; dd < 64; dd += 4) {
-        const int d = d0 + dd, pc = p0 + tx;
-        if (d < Dk && pc < Np) op[(int64_t)d * Np + pc] = tile[tx][dd];
-    }
-}
-
 namespace fta {
-int launch_transpose(const void* x, const int64_t* s, int B, int H, int N, int Dreal, int Dk, int Np, int pad,
-                     int blk_len, int blk_stride, void* out, hipStream_t st) {
-    const int ntp = (Np + 63) / 64, ntd = (Dk + 63) / 64;
-    const int64_t grid = (int64_t)B * H * ntp * ntd;
-    if (grid > 0)
-        hipLaunchKernelGGL(fta_transpose_kernel, dim3((unsigned)grid), dim3(256), 0, st, (const uint16_t*)x, s[0],
-                           s[1], s[2], H, N, Dreal, Dk, Np, pad, blk_len, blk_stride, ntp, ntd, (uint16_t*)out);
-    return check_launch("fta_transpose_kernel");
-}
-
 int launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t st) {
     if (n <= 0) return FTA_OK;
     int64_t blocks = (n + 255) / 256;

@@ -32,8 +32,9 @@ template <int DT, int D>
 __global__ __launch_bounds__(256, 2) void fta_block_score_lse_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
-    int H, int N, int Dreal, int M, int bsz, int pad_head, float c,
-    float* __restrict__ blk_lse, float* __restrict__ row_lse, int qtiles, int total) {
+    int H, int N, int Dreal, int M, int bsz, int pad_head, int pad_tail, float c,
+    float* __restrict__ blk_lse, float* __restrict__ row_lse, int qtiles, int total, int kgroups,
+    int32_t* __restrict__ tau_idx) {
     using E = Elem<DT>;
     constexpr int KS = D / 16;
     constexpr int ROW = D + 8;  // +16 B per LDS row against bank conflicts
@@ -91,6 +92,13 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_kernel(
 
     float m_run[2] = {-FTA_INF, -FTA_INF}, L_run[2] = {0.f, 0.f};
     float mb[2] = {-FTA_INF, -FTA_INF}, lb[2] = {0.f, 0.f};
+    // Lower bound for the top-k selector: split the M blocks into kgroups
+    // groups, keep each group's best block (by log2 average mass) and the worst
+    // of those group maxima -- at least kgroups blocks are at least that good.
+    float gkey = -FTA_INF, tkey = FTA_INF;
+    int gidx = 0, tidx = 0, curg = -1;
+    const float adj_head = (pad_head > 0) ? fta_log2((float)bsz / (float)(bsz - pad_head)) : 0.f;
+    const float adj_tail = (pad_tail > 0) ? fta_log2((float)bsz / (float)(bsz - pad_tail)) : 0.f;
 
     load_chunk(0);
     store_chunk(0);
@@ -182,7 +190,26 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_kernel(
                 }
             }
             const int qi = qbase + lane;
-            if (qi < N) blk_lse[((int64_t)bh * M + m) * N + qi] = (lane < 32) ? lse_b[0] : lse_b[1];
+            const float mine = (lane < 32) ? lse_b[0] : lse_b[1];
+            if (qi < N) blk_lse[((int64_t)bh * M + m) * N + qi] = mine;
+            if (kgroups > 0) {
+                const int gm = (int)(((int64_t)m * kgroups) / M);
+                float key = mine;
+                if (m == 0) key += adj_head;
+                if (m == M - 1) key += adj_tail;
+                if (gm != curg) {
+                    if (curg >= 0 && gkey < tkey) {
+                        tkey = gkey;
+                        tidx = gidx;
+                    }
+                    curg = gm;
+                    gkey = key;
+                    gidx = m;
+                } else if (key > gkey) {
+                    gkey = key;
+                    gidx = m;
+                }
+            }
         }
 
         if (it + 1 < total_it) store_chunk(buf ^ 1);
@@ -195,6 +222,10 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_kernel(
         const float mr = (t == 0) ? m_run[0] : m_run[1];
         const float Lr = (t == 0) ? L_run[0] : L_run[1];
         row_lse[(int64_t)bh * N + qi] = (Lr > 0.f) ? fmaf(mr, c, fta_log2(Lr)) : -FTA_INF;
+        if (kgroups > 0) {
+            if (curg >= 0 && gkey < tkey) tidx = gidx;
+            tau_idx[(int64_t)bh * N + qi] = tidx;
+        }
     }
 }
 
@@ -249,8 +280,9 @@ template <int KB, int MODE>
 __global__ __launch_bounds__(256) void fta_topk_select_kernel(
     const float* __restrict__ in, int64_t stride_row, int64_t stride_m, const float* __restrict__ row_lse,
     int N, int rows, int M, int m_out, int bsz, int pad_head, int pad_tail, float threshold,
-    int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg) {
-    constexpr int CAP = 32;
+    int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg,
+    const int32_t* __restrict__ tau_idx) {
+    constexpr int CAP = 16;
     __shared__ float cand_v[4][CAP][64];
     __shared__ int cand_i[4][CAP][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -280,8 +312,28 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
         rl = row_lse[active ? row : 0];
     }
 
+    // Raw-score pre-filter: a block can only beat tau if raw >= tau * vc; the
+    // bound is relaxed by 2^-20 relative so that the exact (avg, index) test
+    // below decides every candidate.
+    float thr_norm = -FTA_INF;
+    auto set_thr = [&]() {
+        const float t = tv * (float)bsz;
+        thr_norm = t - fabsf(t) * 9.5367431640625e-07f;
+    };
+    if (MODE == 1 && tau_idx != nullptr && active) {
+        const int t0 = tau_idx[row];
+        const float rt = fta_exp2(src[(int64_t)t0 * N] - rl);
+        const float at = rt / (float)fta_valid_count(t0, M, bsz, pad_head, pad_tail);
+        tv = at - fabsf(at) * 1.52587890625e-05f;  // at least m_out blocks have avg >= this
+        ti = 0x7fffffff;
+    }
+    set_thr();
+
     auto flush = [&]() {
-        for (int j = 0; j < CAP; ++j) {
+        int mc = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) mc = max(mc, __shfl_xor(mc, off, 64));
+        for (int j = 0; j < mc; ++j) {
             const bool ok = j < cnt;
             const float v = ok ? cand_v[wave][j][lane] : -FTA_INF;
             const int id = ok ? cand_i[wave][j][lane] : 0x7fffffff;
@@ -303,10 +355,11 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
         cnt = 0;
 #pragma unroll
         for (int p = 0; p < KB; ++p)
-            if (p == m_out - 1) {
+            if (p == m_out - 1 && li[p] != 0x7fffffff) {
                 tv = lv[p];
                 ti = li[p];
             }
+        set_thr();
     };
 
     for (int m = 0; m < M; ++m) {
@@ -316,11 +369,14 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
         } else {
             raw = active ? fta_exp2(src[(int64_t)m * N] - rl) : 0.f;
         }
-        const float avg = raw / (float)fta_valid_count(m, M, bsz, pad_head, pad_tail);
-        if (active && fta_better(avg, m, tv, ti)) {
-            cand_v[wave][cnt][lane] = avg;
-            cand_i[wave][cnt][lane] = m;
-            ++cnt;
+        const bool edge = (m == 0 && pad_head > 0) || (m == M - 1 && pad_tail > 0);
+        if (active && (raw >= thr_norm || edge)) {
+            const float avg = raw / (float)fta_valid_count(m, M, bsz, pad_head, pad_tail);
+            if (fta_better(avg, m, tv, ti)) {
+                cand_v[wave][cnt][lane] = avg;
+                cand_i[wave][cnt][lane] = m;
+                ++cnt;
+            }
         }
         if (__ballot(cnt == CAP) != 0ull) flush();
     }
@@ -443,15 +499,15 @@ namespace {
 
 template <int DT>
 int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D, int Dk, const int64_t* qs,
-                        const int64_t* ks, int M, int bsz, int pad_head, float scale, float* blk_lse,
-                        float* row_lse, hipStream_t st) {
+                        const int64_t* ks, int M, int bsz, int pad_head, int pad_tail, float scale,
+                        float* blk_lse, float* row_lse, int kgroups, int32_t* tau, hipStream_t st) {
     const int qtiles = (N + 255) / 256;
     const int total = qtiles * B * H;
     const float c = scale * 1.4426950408889634f;
 #define FTA_LAUNCH_SCORE(DK)                                                                               \
     hipLaunchKernelGGL((fta_block_score_lse_kernel<DT, DK>), dim3(total), dim3(256), 0, st,                \
                        (const uint16_t*)q, (const uint16_t*)k, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], H, N, \
-                       D, M, bsz, pad_head, c, blk_lse, row_lse, qtiles, total)
+                       D, M, bsz, pad_head, pad_tail, c, blk_lse, row_lse, qtiles, total, kgroups, tau)
     switch (Dk) {
         case 32: FTA_LAUNCH_SCORE(32); break;
         case 64: FTA_LAUNCH_SCORE(64); break;
@@ -466,30 +522,30 @@ int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D
 }
 
 int launch_score_lse(const void* q, const void* k, int dtype, int B, int H, int N, int D, const int64_t* qs,
-                     const int64_t* ks, int M, int bsz, int pad_head, float scale, float* blk_lse, float* row_lse,
-                     hipStream_t st) {
+                     const int64_t* ks, int M, int bsz, int pad_head, int pad_tail, float scale, float* blk_lse,
+                     float* row_lse, int kgroups, int32_t* tau, hipStream_t st) {
     const int Dk = fta::kernel_head_dim(D);
     if (Dk < 0) return fta::arg_error("block_score: head dim must be <= 256");
     if (D % 8 != 0) return fta::arg_error("block_score: head dim must be a multiple of 8");
     if (dtype == FTA_DTYPE_BF16)
-        return launch_score_lse_dt<FTA_DTYPE_BF16>(q, k, B, H, N, D, Dk, qs, ks, M, bsz, pad_head, scale, blk_lse,
-                                                   row_lse, st);
+        return launch_score_lse_dt<FTA_DTYPE_BF16>(q, k, B, H, N, D, Dk, qs, ks, M, bsz, pad_head, pad_tail, scale,
+                                                   blk_lse, row_lse, kgroups, tau, st);
     if (dtype == FTA_DTYPE_F16)
-        return launch_score_lse_dt<FTA_DTYPE_F16>(q, k, B, H, N, D, Dk, qs, ks, M, bsz, pad_head, scale, blk_lse,
-                                                  row_lse, st);
+        return launch_score_lse_dt<FTA_DTYPE_F16>(q, k, B, H, N, D, Dk, qs, ks, M, bsz, pad_head, pad_tail, scale,
+                                                  blk_lse, row_lse, kgroups, tau, st);
     return fta::arg_error("block_score: dtype must be bf16 or fp16");
 }
 
 template <int MODE>
 int launch_topk(const float* in, int64_t stride_row, int64_t stride_m, const float* row_lse, int N, int rows,
                 int M, int m_out, int bsz, int pad_head, int pad_tail, float threshold, int32_t* idx, float* raw,
-                float* avg, hipStream_t st) {
+                float* avg, const int32_t* tau, hipStream_t st) {
     if (rows == 0) return FTA_OK;
     if (m_out <= 64) {
         const int grid = (rows + 255) / 256;
 #define FTA_LAUNCH_TOPK(KB)                                                                                \
     hipLaunchKernelGGL((fta_topk_select_kernel<KB, MODE>), dim3(grid), dim3(256), 0, st, in, stride_row,   \
-                       stride_m, row_lse, N, rows, M, m_out, bsz, pad_head, pad_tail, threshold, idx, raw, avg)
+                       stride_m, row_lse, N, rows, M, m_out, bsz, pad_head, pad_tail, threshold, idx, raw, avg, tau)
         if (m_out <= 8)
             FTA_LAUNCH_TOPK(8);
         else if (m_out <= 16)
@@ -518,8 +574,8 @@ int fta_block_score_lse(const void* q, const void* k, int dtype, int B, int H, i
     int st = fta::check_score_args(B, H, N, D, score_block_size, pad_head, pad_tail, &M);
     if (st != FTA_OK) return st;
     if (!q || !k || !blk_lse || !row_lse) return fta::arg_error("block_score_lse: null pointer");
-    return launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, scale,
-                            blk_lse, row_lse, (hipStream_t)stream);
+    return launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, pad_tail,
+                            scale, blk_lse, row_lse, 0, nullptr, (hipStream_t)stream);
     FTA_TRY_END
 }
 
@@ -540,8 +596,8 @@ int fta_block_score(const void* q, const void* k, int dtype, int B, int H, int N
     float* blk_lse = (float*)workspace;
     float* row_lse = (float*)((char*)workspace + fta::align_up((size_t)B * H * M * N * sizeof(float)));
     hipStream_t s = (hipStream_t)stream;
-    st = launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, scale,
-                          blk_lse, row_lse, s);
+    st = launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, pad_tail,
+                          scale, blk_lse, row_lse, 0, nullptr, s);
     if (st != FTA_OK) return st;
     const int tn = (N + 63) / 64, tm = (M + 63) / 64;
     if ((int64_t)B * H * tn * tm > 0) {
@@ -565,11 +621,13 @@ int fta_topk_select(const float* block_scores, int64_t rows, int M, int64_t stri
     if (rows < 0 || rows > 0x7fffffff) return fta::arg_error("topk_select: bad row count");
     const int m_out = (max_topk > 0 && max_topk < M) ? max_topk : M;
     return launch_topk<0>(block_scores, stride_row, stride_m, nullptr, 1, (int)rows, M, m_out, score_block_size,
-                          pad_head, pad_tail, threshold, topk_indices, topk_raw, topk_avg, (hipStream_t)stream);
+                          pad_head, pad_tail, threshold, topk_indices, topk_raw, topk_avg, nullptr, (hipStream_t)stream);
     FTA_TRY_END
 }
 
-size_t fta_topk_score_workspace_size(int B, int H, int N, int M) { return fta_block_score_workspace_size(B, H, N, M); }
+size_t fta_topk_score_workspace_size(int B, int H, int N, int M) {
+    return fta_block_score_workspace_size(B, H, N, M) + fta::align_up((size_t)B * H * N * sizeof(int32_t));
+}
 
 int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N, int D, const int64_t* q_strides,
                    const int64_t* k_strides, int score_block_size, int pad_head, int pad_tail, float scale,
@@ -586,12 +644,14 @@ int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N,
     float* blk_lse = (float*)workspace;
     float* row_lse = (float*)((char*)workspace + fta::align_up((size_t)B * H * M * N * sizeof(float)));
     hipStream_t s = (hipStream_t)stream;
-    st = launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, scale,
-                          blk_lse, row_lse, s);
-    if (st != FTA_OK) return st;
+    int32_t* tau = (int32_t*)((char*)workspace + fta_block_score_workspace_size(B, H, N, M));
     const int m_out = (max_topk > 0 && max_topk < M) ? max_topk : M;
+    const int kgroups = (m_out <= 64) ? m_out : 0;
+    st = launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, pad_tail,
+                          scale, blk_lse, row_lse, kgroups, tau, s);
+    if (st != FTA_OK) return st;
     return launch_topk<1>(blk_lse, 0, 0, row_lse, N, B * H * N, M, m_out, score_block_size, pad_head, pad_tail,
-                          threshold, topk_indices, topk_raw, topk_avg, s);
+                          threshold, topk_indices, topk_raw, topk_avg, kgroups ? tau : nullptr, s);
     FTA_TRY_END
 }
 
