@@ -29,7 +29,7 @@
 // in-lane plus one exchange with lane ^ 32.
 // ----------------------------------------------------------------------------
 template <int DT, int D>
-__global__ __launch_bounds__(256, 2) void fta_block_score_lse_kernel(
+__global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
     int H, int N, int Dreal, int M, int bsz, int pad_head, int pad_tail, float c,
@@ -222,6 +222,244 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_kernel(
         const float mr = (t == 0) ? m_run[0] : m_run[1];
         const float Lr = (t == 0) ? L_run[0] : L_run[1];
         row_lse[(int64_t)bh * N + qi] = (Lr > 0.f) ? fmaf(mr, c, fta_log2(Lr)) : -FTA_INF;
+        if (kgroups > 0) {
+            if (curg >= 0 && gkey < tkey) tidx = gidx;
+            tau_idx[(int64_t)bh * N + qi] = tidx;
+        }
+    }
+}
+
+
+// Sum of 2^{c v_i - r} over n values: all exps are issued before any add and the
+// adds form a tree, so no add waits on the exp issued just before it.
+template <int NV>
+__device__ __forceinline__ float fta_sum_exp2(const float* v, float c, float r) {
+    float e[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) e[i] = fta_exp2(fmaf(v[i], c, -r));
+#pragma unroll
+    for (int w = 1; w < NV; w <<= 1)
+#pragma unroll
+        for (int i = 0; i + w < NV; i += 2 * w) e[i] += e[i + w];
+    return e[0];
+}
+// ----------------------------------------------------------------------------
+// Stage 1, blocks of at most 64 keys (one LDS chunk per block).  Same tiling
+// as above, but the per-block max pass is replaced by a running per-row log2
+// reference R: p = 2^{c s - R}, block total = exchange of two lane halves.
+// R starts at -inf, which makes the first block take the exact path (per-block
+// max, as above); it is re-based onto a block's log-sum whenever a block
+// total exceeds 2^40, and any non-finite or > 2^100 total (a logit more than
+// ~100/c above the reference) recomputes that block exactly.  Blocks far below
+// R lose mass to underflow only when they sit more than 2^-126 below R, i.e.
+// when their score is below fp32 resolution anyway.
+// ----------------------------------------------------------------------------
+template <int DT, int D>
+__global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fast_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+    int H, int N, int Dreal, int M, int bsz, int pad_head, int pad_tail, float c,
+    float* __restrict__ blk_lse, float* __restrict__ row_lse, int qtiles, int total, int kgroups,
+    int32_t* __restrict__ tau_idx) {
+    using E = Elem<DT>;
+    constexpr int KS = D / 16;
+    constexpr int ROW = D + 8;
+    constexpr int SEGS = D / 8;
+    constexpr int LOADS = (64 * SEGS) / 256;
+    static_assert((64 * SEGS) % 256 == 0, "D must be a multiple of 32");
+    __shared__ __align__(16) uint16_t sk[2][64 * ROW];
+
+    const int wg = fta_xcd_remap(blockIdx.x, total);
+    const int bh = wg / qtiles;
+    const int qt = wg - bh * qtiles;
+    const int b = bh / H, h = bh - (bh / H) * H;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int qbase = qt * 256 + wave * 64;
+    const uint16_t* qp = q + b * q_sb + h * q_sh;
+    const uint16_t* kp = k + b * k_sb + h * k_sh;
+
+    uint4 qf[2][KS];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int qi = qbase + t * 32 + (lane & 31);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d = ks * 16 + (lane >> 5) * 8;
+            qf[t][ks] = (qi < N && d < Dreal) ? *reinterpret_cast<const uint4*>(qp + (int64_t)qi * q_sn + d)
+                                              : fta_zero4();
+        }
+    }
+
+    uint4 stage[LOADS];
+    auto load_block = [&](int m) {
+        const int kb = m * bsz - pad_head;
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int s = tid + i * 256;
+            const int row = s / SEGS, seg = s - (s / SEGS) * SEGS;
+            const int t = kb + row;
+            const bool ok = row < bsz && t >= 0 && t < N && seg * 8 < Dreal;
+            stage[i] = ok ? *reinterpret_cast<const uint4*>(kp + (int64_t)t * k_sn + seg * 8) : fta_zero4();
+        }
+    };
+    auto store_block = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int s = tid + i * 256;
+            const int row = s / SEGS, seg = s - (s / SEGS) * SEGS;
+            *reinterpret_cast<uint4*>(&sk[buf][row * ROW + seg * 8]) = stage[i];
+        }
+    };
+
+    float R[2] = {-FTA_INF, -FTA_INF}, L[2] = {0.f, 0.f};
+    float gkey = -FTA_INF, tkey = FTA_INF;
+    int gidx = 0, tidx = 0, curg = -1, next_start = 0;
+    const float adj_head = (pad_head > 0) ? fta_log2((float)bsz / (float)(bsz - pad_head)) : 0.f;
+    const float adj_tail = (pad_tail > 0) ? fta_log2((float)bsz / (float)(bsz - pad_tail)) : 0.f;
+    const bool two = bsz > 32;
+    const int kr0 = (lane & 31) * ROW + (lane >> 5) * 8;
+
+    load_block(0);
+    store_block(0);
+    __syncthreads();
+
+    for (int m = 0; m < M; ++m) {
+        const int buf = m & 1;
+        if (m + 1 < M) load_block(m + 1);
+        const int kb = m * bsz - pad_head;
+
+        f32x16 acc[2][2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[s][t][i] = 0.f;
+        const uint16_t* base = &sk[buf][0];
+        if (two) {
+            uint4 a0 = *reinterpret_cast<const uint4*>(base + kr0);
+            uint4 a1 = *reinterpret_cast<const uint4*>(base + kr0 + 32 * ROW);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                uint4 n0 = a0, n1 = a1;
+                if (ks + 1 < KS) {
+                    n0 = *reinterpret_cast<const uint4*>(base + kr0 + (ks + 1) * 16);
+                    n1 = *reinterpret_cast<const uint4*>(base + kr0 + 32 * ROW + (ks + 1) * 16);
+                }
+                acc[0][0] = E::mma(a0, qf[0][ks], acc[0][0]);
+                acc[0][1] = E::mma(a0, qf[1][ks], acc[0][1]);
+                acc[1][0] = E::mma(a1, qf[0][ks], acc[1][0]);
+                acc[1][1] = E::mma(a1, qf[1][ks], acc[1][1]);
+                a0 = n0;
+                a1 = n1;
+            }
+        } else {
+            uint4 a0 = *reinterpret_cast<const uint4*>(base + kr0);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                uint4 n0 = a0;
+                if (ks + 1 < KS) n0 = *reinterpret_cast<const uint4*>(base + kr0 + (ks + 1) * 16);
+                acc[0][0] = E::mma(a0, qf[0][ks], acc[0][0]);
+                acc[0][1] = E::mma(a0, qf[1][ks], acc[0][1]);
+                a0 = n0;
+            }
+        }
+
+        if (kb < 0 || kb + 64 > N || bsz < 64) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int rel = s * 32 + c_row(i, lane);
+                    const int t = kb + rel;
+                    if (rel >= bsz || t < 0 || t >= N) {
+                        acc[s][0][i] = -FTA_INF;
+                        acc[s][1][i] = -FTA_INF;
+                    }
+                }
+        }
+
+        float tot[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            float v[32];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                v[i] = acc[0][t][i];
+                v[16 + i] = acc[1][t][i];
+            }
+            const float part = two ? fta_sum_exp2<32>(v, c, R[t]) : fta_sum_exp2<16>(v, c, R[t]);
+            tot[t] = part + fta_xor32(part);
+        }
+        const bool bad = !(tot[0] < 0x1p100f) || !(tot[1] < 0x1p100f);
+        if (__ballot(bad) != 0ull) {
+            // exact path: reference = this block's max
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                float mx = acc[0][t][0];
+#pragma unroll
+                for (int i = 1; i < 16; ++i) mx = fmaxf(mx, acc[0][t][i]);
+                if (two) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, acc[1][t][i]);
+                }
+                mx = fmaxf(mx, fta_xor32(mx));
+                const float Rn = (mx == -FTA_INF) ? 0.f : mx * c;
+                L[t] = (L[t] > 0.f) ? L[t] * fta_exp2(R[t] - Rn) : 0.f;
+                R[t] = Rn;
+                float v[32];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    v[i] = acc[0][t][i];
+                    v[16 + i] = acc[1][t][i];
+                }
+                const float part = two ? fta_sum_exp2<32>(v, c, Rn) : fta_sum_exp2<16>(v, c, Rn);
+                tot[t] = part + fta_xor32(part);
+            }
+        }
+        float lse_b[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            lse_b[t] = (tot[t] > 0.f) ? R[t] + fta_log2(tot[t]) : -FTA_INF;
+            L[t] += tot[t];
+            if (tot[t] > 0x1p40f) {
+                const float Rn = lse_b[t];
+                L[t] *= fta_exp2(R[t] - Rn);
+                R[t] = Rn;
+            }
+        }
+        const int qi = qbase + lane;
+        const float mine = (lane < 32) ? lse_b[0] : lse_b[1];
+        if (qi < N) blk_lse[((int64_t)bh * M + m) * N + qi] = mine;
+        if (kgroups > 0) {
+            float key = mine;
+            if (m == 0) key += adj_head;
+            if (m == M - 1) key += adj_tail;
+            if (m == next_start) {
+                if (curg >= 0 && gkey < tkey) {
+                    tkey = gkey;
+                    tidx = gidx;
+                }
+                ++curg;
+                next_start = ((curg + 1) * M + kgroups - 1) / kgroups;  // first block of group curg + 1
+                gkey = key;
+                gidx = m;
+            } else if (key > gkey) {
+                gkey = key;
+                gidx = m;
+            }
+        }
+
+        if (m + 1 < M) store_block(buf ^ 1);
+        __syncthreads();
+    }
+
+    const int qi = qbase + lane;
+    if (qi < N) {
+        const int t = lane >> 5;
+        const float Rr = (t == 0) ? R[0] : R[1];
+        const float Lr = (t == 0) ? L[0] : L[1];
+        row_lse[(int64_t)bh * N + qi] = (Lr > 0.f) ? Rr + fta_log2(Lr) : -FTA_INF;
         if (kgroups > 0) {
             if (curg >= 0 && gkey < tkey) tidx = gidx;
             tau_idx[(int64_t)bh * N + qi] = tidx;
@@ -505,6 +743,11 @@ int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D
     const int total = qtiles * B * H;
     const float c = scale * 1.4426950408889634f;
 #define FTA_LAUNCH_SCORE(DK)                                                                               \
+    if (bsz <= 64)                                                                                         \
+        hipLaunchKernelGGL((fta_block_score_lse_fast_kernel<DT, DK>), dim3(total), dim3(256), 0, st,       \
+                           (const uint16_t*)q, (const uint16_t*)k, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], H, \
+                           N, D, M, bsz, pad_head, pad_tail, c, blk_lse, row_lse, qtiles, total, kgroups, tau); \
+    else                                                                                                   \
     hipLaunchKernelGGL((fta_block_score_lse_kernel<DT, DK>), dim3(total), dim3(256), 0, st,                \
                        (const uint16_t*)q, (const uint16_t*)k, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], H, N, \
                        D, M, bsz, pad_head, pad_tail, c, blk_lse, row_lse, qtiles, total, kgroups, tau)
