@@ -336,6 +336,7 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
 #pragma unroll
                 for (int i = 0; i < 16; ++i) acc[s][t][i] = 0.f;
         const uint16_t* base = &sk[buf][0];
+        __builtin_amdgcn_s_setprio(1);  // keep the matrix core fed while the co-resident wave runs VALU
         if (two) {
             uint4 a0 = *reinterpret_cast<const uint4*>(base + kr0);
             uint4 a1 = *reinterpret_cast<const uint4*>(base + kr0 + 32 * ROW);
@@ -365,6 +366,7 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
             }
         }
 
+        __builtin_amdgcn_s_setprio(0);
         if (kb < 0 || kb + 64 > N || bsz < 64) {
 #pragma unroll
             for (int s = 0; s < 2; ++s)
