@@ -83,6 +83,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-iid", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=8192)
+    ap.add_argument("--only", choices=["score", "topk", "merge", "fwd", "bwd", "copy"], default=None,
+                    help="profiling aid: run one stage of the C3 step --steps times and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); every stage is per (b, h) "
@@ -118,6 +120,36 @@ def main():
             ev[4].record(stream)
             record.append(ev)
         return counts
+
+    if args.only:
+        idx, raw, avg = fta.flash_topk_score(q, k, H, b, topk, (0, 0), thr)
+        merged, counts, Wd = fta.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
+        o, lse = fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, b)
+        M_ = N // b
+        blk = torch.empty(B * H * M_ * N, device=dev, dtype=torch.float32)
+        row = torch.empty(B * H * N, device=dev, dtype=torch.float32)
+        sst = _lib.i64arr([N * H * D, D, H * D])
+        big = torch.empty(256 << 20, device=dev, dtype=torch.uint8)
+        for _ in range(args.steps):
+            if args.only == "score":
+                _lib.check(_lib.lib().fta_block_score_lse(q.data_ptr(), k.data_ptr(), 0, B, H, N, D, sst, sst, b, 0, 0,
+                                                          D ** -0.5, blk.data_ptr(), row.data_ptr(),
+                                                          stream.cuda_stream), "score")
+            elif args.only == "topk":
+                fta.flash_topk_score(q, k, H, b, topk, (0, 0), thr)
+            elif args.only == "merge":
+                fta.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
+            elif args.only == "fwd":
+                fta.flash_topk_attn(q, k, v, merged, counts, H, g, b)
+            elif args.only == "bwd":
+                ql.grad = kl.grad = vl.grad = None
+                o, lse = fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, b)
+                o.backward(do)
+            else:  # plain copy of 256 MiB: calibrates FETCH_SIZE / WRITE_SIZE
+                big[: 128 << 20].copy_(big[128 << 20:])
+        torch.cuda.synchronize()
+        print(json.dumps({"only": args.only, "steps": args.steps}), flush=True)
+        return
 
     for _ in range(args.warmup):
         step()

@@ -293,13 +293,25 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
     uint4 stage[LOADS];
     auto load_block = [&](int m) {
         const int kb = m * bsz - pad_head;
+        if (kb >= 0 && kb + 64 <= N && bsz == 64 && Dreal == D) {
+            // interior block: no bounds checks
 #pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-            const int s = tid + i * 256;
-            const int row = s / SEGS, seg = s - (s / SEGS) * SEGS;
-            const int t = kb + row;
-            const bool ok = row < bsz && t >= 0 && t < N && seg * 8 < Dreal;
-            stage[i] = ok ? *reinterpret_cast<const uint4*>(kp + (int64_t)t * k_sn + seg * 8) : fta_zero4();
+            for (int i = 0; i < LOADS; ++i) {
+                const int s = tid + i * 256;
+                const int row = s / SEGS, seg = s - (s / SEGS) * SEGS;
+                stage[i] = *reinterpret_cast<const uint4*>(kp + (int64_t)(kb + row) * k_sn + seg * 8);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < LOADS; ++i) {
+                const int s = tid + i * 256;
+                const int row = s / SEGS, seg = s - (s / SEGS) * SEGS;
+                const int t = kb + row;
+                const bool ok = row < bsz && t >= 0 && t < N && seg * 8 < Dreal;
+                const int tc = min(max(t, 0), N - 1);
+                const uint4 v = *reinterpret_cast<const uint4*>(kp + (int64_t)tc * k_sn + (ok ? seg * 8 : 0));
+                stage[i] = ok ? v : fta_zero4();
+            }
         }
     };
     auto store_block = [&](int buf) {
@@ -329,12 +341,7 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
         const int kb = m * bsz - pad_head;
 
         f32x16 acc[2][2];
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[s][t][i] = 0.f;
+        const f32x16 zacc = {};
         const uint16_t* base = &sk[buf][0];
         __builtin_amdgcn_s_setprio(1);  // keep the matrix core fed while the co-resident wave runs VALU
         if (two) {
@@ -347,10 +354,10 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
                     n0 = *reinterpret_cast<const uint4*>(base + kr0 + (ks + 1) * 16);
                     n1 = *reinterpret_cast<const uint4*>(base + kr0 + 32 * ROW + (ks + 1) * 16);
                 }
-                acc[0][0] = E::mma(a0, qf[0][ks], acc[0][0]);
-                acc[0][1] = E::mma(a0, qf[1][ks], acc[0][1]);
-                acc[1][0] = E::mma(a1, qf[0][ks], acc[1][0]);
-                acc[1][1] = E::mma(a1, qf[1][ks], acc[1][1]);
+                acc[0][0] = E::mma(a0, qf[0][ks], ks ? acc[0][0] : zacc);
+                acc[0][1] = E::mma(a0, qf[1][ks], ks ? acc[0][1] : zacc);
+                acc[1][0] = E::mma(a1, qf[0][ks], ks ? acc[1][0] : zacc);
+                acc[1][1] = E::mma(a1, qf[1][ks], ks ? acc[1][1] : zacc);
                 a0 = n0;
                 a1 = n1;
             }
@@ -360,10 +367,12 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
             for (int ks = 0; ks < KS; ++ks) {
                 uint4 n0 = a0;
                 if (ks + 1 < KS) n0 = *reinterpret_cast<const uint4*>(base + kr0 + (ks + 1) * 16);
-                acc[0][0] = E::mma(a0, qf[0][ks], acc[0][0]);
-                acc[0][1] = E::mma(a0, qf[1][ks], acc[0][1]);
+                acc[0][0] = E::mma(a0, qf[0][ks], ks ? acc[0][0] : zacc);
+                acc[0][1] = E::mma(a0, qf[1][ks], ks ? acc[0][1] : zacc);
                 a0 = n0;
             }
+            acc[1][0] = zacc;
+            acc[1][1] = zacc;
         }
 
         __builtin_amdgcn_s_setprio(0);
