@@ -21,6 +21,7 @@
 // reaches the threshold.
 #include "fta_common.h"
 
+
 // ----------------------------------------------------------------------------
 // Stage 1: per-block log2-sum-exp.
 // WG = 4 waves, each wave owns 64 queries (two 32-column MFMA tiles); the WG
@@ -254,8 +255,8 @@ __device__ __forceinline__ float fta_sum_exp2(const float* v, float c, float r) 
 // R lose mass to underflow only when they sit more than 2^-126 below R, i.e.
 // when their score is below fp32 resolution anyway.
 // ----------------------------------------------------------------------------
-template <int DT, int D>
-__global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fast_kernel(
+template <int DT, int D, int QT>
+__global__ __launch_bounds__(256 * (2 / QT), (D > 160) ? 1 : 2) void fta_block_score_lse_fast_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
     int H, int N, int Dreal, int M, int bsz, int pad_head, int pad_tail, float c,
@@ -265,8 +266,9 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
     constexpr int KS = D / 16;
     constexpr int ROW = D + 8;
     constexpr int SEGS = D / 8;
-    constexpr int LOADS = (64 * SEGS) / 256;
-    static_assert((64 * SEGS) % 256 == 0, "D must be a multiple of 32");
+    constexpr int NTHR = 256 * (2 / QT);
+    constexpr int LOADS = (64 * SEGS + NTHR - 1) / NTHR;
+    static_assert(QT == 1 || QT == 2, "one or two query tiles per wave");
     __shared__ __align__(16) uint16_t sk[2][64 * ROW];
 
     const int wg = fta_xcd_remap(blockIdx.x, total);
@@ -274,13 +276,13 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
     const int qt = wg - bh * qtiles;
     const int b = bh / H, h = bh - (bh / H) * H;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int qbase = qt * 256 + wave * 64;
+    const int qbase = qt * 256 + wave * 32 * QT;
     const uint16_t* qp = q + b * q_sb + h * q_sh;
     const uint16_t* kp = k + b * k_sb + h * k_sh;
 
-    uint4 qf[2][KS];
+    uint4 qf[QT][KS];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < QT; ++t) {
         const int qi = qbase + t * 32 + (lane & 31);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -297,17 +299,17 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
             // interior block: no bounds checks
 #pragma unroll
             for (int i = 0; i < LOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int row = s / SEGS, seg = s - (s / SEGS) * SEGS;
-                stage[i] = *reinterpret_cast<const uint4*>(kp + (int64_t)(kb + row) * k_sn + seg * 8);
+                if (s < 64 * SEGS) stage[i] = *reinterpret_cast<const uint4*>(kp + (int64_t)(kb + row) * k_sn + seg * 8);
             }
         } else {
 #pragma unroll
             for (int i = 0; i < LOADS; ++i) {
-                const int s = tid + i * 256;
+                const int s = tid + i * NTHR;
                 const int row = s / SEGS, seg = s - (s / SEGS) * SEGS;
                 const int t = kb + row;
-                const bool ok = row < bsz && t >= 0 && t < N && seg * 8 < Dreal;
+                const bool ok = s < 64 * SEGS && row < bsz && t >= 0 && t < N && seg * 8 < Dreal;
                 const int tc = min(max(t, 0), N - 1);
                 const uint4 v = *reinterpret_cast<const uint4*>(kp + (int64_t)tc * k_sn + (ok ? seg * 8 : 0));
                 stage[i] = ok ? v : fta_zero4();
@@ -317,9 +319,9 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
     auto store_block = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
-            const int s = tid + i * 256;
+            const int s = tid + i * NTHR;
             const int row = s / SEGS, seg = s - (s / SEGS) * SEGS;
-            *reinterpret_cast<uint4*>(&sk[buf][row * ROW + seg * 8]) = stage[i];
+            if (s < 64 * SEGS) *reinterpret_cast<uint4*>(&sk[buf][row * ROW + seg * 8]) = stage[i];
         }
     };
 
@@ -355,9 +357,9 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
                     n1 = *reinterpret_cast<const uint4*>(base + kr0 + 32 * ROW + (ks + 1) * 16);
                 }
                 acc[0][0] = E::mma(a0, qf[0][ks], ks ? acc[0][0] : zacc);
-                acc[0][1] = E::mma(a0, qf[1][ks], ks ? acc[0][1] : zacc);
+                if (QT == 2) acc[0][1] = E::mma(a0, qf[QT - 1][ks], ks ? acc[0][1] : zacc);
                 acc[1][0] = E::mma(a1, qf[0][ks], ks ? acc[1][0] : zacc);
-                acc[1][1] = E::mma(a1, qf[1][ks], ks ? acc[1][1] : zacc);
+                if (QT == 2) acc[1][1] = E::mma(a1, qf[QT - 1][ks], ks ? acc[1][1] : zacc);
                 a0 = n0;
                 a1 = n1;
             }
@@ -368,7 +370,7 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
                 uint4 n0 = a0;
                 if (ks + 1 < KS) n0 = *reinterpret_cast<const uint4*>(base + kr0 + (ks + 1) * 16);
                 acc[0][0] = E::mma(a0, qf[0][ks], ks ? acc[0][0] : zacc);
-                acc[0][1] = E::mma(a0, qf[1][ks], ks ? acc[0][1] : zacc);
+                if (QT == 2) acc[0][1] = E::mma(a0, qf[QT - 1][ks], ks ? acc[0][1] : zacc);
                 a0 = n0;
             }
             acc[1][0] = zacc;
@@ -392,7 +394,7 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
 
         float tot[2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < QT; ++t) {
             float v[32];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -402,11 +404,11 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
             const float part = two ? fta_sum_exp2<32>(v, c, R[t]) : fta_sum_exp2<16>(v, c, R[t]);
             tot[t] = part + fta_xor32(part);
         }
-        const bool bad = !(tot[0] < 0x1p100f) || !(tot[1] < 0x1p100f);
+        const bool bad = !(tot[0] < 0x1p100f) || (QT == 2 && !(tot[QT - 1] < 0x1p100f));
         if (__ballot(bad) != 0ull) {
             // exact path: reference = this block's max
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < QT; ++t) {
                 float mx = acc[0][t][0];
 #pragma unroll
                 for (int i = 1; i < 16; ++i) mx = fmaxf(mx, acc[0][t][i]);
@@ -430,7 +432,7 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
         }
         float lse_b[2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < QT; ++t) {
             lse_b[t] = (tot[t] > 0.f) ? R[t] + fta_log2(tot[t]) : -FTA_INF;
             L[t] += tot[t];
             if (tot[t] > 0x1p40f) {
@@ -439,9 +441,10 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
                 R[t] = Rn;
             }
         }
-        const int qi = qbase + lane;
-        const float mine = (lane < 32) ? lse_b[0] : lse_b[1];
-        if (qi < N) blk_lse[((int64_t)bh * M + m) * N + qi] = mine;
+        // lane owns query (lane & 31) of tile (lane >> 5) (two tiles) or of the only tile
+        const int qi = qbase + ((QT == 2) ? lane : (lane & 31));
+        const float mine = (QT == 2 && lane >= 32) ? lse_b[QT - 1] : lse_b[0];
+        if (qi < N && (QT == 2 || lane < 32)) blk_lse[((int64_t)bh * M + m) * N + qi] = mine;
         if (kgroups > 0) {
             float key = mine;
             if (m == 0) key += adj_head;
@@ -465,11 +468,11 @@ __global__ __launch_bounds__(256, (D > 160) ? 1 : 2) void fta_block_score_lse_fa
         __syncthreads();
     }
 
-    const int qi = qbase + lane;
-    if (qi < N) {
-        const int t = lane >> 5;
-        const float Rr = (t == 0) ? R[0] : R[1];
-        const float Lr = (t == 0) ? L[0] : L[1];
+    const int qi = qbase + ((QT == 2) ? lane : (lane & 31));
+    if (qi < N && (QT == 2 || lane < 32)) {
+        const bool t1 = QT == 2 && lane >= 32;
+        const float Rr = t1 ? R[QT - 1] : R[0];
+        const float Lr = t1 ? L[QT - 1] : L[0];
         row_lse[(int64_t)bh * N + qi] = (Lr > 0.f) ? Rr + fta_log2(Lr) : -FTA_INF;
         if (kgroups > 0) {
             if (curg >= 0 && gkey < tkey) tidx = gidx;
@@ -755,7 +758,8 @@ int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D
     const float c = scale * 1.4426950408889634f;
 #define FTA_LAUNCH_SCORE(DK)                                                                               \
     if (bsz <= 64)                                                                                         \
-        hipLaunchKernelGGL((fta_block_score_lse_fast_kernel<DT, DK>), dim3(total), dim3(256), 0, st,       \
+        hipLaunchKernelGGL((fta_block_score_lse_fast_kernel<DT, DK, (DK > 128) ? 1 : 2>), dim3(total),    \
+                           dim3(256 * (2 / ((DK > 128) ? 1 : 2))), 0, st,                                \
                            (const uint16_t*)q, (const uint16_t*)k, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], H, \
                            N, D, M, bsz, pad_head, pad_tail, c, blk_lse, row_lse, qtiles, total, kgroups, tau); \
     else                                                                                                   \
