@@ -24,6 +24,13 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
+# HBM bytes per fta_block_score_lse launch on the default workload, from rocprofv3 --pmc
+# FETCH_SIZE (8.027e5 KiB, x2.0) and WRITE_SIZE (2.102e6 KiB, x1.0); the factors are what the
+# same counters read for a 128 MiB device copy (bench.py --only copy).  A PMC pass cannot run
+# inside this process, so the figure is the last measured one and is refreshed with the kernel.
+SCORE_TRAFFIC_BYTES = int((2.0 * 8.027e5 + 1.0 * 2.102e6) * 1024)
+
+
 def make_inputs(B, N, H, D, peaked, seed, dev):
     import torch
 
@@ -215,9 +222,11 @@ def main():
                    "global_batch": B, "seq_len": N, "heads": H, "head_dim": D, "parallelism": "none"},
         "stage_ms": {k2: round(v2, 3) for k2, v2 in stage.items()},
         "flops": {"score": f_score, "fwd": f_fwd, "bwd_10DP": f_bwd, "P_pairs": P},
-        "roofline": {"bound": "mfma", "kernel": "fta_block_score_lse_kernel", "achieved": round(achieved, 2),
+        "roofline": {"bound": "mfma", "kernel": "fta_block_score_lse_fast_kernel", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "kernel_ms": round(k_ms, 3), "traffic": None},
+                     "kernel_ms": round(k_ms, 3),
+                     "traffic": SCORE_TRAFFIC_BYTES if (B, N, H, D, b) == (1, 32768, 32, 128, 64) else None,
+                     "algorithmic_bytes": 2 * B * H * N * D * 2 + 4 * B * H * (M + 1) * N},
     }
 
     if not args.no_iid:

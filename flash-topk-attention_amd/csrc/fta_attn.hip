@@ -535,27 +535,34 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
 }
 
 // ----------------------------------------------------------------------------
-// dK / dV.  WG = 4 waves x one 32-key tile; tiles enumerate (KV block, 32-key
-// sub-tile) pairs.  Column masks over 32-query chunks come from the membership
-// bitmap.  Per union chunk (Q, dO rows and T-layout copies staged in LDS):
+// dK / dV.  WG = TT x CS waves.  The WG owns TT 32-key tiles (consecutive
+// (KV block, 32-key sub-tile) pairs); wave w works on tile w % TT and chunk
+// slot w / TT.  Column masks over 32-query chunks come from the membership
+// bitmap; the union of the tiles' chunks is walked CS chunks per step, each
+// step's Q and dO rows staged once in LDS (double-buffered).  Per (tile, chunk):
 //   S = Q K^T, P = 2^{c S - lse2}, dP = dO V^T, dS = P (dP - delta),
-//   dV += P^T dO, dK += dS^T Q.  No atomics.
+//   dV += P^T dO, dK += dS^T Q.
+// Slot partials are summed through LDS at the end; no atomics.  With TT equal
+// to the tiles of one KV block, all waves share that block's chunk list, so no
+// wave idles on chunks that only another block selected.
 // ----------------------------------------------------------------------------
-template <int DT, int D, int NW>
-__global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
+template <int DT, int D, int TT, int CS>
+__global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
     using E = Elem<DT>;
+    constexpr int NW = TT * CS;
     constexpr int NTHR = NW * 64;
-    constexpr int T = NW;
     constexpr int KS = D / 16;
     constexpr int DT32 = D / 32;
     constexpr int QROW = D + 8;
     constexpr int QSEG = D / 8;
-    constexpr int QLOADS = (32 * QSEG + NTHR - 1) / NTHR;
-    __shared__ __align__(16) uint16_t sQ[2][32 * QROW];
-    __shared__ __align__(16) uint16_t sO[2][32 * QROW];
-    __shared__ float sL[2][32];
-    __shared__ float sDl[2][32];
-    __shared__ uint32_t sMask[T][kSeg];
+    constexpr int CHUNK = 32 * QSEG;                     // uint4 per staged chunk (Q or dO)
+    constexpr int QLOADS = (CS * CHUNK + NTHR - 1) / NTHR;
+    constexpr int STAGE = 2 * CS * 32 * QROW;            // uint16 per buffer (Q then dO, CS chunks each)
+    static_assert(CS == 1 || TT * 32 * D * 4 <= 2 * STAGE * 2, "reduction tile must fit the staging buffers");
+    __shared__ __align__(16) uint16_t sQO[2][STAGE];
+    __shared__ float sL[2][CS][32];
+    __shared__ float sDl[2][CS][32];
+    __shared__ uint32_t sMask[TT][kSeg];
     __shared__ int sList[kSeg];
     __shared__ int s_tmp[8];
 
@@ -565,10 +572,11 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
     const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int hf = lane >> 5;
+    const int tt = wave % TT, slot = wave / TT;
     const int Tb = (a.kvb + 31) >> 5;  // 32-key tiles per KV block
 
     // this wave's key tile
-    const int G = wk * T + wave;
+    const int G = wk * TT + tt;
     const int mblk = G / Tb;
     const int tin = G - (G / Tb) * Tb;
     const bool tile_live = mblk < a.Mkv;
@@ -604,27 +612,24 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
 
     for (int seg0 = 0; seg0 < a.NC; seg0 += kSeg) {
         const int segn = min(kSeg, a.NC - seg0);
-        // masks: tile tau x chunk (seg0 + cl) -> bits over the chunk's 32 queries
-        for (int i = tid; i < T * kSeg; i += NTHR) sMask[i / kSeg][i % kSeg] = 0u;
-        __syncthreads();
-        for (int pi = tid; pi < T * segn; pi += NTHR) {
-            const int tau = pi / segn, cl = pi - (pi / segn) * segn;
-            const int Gt = wk * T + tau;
-            const int mt = Gt / Tb;
-            if (mt >= a.Mkv) continue;
-            const int c = seg0 + cl;
-            const int pc = 32 * c;
-            const int qb_a = pc / a.g;
-            int qb_b = (pc + 31) / a.g;
-            if (qb_b > a.QM - 1) qb_b = a.QM - 1;
-            const uint32_t* srow = a.sel + ((int64_t)bh * a.Mkv + mt) * qw;
+        // masks: tile t x chunk (seg0 + cl) -> bits over the chunk's 32 queries
+        for (int pi = tid; pi < TT * segn; pi += NTHR) {
+            const int t = pi / segn, cl = pi - (pi / segn) * segn;
+            const int mt = (wk * TT + t) / Tb;
             uint32_t bits = 0u;
-            for (int qb = qb_a; qb <= qb_b; ++qb) {
-                if ((srow[qb >> 5] >> (qb & 31)) & 1u)
-                    bits |= fta_range_bits(qb * a.g - pc, qb * a.g + a.g - pc);
+            if (mt < a.Mkv) {
+                const int pc = 32 * (seg0 + cl);
+                const int qb_a = pc / a.g;
+                int qb_b = (pc + 31) / a.g;
+                if (qb_b > a.QM - 1) qb_b = a.QM - 1;
+                const uint32_t* srow = a.sel + ((int64_t)bh * a.Mkv + mt) * qw;
+                for (int qb = qb_a; qb <= qb_b; ++qb) {
+                    if ((srow[qb >> 5] >> (qb & 31)) & 1u)
+                        bits |= fta_range_bits(qb * a.g - pc, qb * a.g + a.g - pc);
+                }
+                bits &= fta_range_bits(a.q_pad - pc, a.q_pad + a.N - pc);
             }
-            bits &= fta_range_bits(a.q_pad - pc, a.q_pad + a.N - pc);
-            sMask[tau][cl] = bits;
+            sMask[t][cl] = bits;
         }
         __syncthreads();
         int U = 0;
@@ -633,7 +638,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
             int any = 0;
             if (cl < segn) {
 #pragma unroll
-                for (int t = 0; t < T; ++t) any |= (sMask[t][cl] != 0u);
+                for (int t = 0; t < TT; ++t) any |= (sMask[t][cl] != 0u);
             }
             int x = any;
 #pragma unroll
@@ -656,20 +661,26 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
         }
         if (U == 0) continue;
 
-        auto load = [&](int u) {
-            const int c = seg0 + sList[u];
+        // stage chunks u0 .. u0 + CS - 1 of the union list (slots past U load zeros)
+        auto load = [&](int u0) {
 #pragma unroll
             for (int i = 0; i < QLOADS; ++i) {
                 const int s = tid + i * NTHR;
-                const int row = s / QSEG, sg = s - (s / QSEG) * QSEG;
+                const int sl = s / CHUNK, r = s - sl * CHUNK;
+                const int row = r / QSEG, sg = r - (r / QSEG) * QSEG;
+                const bool live = s < CS * CHUNK && u0 + sl < U;
+                const int c = live ? seg0 + sList[u0 + sl] : 0;
                 const int t = 32 * c + row - a.q_pad;
-                const bool ok = s < 32 * QSEG && t >= 0 && t < a.N && sg * 8 < a.Dreal;
+                const bool ok = live && t >= 0 && t < a.N && sg * 8 < a.Dreal;
                 qst[i] = ok ? *reinterpret_cast<const uint4*>(qp + (int64_t)t * a.q_sn + sg * 8) : fta_zero4();
                 ost[i] = ok ? *reinterpret_cast<const uint4*>(dp + (int64_t)t * a.d_sn + sg * 8) : fta_zero4();
             }
-            if (tid < 32) {
-                const int t = 32 * c + tid - a.q_pad;
-                const bool ok = t >= 0 && t < a.N;
+            if (tid < 32 * CS) {
+                const int sl = tid >> 5;
+                const bool live = u0 + sl < U;
+                const int c = live ? seg0 + sList[u0 + sl] : 0;
+                const int t = 32 * c + (tid & 31) - a.q_pad;
+                const bool ok = live && t >= 0 && t < a.N;
                 lst = ok ? a.lse_in[(int64_t)bh * a.N + t] * 1.4426950408889634f : -FTA_INF;
                 dst = ok ? a.delta_in[(int64_t)bh * a.N + t] : 0.f;
             }
@@ -678,26 +689,27 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
 #pragma unroll
             for (int i = 0; i < QLOADS; ++i) {
                 const int s = tid + i * NTHR;
-                if (s < 32 * QSEG) {
-                    const int row = s / QSEG, sg = s - (s / QSEG) * QSEG;
-                    *reinterpret_cast<uint4*>(&sQ[buf][row * QROW + sg * 8]) = qst[i];
-                    *reinterpret_cast<uint4*>(&sO[buf][row * QROW + sg * 8]) = ost[i];
+                if (s < CS * CHUNK) {
+                    const int sl = s / CHUNK, r = s - sl * CHUNK;
+                    const int row = r / QSEG, sg = r - (r / QSEG) * QSEG;
+                    uint16_t* base = &sQO[buf][sl * 32 * QROW];
+                    *reinterpret_cast<uint4*>(base + row * QROW + sg * 8) = qst[i];
+                    *reinterpret_cast<uint4*>(base + CS * 32 * QROW + row * QROW + sg * 8) = ost[i];
                 }
             }
-            if (tid < 32) {
-                sL[buf][tid] = lst;
-                sDl[buf][tid] = dst;
+            if (tid < 32 * CS) {
+                sL[buf][tid >> 5][tid & 31] = lst;
+                sDl[buf][tid >> 5][tid & 31] = dst;
             }
         };
 
         load(0);
         store(0);
         __syncthreads();
-        for (int u = 0; u < U; ++u) {
-            const int buf = u & 1;
-            if (u + 1 < U) load(u + 1);
-            const int cl = sList[u];
-            const uint32_t mk = __builtin_amdgcn_readfirstlane(sMask[wave][cl]);
+        for (int u0 = 0; u0 < U; u0 += CS) {
+            const int buf = (u0 / CS) & 1;
+            if (u0 + CS < U) load(u0 + CS);
+            const uint32_t mk = (u0 + slot < U) ? __builtin_amdgcn_readfirstlane(sMask[tt][sList[u0 + slot]]) : 0u;
             if (mk) {
                 f32x16 s, dpv;
 #pragma unroll
@@ -705,8 +717,10 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
                     s[i] = 0.f;
                     dpv[i] = 0.f;
                 }
-                const uint16_t* qb = &sQ[buf][0];
-                const uint16_t* ob = &sO[buf][0];
+                const uint16_t* qb = &sQO[buf][slot * 32 * QROW];
+                const uint16_t* ob = qb + CS * 32 * QROW;
+                const float* lrow = sL[buf][slot];
+                const float* drow = sDl[buf][slot];
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
                     const int off = (lane & 31) * QROW + ks * 16 + hf * 8;
@@ -722,10 +736,10 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
                         const int i = 8 * ks + e;
                         const int r = c_row(i, lane);
                         const bool ok = kok && ((mk >> r) & 1u);
-                        const float l2 = sL[buf][r];
+                        const float l2 = lrow[r];
                         const float p = (ok && l2 != -FTA_INF) ? fta_exp2(fmaf(s[i], a.c, -l2)) : 0.f;
                         pv[e] = p;
-                        dv8[e] = p * (dpv[i] - sDl[buf][r]);
+                        dv8[e] = p * (dpv[i] - drow[r]);
                     }
                     pf[ks] = make_uint4(E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
                                         E::pack2(pv[6], pv[7]));
@@ -741,12 +755,45 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) 
                     }
                 }
             }
-            if (u + 1 < U) store(buf ^ 1);
+            if (u0 + CS < U) store(buf ^ 1);
             __syncthreads();
         }
     }
 
-    if (!tile_live) return;
+    if (CS > 1) {
+        // sum the slot partials into slot 0, one slot and one operand at a time;
+        // lane-linear layout [tile][dt][i][lane] keeps LDS accesses conflict-free
+        float* red = reinterpret_cast<float*>(&sQO[0][0]);
+#pragma unroll
+        for (int sl = 1; sl < CS; ++sl) {
+#pragma unroll
+            for (int which = 0; which < 2; ++which) {
+                if (slot == sl) {
+#pragma unroll
+                    for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i)
+                            red[((tt * DT32 + dt) * 16 + i) * 64 + lane] = which ? dva[dt][i] : dka[dt][i];
+                }
+                __syncthreads();
+                if (slot == 0) {
+#pragma unroll
+                    for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            const float x = red[((tt * DT32 + dt) * 16 + i) * 64 + lane];
+                            if (which)
+                                dva[dt][i] += x;
+                            else
+                                dka[dt][i] += x;
+                        }
+                }
+                __syncthreads();
+            }
+        }
+    }
+
+    if (!tile_live || slot != 0) return;
     // C layout: lane column = d (dt * 32 + lane & 31), rows = keys c_row(i, lane)
     uint16_t* kout = a.out0 + b * a.o0_sb + h * a.o0_sh;
     uint16_t* vout = a.out1 + b * a.o1_sb + h * a.o1_sh;
@@ -855,23 +902,40 @@ int launch_dq_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
     return fta::check_launch("fta_sparse_dq_kernel");
 }
 
+// dK/dV launch shape: TT key tiles x CS chunk slots.  TT covers the 32-key tiles
+// of one KV block when a block has at most two, so every wave of a workgroup
+// shares one chunk list; longer blocks, and D = 256 (whose slot partials would
+// spill), use one slot (TT = all waves).
 template <int DT>
-int launch_dkv_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
+int launch_dkv_dt(AttnArgs& a, int Dk, int Tb, int B, int H, int ntiles, hipStream_t st) {
+    int TT = 0;
+    auto go = [&](auto kern, int tt, int nw) {
+        TT = tt;
+        a.wg_per_bh = (ntiles + tt - 1) / tt;
+        a.total = a.wg_per_bh * B * H;
+        hipLaunchKernelGGL(kern, dim3(a.total), dim3(nw * 64), 0, st, a);
+    };
     switch (Dk) {
-#define FTA_DKV(DK, NW)                                                                                  \
-    case DK:                                                                                             \
-        hipLaunchKernelGGL((fta_sparse_dkv_kernel<DT, DK, NW>), dim3(grid), dim3(NW * 64), 0, st, a);     \
+#define FTA_DKV(DK, NW, TT1, CS1, TT2, CS2)                                                  \
+    case DK:                                                                                 \
+        if (Tb == 1)                                                                         \
+            go(fta_sparse_dkv_kernel<DT, DK, TT1, CS1>, TT1, TT1 * CS1);                     \
+        else if (Tb == 2)                                                                    \
+            go(fta_sparse_dkv_kernel<DT, DK, TT2, CS2>, TT2, TT2 * CS2);                     \
+        else                                                                                 \
+            go(fta_sparse_dkv_kernel<DT, DK, NW, 1>, NW, NW);                                \
         break;
-        FTA_DKV(32, 8)
-        FTA_DKV(64, 8)
-        FTA_DKV(96, 4)
-        FTA_DKV(128, 4)
-        FTA_DKV(160, 4)
-        FTA_DKV(256, 4)
+        FTA_DKV(32, 8, 1, 4, 2, 4)
+        FTA_DKV(64, 8, 1, 4, 2, 4)
+        FTA_DKV(96, 4, 1, 4, 2, 2)
+        FTA_DKV(128, 4, 1, 4, 2, 2)
+        FTA_DKV(160, 4, 2, 2, 2, 2)
+        FTA_DKV(256, 4, 4, 1, 4, 1)
 #undef FTA_DKV
         default:
             return fta::arg_error("sparse_attn_bwd: unsupported head dim");
     }
+    (void)TT;
     return fta::check_launch("fta_sparse_dkv_kernel");
 }
 
@@ -1018,12 +1082,10 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, 
     a.o1_sb = dv_strides[0];
     a.o1_sh = dv_strides[1];
     a.o1_sn = dv_strides[2];
-    const int ntiles = G.Mkv * ((kv_block_size + 31) / 32);
-    const int Tk = (G.Dk <= 64) ? 8 : 4;  // key tiles per dK/dV workgroup
-    a.wg_per_bh = (ntiles + Tk - 1) / Tk;
-    a.total = a.wg_per_bh * B * H;
-    if (dtype == FTA_DTYPE_BF16) return launch_dkv_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);
-    return launch_dkv_dt<FTA_DTYPE_F16>(a, G.Dk, a.total, st);
+    const int Tb = (kv_block_size + 31) / 32;
+    const int ntiles = G.Mkv * Tb;
+    if (dtype == FTA_DTYPE_BF16) return launch_dkv_dt<FTA_DTYPE_BF16>(a, G.Dk, Tb, B, H, ntiles, st);
+    return launch_dkv_dt<FTA_DTYPE_F16>(a, G.Dk, Tb, B, H, ntiles, st);
     FTA_TRY_END
 }
 

@@ -130,6 +130,14 @@ ATTN_CASES = [
     (1, 600, 1, 256, 48, 40, (0, 24), (0, 0), 7, torch.bfloat16),
     (1, 500, 2, 160, 20, 128, (0, 0), (20, 120), 3, torch.float16),
     (1, 256, 2, 64, 32, 64, (0, 0), (0, 0), 4, torch.float32),
+    # kv blocks of one 32-key tile (dK/dV: one tile, four chunk slots per workgroup)
+    (1, 1024, 2, 128, 32, 32, (0, 0), (0, 0), 24, torch.bfloat16),
+    (1, 700, 2, 64, 16, 16, (2, 2), (4, 0), 20, torch.float16),
+    (1, 512, 1, 160, 32, 32, (0, 0), (0, 0), 8, torch.float16),
+    (1, 640, 2, 96, 32, 64, (0, 0), (0, 0), 6, torch.bfloat16),
+    # more than 512 query chunks / KV blocks: masks are built in several segments
+    (1, 17024, 1, 64, 32, 64, (0, 0), (0, 0), 4, torch.bfloat16),
+    (1, 16448, 1, 32, 32, 16, (0, 0), (0, 0), 3, torch.bfloat16),
 ]
 
 
@@ -185,9 +193,12 @@ def test_sparse_attn_fwd_bwd_vs_oracle(case):
     np.testing.assert_allclose(l[fin], rl[fin], rtol=1e-4, atol=1e-4)
     dq, dk, dv = O.sparse_attn_bwd(qn, kn, vn, np32(do), merged, H, g, b, None, qpad, kvpad)
     for name, got, ref in (("dq", q.grad, dq), ("dk", k.grad, dk), ("dv", v.grad, dv)):
-        # gradients are O(sqrt(#keys)) larger than o; the atol scales with their magnitude
+        # gradients are O(sqrt(#keys)) larger than o; the atol scales with their magnitude.  dS and P
+        # are rounded to 16 bits before the dQ / dK / dV products (as in the reference kernels); with
+        # few keys per query and small D those rounding errors do not average out, so up to 5e-4 of
+        # the elements may exceed the soft bound, none the hard one.
         assert_close_frac(np32(got), ref, atol=2e-3 * max(1.0, np.abs(ref).max() / 4), rtol=1e-2, name=name,
-                          hard_atol=1e-2 * max(1.0, np.abs(ref).max() / 4))
+                          min_frac=0.9995, hard_atol=1e-2 * max(1.0, np.abs(ref).max() / 4))
 
 
 def test_reverse_indices_and_sort_by_count():
