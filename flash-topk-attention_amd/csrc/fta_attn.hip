@@ -53,10 +53,14 @@ struct AttnArgs {
     int wg_per_bh, total;
 };
 
-__device__ __forceinline__ uint32_t fta_range_bits(int lo, int hi) {  // bits [lo, hi) of 32
+// Bits [lo, hi) of a 32-bit mask; lo and hi may lie anywhere (they are clamped
+// to [0, 32] first, so a range wholly outside the word gives 0).
+__device__ __forceinline__ uint32_t fta_range_bits(int lo, int hi) {
+    lo = max(lo, 0);
+    hi = min(hi, 32);
     if (hi <= lo) return 0u;
-    const uint32_t up = (hi >= 32) ? 0xffffffffu : ((1u << hi) - 1u);
-    const uint32_t dn = (lo <= 0) ? 0u : ((1u << lo) - 1u);
+    const uint32_t up = (hi == 32) ? 0xffffffffu : ((1u << hi) - 1u);
+    const uint32_t dn = (1u << lo) - 1u;
     return up & ~dn;
 }
 
@@ -538,30 +542,46 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
 // dK / dV.  WG = TT x CS waves.  The WG owns TT 32-key tiles (consecutive
 // (KV block, 32-key sub-tile) pairs); wave w works on tile w % TT and chunk
 // slot w / TT.  Column masks over 32-query chunks come from the membership
-// bitmap; the union of the tiles' chunks is walked CS chunks per step, each
-// step's Q and dO rows staged once in LDS (double-buffered).  Per (tile, chunk):
+// bitmap; the union of the tiles' chunks is walked CS chunks per step.  Each
+// step's Q and dO rows (and lse, delta) are gathered straight into LDS with
+// LDS DMA, NST steps in flight, so the gather latency is covered without
+// holding staging registers.  Per (tile, chunk):
 //   S = Q K^T, P = 2^{c S - lse2}, dP = dO V^T, dS = P (dP - delta),
 //   dV += P^T dO, dK += dS^T Q.
 // Slot partials are summed through LDS at the end; no atomics.  With TT equal
 // to the tiles of one KV block, all waves share that block's chunk list, so no
 // wave idles on chunks that only another block selected.
+// Rows outside the sequence and columns past D are loaded from clamped
+// addresses (finite data); the masks zero their P and dS, and the columns are
+// never stored.
 // ----------------------------------------------------------------------------
+template <int D, int TT, int CS>
+struct DkvShape {
+    static constexpr int NW = TT * CS;
+    static constexpr int NTHR = NW * 64;
+    static constexpr int QSEG = D / 8;
+    static constexpr int TILE = 32 * QSEG;                       // 16-byte slots per 32-row tile
+    static constexpr int LQ = (2 * CS * TILE + NTHR - 1) / NTHR;  // DMA instructions per wave per step
+    static constexpr int L = LQ + 1;                              // + one for lse / delta
+    static constexpr int LD_OFF = LQ * NW * 1024;                 // byte offset of lse / delta in a step
+    static constexpr int STAGE_B = LD_OFF + NW * 256;
+    static constexpr int FIXED_B = TT * kSeg * 4 + kSeg * 4 + 64;
+    static constexpr int NST_FIT = (150 * 1024 - FIXED_B) / STAGE_B;
+    static constexpr int NST = NST_FIT > 4 ? 4 : NST_FIT;
+    static_assert(NST >= 2, "two steps must fit in LDS");
+    static_assert((NST - 2) * L < 64, "vmcnt range");
+};
+
 template <int DT, int D, int TT, int CS>
 __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
     using E = Elem<DT>;
-    constexpr int NW = TT * CS;
-    constexpr int NTHR = NW * 64;
+    using Sh = DkvShape<D, TT, CS>;
+    constexpr int NW = Sh::NW, QSEG = Sh::QSEG, TILE = Sh::TILE, LQ = Sh::LQ, NST = Sh::NST;
+    using SW = FtaSwz<QSEG>;
     constexpr int KS = D / 16;
     constexpr int DT32 = D / 32;
-    constexpr int QROW = D + 8;
-    constexpr int QSEG = D / 8;
-    constexpr int CHUNK = 32 * QSEG;                     // uint4 per staged chunk (Q or dO)
-    constexpr int QLOADS = (CS * CHUNK + NTHR - 1) / NTHR;
-    constexpr int STAGE = 2 * CS * 32 * QROW;            // uint16 per buffer (Q then dO, CS chunks each)
-    static_assert(CS == 1 || TT * 32 * D * 4 <= 2 * STAGE * 2, "reduction tile must fit the staging buffers");
-    __shared__ __align__(16) uint16_t sQO[2][STAGE];
-    __shared__ float sL[2][CS][32];
-    __shared__ float sDl[2][CS][32];
+    static_assert(CS == 1 || TT * 32 * D * 4 <= NST * Sh::STAGE_B, "reduction tile must fit the staging buffers");
+    __shared__ __align__(1024) unsigned char sStage[NST][Sh::STAGE_B];
     __shared__ uint32_t sMask[TT][kSeg];
     __shared__ int sList[kSeg];
     __shared__ int s_tmp[8];
@@ -570,7 +590,8 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
     const int bh = wgi / a.wg_per_bh;
     const int wk = wgi - bh * a.wg_per_bh;
     const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hf = lane >> 5;
     const int tt = wave % TT, slot = wave / TT;
     const int Tb = (a.kvb + 31) >> 5;  // 32-key tiles per KV block
@@ -588,6 +609,8 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
     const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
     const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
     const uint16_t* dp = a.dout + b * a.d_sb + h * a.d_sh;
+    const float* lsep = a.lse_in + (int64_t)bh * a.N;
+    const float* dlp = a.delta_in + (int64_t)bh * a.N;
 
     uint4 kf[KS], vf[KS];
 #pragma unroll
@@ -597,6 +620,35 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
         kf[ks] = ok ? *reinterpret_cast<const uint4*>(kp + (int64_t)tk * a.k_sn + d) : fta_zero4();
         vf[ks] = ok ? *reinterpret_cast<const uint4*>(vp + (int64_t)tk * a.v_sn + d) : fta_zero4();
     }
+    // complete the register loads here: the DMA steps below are invisible to the
+    // compiler, which would otherwise wait for these loads (and with them every
+    // DMA issued before their first use) inside the step loop
+    fta_wait_vmcnt<0>();
+
+    // Per-lane DMA sources.  Step layout: [Q slot 0..CS-1][dO slot 0..CS-1] 32-row
+    // tiles, then lse / delta.  Instruction i of this wave fills 1 KB block
+    // blk = i * NW + wave; a block never straddles a tile, so its tensor (ten)
+    // and slot (sl) are wave-uniform, while the row and 16-byte slot are per
+    // lane and the same for every step.  roff[i] = row * stride + column.
+    int64_t roff[LQ];  // bytes
+#pragma unroll
+    for (int i = 0; i < LQ; ++i) {
+        const int blk = i * NW + wave;
+        const int ten = (blk * 64) / (CS * TILE);
+        const int r2 = (blk * 64 + lane) % TILE;
+        const int row = r2 / QSEG;
+        int j = SW::slot(row, r2 - row * QSEG);
+        if (j * 8 >= a.Dreal) j = 0;  // columns past D: any finite data (never stored)
+        roff[i] = 2 * ((int64_t)row * (ten == 1 ? a.d_sn : a.q_sn) + j * 8);
+    }
+    // lse / delta lane: value v = wave * 64 + lane -> (which array, slot, row)
+    const int lv = wave * 64 + lane;
+    const bool l_isd = lv >= 32 * CS && lv < 64 * CS;
+    const int l_sl = (lv < 64 * CS) ? ((lv >> 5) % CS) : 0;
+    const int l_row = lv & 31;
+    const float* l_base = l_isd ? dlp : lsep;
+    const uint32_t lds0 = fta_lds_addr(&sStage[0][0]);
+
     f32x16 dka[DT32], dva[DT32];
 #pragma unroll
     for (int dt = 0; dt < DT32; ++dt)
@@ -606,14 +658,11 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
             dva[dt][i] = 0.f;
         }
 
-    uint4 qst[QLOADS], ost[QLOADS];
-    float lst = 0.f, dst = 0.f;
     const int qw = a.QW;
-
     for (int seg0 = 0; seg0 < a.NC; seg0 += kSeg) {
         const int segn = min(kSeg, a.NC - seg0);
         // masks: tile t x chunk (seg0 + cl) -> bits over the chunk's 32 queries
-        for (int pi = tid; pi < TT * segn; pi += NTHR) {
+        for (int pi = tid; pi < TT * segn; pi += Sh::NTHR) {
             const int t = pi / segn, cl = pi - (pi / segn) * segn;
             const int mt = (wk * TT + t) / Tb;
             uint32_t bits = 0u;
@@ -633,7 +682,7 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
         }
         __syncthreads();
         int U = 0;
-        for (int base = 0; base < segn; base += NTHR) {
+        for (int base = 0; base < segn; base += Sh::NTHR) {
             const int cl = base + tid;
             int any = 0;
             if (cl < segn) {
@@ -660,73 +709,110 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
             U += tot;
         }
         if (U == 0) continue;
+        const int nsteps = (U + CS - 1) / CS;
 
-        // stage chunks u0 .. u0 + CS - 1 of the union list (slots past U load zeros)
-        auto load = [&](int u0) {
+        // gather step k (chunks k*CS .. k*CS + CS - 1 of the union list) into stage buffer st
+        auto issue = [&](int st, int k) {
+            const uint32_t sbase = lds0 + st * Sh::STAGE_B;
+            const int u0 = k * CS;
+            int cs[CS];
+            bool inner = true;  // every row of every chunk lies in [0, N)
 #pragma unroll
-            for (int i = 0; i < QLOADS; ++i) {
-                const int s = tid + i * NTHR;
-                const int sl = s / CHUNK, r = s - sl * CHUNK;
-                const int row = r / QSEG, sg = r - (r / QSEG) * QSEG;
-                const bool live = s < CS * CHUNK && u0 + sl < U;
-                const int c = live ? seg0 + sList[u0 + sl] : 0;
-                const int t = 32 * c + row - a.q_pad;
-                const bool ok = live && t >= 0 && t < a.N && sg * 8 < a.Dreal;
-                qst[i] = ok ? *reinterpret_cast<const uint4*>(qp + (int64_t)t * a.q_sn + sg * 8) : fta_zero4();
-                ost[i] = ok ? *reinterpret_cast<const uint4*>(dp + (int64_t)t * a.d_sn + sg * 8) : fta_zero4();
+            for (int sl = 0; sl < CS; ++sl) {
+                cs[sl] = __builtin_amdgcn_readfirstlane(seg0 + sList[min(u0 + sl, U - 1)]);
+                const int t0 = 32 * cs[sl] - a.q_pad;
+                inner = inner && t0 >= 0 && t0 + 31 < a.N;
             }
-            if (tid < 32 * CS) {
-                const int sl = tid >> 5;
-                const bool live = u0 + sl < U;
-                const int c = live ? seg0 + sList[u0 + sl] : 0;
-                const int t = 32 * c + (tid & 31) - a.q_pad;
-                const bool ok = live && t >= 0 && t < a.N;
-                lst = ok ? a.lse_in[(int64_t)bh * a.N + t] * 1.4426950408889634f : -FTA_INF;
-                dst = ok ? a.delta_in[(int64_t)bh * a.N + t] : 0.f;
-            }
-        };
-        auto store = [&](int buf) {
+            if (inner) {
 #pragma unroll
-            for (int i = 0; i < QLOADS; ++i) {
-                const int s = tid + i * NTHR;
-                if (s < CS * CHUNK) {
-                    const int sl = s / CHUNK, r = s - sl * CHUNK;
-                    const int row = r / QSEG, sg = r - (r / QSEG) * QSEG;
-                    uint16_t* base = &sQO[buf][sl * 32 * QROW];
-                    *reinterpret_cast<uint4*>(base + row * QROW + sg * 8) = qst[i];
-                    *reinterpret_cast<uint4*>(base + CS * 32 * QROW + row * QROW + sg * 8) = ost[i];
+                for (int i = 0; i < LQ; ++i) {
+                    const int blk = i * NW + wave;
+                    const int ten = (blk * 64) / (CS * TILE);
+                    const int sl = ((blk * 64) / TILE) % CS;
+                    const int64_t t0 = 32 * cs[sl] - a.q_pad;
+                    const char* base = reinterpret_cast<const char*>(ten == 1 ? dp + t0 * a.d_sn : qp + t0 * a.q_sn);
+                    fta_dma16_at(base + roff[i], sbase + blk * 1024);
+                }
+            } else {  // a chunk at a sequence edge: clamp its rows (masked off) into [0, N)
+#pragma unroll
+                for (int i = 0; i < LQ; ++i) {
+                    const int blk = i * NW + wave;
+                    const int ten = (blk * 64) / (CS * TILE);
+                    const int sl = ((blk * 64) / TILE) % CS;
+                    const int r2 = (blk * 64 + lane) % TILE;
+                    const int row = r2 / QSEG;
+                    int j = SW::slot(row, r2 - row * QSEG);
+                    if (j * 8 >= a.Dreal) j = 0;
+                    const int t = min(max(32 * cs[sl] - a.q_pad + row, 0), a.N - 1);
+                    fta_dma16_at((ten == 1 ? dp + (int64_t)t * a.d_sn : qp + (int64_t)t * a.q_sn) + j * 8,
+                                 sbase + blk * 1024);
                 }
             }
-            if (tid < 32 * CS) {
-                sL[buf][tid >> 5][tid & 31] = lst;
-                sDl[buf][tid >> 5][tid & 31] = dst;
-            }
+            int c = cs[0];
+#pragma unroll
+            for (int sl = 1; sl < CS; ++sl) c = (l_sl == sl) ? cs[sl] : c;
+            const int t = min(max(32 * c - a.q_pad + l_row, 0), a.N - 1);
+            fta_dma4_at(l_base + t, sbase + Sh::LD_OFF + wave * 256);
         };
 
-        load(0);
-        store(0);
-        __syncthreads();
-        for (int u0 = 0; u0 < U; u0 += CS) {
-            const int buf = (u0 / CS) & 1;
-            if (u0 + CS < U) load(u0 + CS);
-            const uint32_t mk = (u0 + slot < U) ? __builtin_amdgcn_readfirstlane(sMask[tt][sList[u0 + slot]]) : 0u;
+#pragma unroll
+        for (int k = 0; k < NST - 1; ++k)
+            if (k < nsteps) issue(k, k);
+        int cur = 0;  // stage buffer of step k
+        for (int k = 0; k < nsteps; ++k) {
+            if (k + NST - 2 < nsteps)
+                fta_wait_vmcnt<Sh::L * (NST - 2)>();
+            else
+                fta_wait_vmcnt<0>();
+            __syncthreads();  // step k visible to all waves; step k - 1's buffer is free
+            if (k + NST - 1 < nsteps) issue(cur == 0 ? NST - 1 : cur - 1, k + NST - 1);
+            const int u = k * CS + slot;
+            const uint32_t mk = (u < U) ? __builtin_amdgcn_readfirstlane(sMask[tt][sList[u]]) : 0u;
             if (mk) {
+                const uint16_t* qb = reinterpret_cast<const uint16_t*>(&sStage[cur][0]) + slot * TILE * 8;
+                const uint16_t* ob = qb + CS * TILE * 8;
+                const float* ld = reinterpret_cast<const float*>(&sStage[cur][Sh::LD_OFF]);
+                // Phased so that LDS latency overlaps MFMA work without exceeding the
+                // 256 VGPRs: (1) operand rows, (2) S and dP MFMAs, (3) transposed
+                // operands and lse / delta (while those MFMAs run), (4) softmax,
+                // (5) dV and dK MFMAs.  sched_barrier keeps the phases in order.
+                uint4 qa[KS], oa[KS];
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const int off = SW::off(lane & 31, 2 * ks + hf);
+                    qa[ks] = *reinterpret_cast<const uint4*>(qb + off);
+                    oa[ks] = *reinterpret_cast<const uint4*>(ob + off);
+                }
                 f32x16 s, dpv;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     s[i] = 0.f;
                     dpv[i] = 0.f;
                 }
-                const uint16_t* qb = &sQO[buf][slot * 32 * QROW];
-                const uint16_t* ob = qb + CS * 32 * QROW;
-                const float* lrow = sL[buf][slot];
-                const float* drow = sDl[buf][slot];
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
-                    const int off = (lane & 31) * QROW + ks * 16 + hf * 8;
-                    s = E::mma(*reinterpret_cast<const uint4*>(qb + off), kf[ks], s);
-                    dpv = E::mma(*reinterpret_cast<const uint4*>(ob + off), vf[ks], dpv);
+                    s = E::mma(qa[ks], kf[ks], s);
+                    dpv = E::mma(oa[ks], vf[ks], dpv);
                 }
+                __builtin_amdgcn_sched_group_barrier(0x100, 2 * KS, 0);  // all operand-row reads
+                __builtin_amdgcn_sched_group_barrier(0x008, 2 * KS, 0);  // then the S / dP MFMAs
+                __builtin_amdgcn_sched_barrier(0);
+                uint4 to[2][DT32], tq[2][DT32];
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int dt = 0; dt < DT32; ++dt) {
+                        to[ks][dt] = fta_tr_frag_sw<QSEG>(ob, ks * 16, dt * 32, lane);
+                        tq[ks][dt] = fta_tr_frag_sw<QSEG>(qb, ks * 16, dt * 32, lane);
+                    }
+                float lr[16], dr[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int r = c_row(i, lane);
+                    lr[i] = ld[slot * 32 + r];
+                    dr[i] = ld[(CS + slot) * 32 + r];
+                }
+                __builtin_amdgcn_sched_barrier(0);
                 uint4 pf[2], dsf[2];
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
@@ -735,11 +821,11 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
                     for (int e = 0; e < 8; ++e) {
                         const int i = 8 * ks + e;
                         const int r = c_row(i, lane);
+                        // a selected row with a valid key has a finite lse
                         const bool ok = kok && ((mk >> r) & 1u);
-                        const float l2 = lrow[r];
-                        const float p = (ok && l2 != -FTA_INF) ? fta_exp2(fmaf(s[i], a.c, -l2)) : 0.f;
+                        const float p = ok ? fta_exp2(fmaf(s[i], a.c, -lr[i] * 1.4426950408889634f)) : 0.f;
                         pv[e] = p;
-                        dv8[e] = p * (dpv[i] - drow[r]);
+                        dv8[e] = p * (dpv[i] - dr[i]);
                     }
                     pf[ks] = make_uint4(E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
                                         E::pack2(pv[6], pv[7]));
@@ -750,20 +836,20 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
                 for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
                     for (int dt = 0; dt < DT32; ++dt) {
-                        dva[dt] = E::mma(pf[ks], fta_tr_frag(ob, QROW, ks * 16, dt * 32, lane), dva[dt]);
-                        dka[dt] = E::mma(dsf[ks], fta_tr_frag(qb, QROW, ks * 16, dt * 32, lane), dka[dt]);
+                        dva[dt] = E::mma(pf[ks], to[ks][dt], dva[dt]);
+                        dka[dt] = E::mma(dsf[ks], tq[ks][dt], dka[dt]);
                     }
                 }
             }
-            if (u0 + CS < U) store(buf ^ 1);
-            __syncthreads();
+            cur = (cur == NST - 1) ? 0 : cur + 1;
         }
+        __syncthreads();  // all waves done with the stage buffers, sMask and sList
     }
 
     if (CS > 1) {
         // sum the slot partials into slot 0, one slot and one operand at a time;
         // lane-linear layout [tile][dt][i][lane] keeps LDS accesses conflict-free
-        float* red = reinterpret_cast<float*>(&sQO[0][0]);
+        float* red = reinterpret_cast<float*>(&sStage[0][0]);
 #pragma unroll
         for (int sl = 1; sl < CS; ++sl) {
 #pragma unroll

@@ -109,6 +109,94 @@ __device__ __forceinline__ uint4 fta_tr_frag(const uint16_t* tile, int row, int 
     return make_uint4(l2.x, l2.y, h2.x, h2.y);
 }
 
+// ---------------------------------------------------------------------------
+// Swizzled token tiles filled by LDS DMA.
+// gfx950 global_load_lds_dwordx4 writes 16 bytes per lane straight into LDS at
+// M0 + 16 * lane (wave-uniform base, per-lane global address; measured on
+// gfx950), so a wave instruction fills 1 KB of contiguous LDS and rows cannot
+// be padded.  Rows of QSEG 16-byte slots are stored unpadded with slot j of
+// row r at position j ^ x(r); the loading lane picks its global source from its
+// physical position, the reading lane swizzles its address.
+// x(r) is chosen from measured gfx950 LDS bank behaviour (SQ_LDS_BANK_CONFLICT):
+//  * 16-byte reads (MFMA operand rows) are served 8 lanes at a time over 128
+//    bytes: 8 consecutive rows reading one logical slot need distinct x mod 8;
+//  * ds_read_b64_tr_b16 is served 32 lanes at a time over 256 bytes: 4
+//    consecutive rows x 64 bytes, so bits 2..3 of x must differ across them.
+// Both hold for the x below with 16 or more slots per row (conflict-free),
+// and for 8 slots with the row-pair form; 4 slots need none.  12 and 20 slots
+// use r & 3 (not tuned).
+// ---------------------------------------------------------------------------
+template <int QSEG>
+struct FtaSwz {
+    static_assert(QSEG % 4 == 0, "rows must be a multiple of 4 slots");
+    __device__ static __forceinline__ int x(int r) {
+        if constexpr (QSEG % 16 == 0) {
+            return ((r & 1) << 2) | (((r >> 1) & 1) * 10) | ((r >> 2) & 1);
+        } else if constexpr (QSEG == 8) {
+            const int h = (r >> 1) & 7;
+            return ((h & 1) << 2) | (h >> 1);
+        } else if constexpr (QSEG == 4) {
+            return 0;
+        } else {
+            return r & 3;
+        }
+    }
+    // uint16 offset of logical slot j of row r
+    __device__ static __forceinline__ int off(int r, int j) { return r * QSEG * 8 + ((j ^ x(r)) << 3); }
+    // logical slot held at physical position p of row r
+    __device__ static __forceinline__ int slot(int r, int p) { return p ^ x(r); }
+};
+
+// fta_tr_frag over a swizzled tile of QSEG slots per row.
+template <int QSEG>
+__device__ __forceinline__ uint4 fta_tr_frag_sw(const uint16_t* tile, int k0, int n0, int lane) {
+    const int g = lane >> 4, i = lane & 15;
+    const int r = k0 + 4 * (g >> 1) + (i >> 2);
+    const int col = n0 + 16 * (g & 1) + 4 * (i & 3);
+    const uint16_t* p0 = tile + FtaSwz<QSEG>::off(r, col >> 3) + (col & 7);
+    const uint16_t* p1 = tile + FtaSwz<QSEG>::off(r + 8, col >> 3) + (col & 7);
+    const fta_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (fta_lds_s16x4*)(__attribute__((address_space(3))) uint16_t*)p0);
+    const fta_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (fta_lds_s16x4*)(__attribute__((address_space(3))) uint16_t*)p1);
+    const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+    return make_uint4(l2.x, l2.y, h2.x, h2.y);
+}
+
+// One wave-wide LDS DMA: lane l copies 16 (or 4) bytes from g to lds + 16 * l
+// (or 4 * l).  `lds` must be wave-uniform.  Completion is tracked by vmcnt and
+// waited for explicitly (fta_wait_vmcnt + barrier).  Issued through inline asm
+// so the compiler's wait insertion does not see an LDS write in flight: with
+// the builtin it waits for every outstanding DMA (vmcnt(0)) before each LDS
+// read, which serialises a multi-stage pipeline.  Loads the compiler does track
+// stay correct: DMAs unknown to it only make its own vmcnt waits stricter.
+// An SALU write of M0 needs one wait state before an LDS DMA reads it (the
+// compiler inserts it for its own code, not inside asm): hence the s_nop.
+__device__ __forceinline__ uint32_t fta_lds_addr(const void* lds) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+}
+__device__ __forceinline__ void fta_dma16_at(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
+                 "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void fta_dma4_at(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g),
+                 "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void fta_dma16(const void* g, void* lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(fta_lds_addr(lds)) : "memory", "m0");
+}
+__device__ __forceinline__ void fta_dma4(const void* g, void* lds) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(fta_lds_addr(lds)) : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void fta_wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Status codes returned by every extern "C" entry point (see include/fta.h).
 #define FTA_OK 0
 #define FTA_ERR_ARG 1
