@@ -661,24 +661,32 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
     const int qw = a.QW;
     for (int seg0 = 0; seg0 < a.NC; seg0 += kSeg) {
         const int segn = min(kSeg, a.NC - seg0);
-        // masks: tile t x chunk (seg0 + cl) -> bits over the chunk's 32 queries
-        for (int pi = tid; pi < TT * segn; pi += Sh::NTHR) {
-            const int t = pi / segn, cl = pi - (pi / segn) * segn;
-            const int mt = (wk * TT + t) / Tb;
-            uint32_t bits = 0u;
-            if (mt < a.Mkv) {
-                const int pc = 32 * (seg0 + cl);
-                const int qb_a = pc / a.g;
-                int qb_b = (pc + 31) / a.g;
-                if (qb_b > a.QM - 1) qb_b = a.QM - 1;
-                const uint32_t* srow = a.sel + ((int64_t)bh * a.Mkv + mt) * qw;
-                for (int qb = qb_a; qb <= qb_b; ++qb) {
-                    if ((srow[qb >> 5] >> (qb & 31)) & 1u)
-                        bits |= fta_range_bits(qb * a.g - pc, qb * a.g + a.g - pc);
-                }
-                bits &= fta_range_bits(a.q_pad - pc, a.q_pad + a.N - pc);
+        // masks: tile t x chunk (seg0 + cl) -> bits over the chunk's 32 queries.
+        // A chunk overlaps at most 33 q-blocks, i.e. two bitmap words per tile;
+        // each thread loads its chunk's words for all tiles first (one latency).
+        for (int cl = tid; cl < segn; cl += Sh::NTHR) {
+            const int pc = 32 * (seg0 + cl);
+            const int qb_a = pc / a.g;
+            const int qb_b = min((pc + 31) / a.g, a.QM - 1);
+            const int w_a = qb_a >> 5, w_b = qb_b >> 5;
+            uint32_t w0[TT], w1[TT];
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                const int mt = (wk * TT + t) / Tb;
+                const uint32_t* srow = a.sel + ((int64_t)bh * a.Mkv + min(mt, a.Mkv - 1)) * qw;
+                w0[t] = (mt < a.Mkv) ? srow[w_a] : 0u;
+                w1[t] = (mt < a.Mkv && w_b > w_a) ? srow[w_b] : 0u;
             }
-            sMask[t][cl] = bits;
+            const uint32_t valid = fta_range_bits(a.q_pad - pc, a.q_pad + a.N - pc);
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                uint32_t bits = 0u;
+                for (int qb = qb_a; qb <= qb_b; ++qb) {
+                    const uint32_t w = ((qb >> 5) == w_a) ? w0[t] : w1[t];
+                    if ((w >> (qb & 31)) & 1u) bits |= fta_range_bits(qb * a.g - pc, qb * a.g + a.g - pc);
+                }
+                sMask[t][cl] = bits & valid;
+            }
         }
         __syncthreads();
         int U = 0;

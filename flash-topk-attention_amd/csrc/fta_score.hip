@@ -482,6 +482,297 @@ __global__ __launch_bounds__(256 * (2 / QT), (D > 160) ? 1 : 2) void fta_block_s
 }
 
 // ----------------------------------------------------------------------------
+// Stage 1, software-pipelined variant for 64-key blocks and D in {64, 128}.
+// Numerics are those of fta_block_score_lse_fast_kernel with two query tiles
+// per wave (same running reference R, exact fallback, rebase, tau tracking and
+// summation order: the 32-term tree per block is tree16(keys 0..31) +
+// tree16(keys 32..63), computed here one half at a time).  The schedule differs:
+//  * K blocks are gathered by LDS DMA into four swizzled buffers, up to three
+//    blocks ahead of use, so no staging registers or LDS stores are needed;
+//  * work is pipelined by half blocks (32 keys): the 16 MFMAs of the next half
+//    are issued interleaved with the exp / sum work of the current half
+//    (sched_group_barrier), so a wave keeps the matrix core and the VALU busy
+//    together; only two half-block score sets are live, which keeps two waves
+//    per SIMD;
+//  * the rare exact path recomputes block m's scores from its LDS buffer.
+// ----------------------------------------------------------------------------
+template <int D>
+struct ScorePipeShape {
+    static constexpr int QSEG = D / 8;
+    static constexpr int SLOTS = 64 * QSEG;  // 16-byte slots per K block
+    static constexpr int LQ = SLOTS / 256;   // DMA instructions per wave per block (4 waves)
+    static constexpr int NBUF = 4;
+    static constexpr int BUF_B = SLOTS * 16;
+    static_assert(SLOTS % 256 == 0, "whole DMA instructions per wave");
+};
+
+template <int DT, int D>
+__global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+    int H, int N, int Dreal, int M, int bsz, int pad_head, int pad_tail, float c,
+    float* __restrict__ blk_lse, float* __restrict__ row_lse, int qtiles, int total, int kgroups,
+    int32_t* __restrict__ tau_idx) {
+    using E = Elem<DT>;
+    using Sh = ScorePipeShape<D>;
+    using SW = FtaSwz<Sh::QSEG>;
+    constexpr int KS = D / 16;
+    constexpr int QSEG = Sh::QSEG, LQ = Sh::LQ, NBUF = Sh::NBUF;
+    __shared__ __align__(1024) unsigned char sK[NBUF][Sh::BUF_B];
+
+    const int wg = fta_xcd_remap(blockIdx.x, total);
+    const int bh = wg / qtiles;
+    const int qt = wg - bh * qtiles;
+    const int b = bh / H, h = bh - (bh / H) * H;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hf = lane >> 5;
+    const int qbase = qt * 256 + wave * 64;
+    const uint16_t* qp = q + b * q_sb + h * q_sh;
+    const uint16_t* kp = k + b * k_sb + h * k_sh;
+
+    uint4 qf[2][KS];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int qi = qbase + t * 32 + (lane & 31);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d = ks * 16 + hf * 8;
+            qf[t][ks] = (qi < N && d < Dreal) ? *reinterpret_cast<const uint4*>(qp + (int64_t)qi * q_sn + d)
+                                              : fta_zero4();
+        }
+    }
+    // complete the register loads before the DMA stream (the compiler does not see the DMAs)
+    fta_wait_vmcnt<0>();
+
+    // Per-lane DMA sources within a K block: instruction i of this wave fills the
+    // 1 KB LDS block i * 4 + wave; roff = row * k_sn + column (elements).
+    int roff[LQ];
+#pragma unroll
+    for (int i = 0; i < LQ; ++i) {
+        const int sidx = (i * 4 + wave) * 64 + lane;
+        const int row = sidx / QSEG;
+        int j = SW::slot(row, sidx - row * QSEG);
+        if (j * 8 >= Dreal) j = 0;  // columns past D meet zero q columns
+        roff[i] = row * (int)k_sn + j * 8;
+    }
+    const uint32_t lds0 = fta_lds_addr(&sK[0][0]);
+    auto issue = [&](int m) {
+        const uint32_t sb = lds0 + (m & (NBUF - 1)) * Sh::BUF_B;
+        const int kb = m * 64 - pad_head;
+        if (kb >= 0 && kb + 64 <= N) {
+            const uint16_t* base = kp + (int64_t)kb * k_sn;
+#pragma unroll
+            for (int i = 0; i < LQ; ++i) fta_dma16_at(base + roff[i], sb + (i * 4 + wave) * 1024);
+        } else {  // block at a sequence edge: clamp rows (masked to -inf below)
+#pragma unroll
+            for (int i = 0; i < LQ; ++i) {
+                const int sidx = (i * 4 + wave) * 64 + lane;
+                const int row = sidx / QSEG;
+                int j = SW::slot(row, sidx - row * QSEG);
+                if (j * 8 >= Dreal) j = 0;
+                const int t = min(max(kb + row, 0), N - 1);
+                fta_dma16_at(kp + (int64_t)t * k_sn + j * 8, sb + (i * 4 + wave) * 1024);
+            }
+        }
+    };
+    // scores of keys 32 s .. 32 s + 31 of block m for both query tiles
+    auto mma_half = [&](int m, int s, f32x16 (&acc)[2]) {
+        const uint16_t* base = reinterpret_cast<const uint16_t*>(&sK[m & (NBUF - 1)][0]) + s * 32 * QSEG * 8;
+        const f32x16 zacc = {};
+        uint4 a[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) a[ks] = *reinterpret_cast<const uint4*>(base + SW::off(lane & 31, 2 * ks + hf));
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            acc[0] = E::mma(a[ks], qf[0][ks], ks ? acc[0] : zacc);
+            acc[1] = E::mma(a[ks], qf[1][ks], ks ? acc[1] : zacc);
+        }
+    };
+    auto edge_mask = [&](int m, int s, f32x16 (&acc)[2]) {
+        const int kb = m * 64 - pad_head;
+        if (kb < 0 || kb + 64 > N) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int t = kb + s * 32 + c_row(i, lane);
+                if (t < 0 || t >= N) {
+                    acc[0][i] = -FTA_INF;
+                    acc[1][i] = -FTA_INF;
+                }
+            }
+        }
+    };
+    auto sums16 = [&](const f32x16 (&acc)[2], const float* Rr, float* e) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = acc[t][i];
+            e[t] = fta_sum_exp2<16>(v, c, Rr[t]);
+        }
+    };
+    float R[2] = {-FTA_INF, -FTA_INF}, L[2] = {0.f, 0.f};
+    // One pipeline stage, written in issue order: the MFMAs of half s of block mb
+    // (into dst) interleaved with the exps of src, 32 / KS exps after each MFMA
+    // pair; sched_barrier freezes the order.  The sums use the same 16-term
+    // tree as fta_sum_exp2<16>.
+    auto stage = [&](int mb, int s, f32x16 (&dst)[2], const f32x16 (&src)[2], float* e_out) {
+        const uint16_t* base = reinterpret_cast<const uint16_t*>(&sK[mb & (NBUF - 1)][0]) + s * 32 * QSEG * 8;
+        const f32x16 zacc = {};
+        uint4 a[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) a[ks] = *reinterpret_cast<const uint4*>(base + SW::off(lane & 31, 2 * ks + hf));
+        constexpr int PER = 32 / KS;
+        float ex[2][16];
+#pragma unroll
+        for (int g = 0; g < KS; ++g) {
+            dst[0] = E::mma(a[g], qf[0][g], g ? dst[0] : zacc);
+            dst[1] = E::mma(a[g], qf[1][g], g ? dst[1] : zacc);
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const int idx = g * PER + u, t = idx >> 4, i = idx & 15;
+                ex[t][i] = fta_exp2(fmaf(src[t][i], c, -R[t]));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int w = 1; w < 16; w <<= 1)
+#pragma unroll
+                for (int i = 0; i + w < 16; i += 2 * w) ex[t][i] += ex[t][i + w];
+            e_out[t] = ex[t][0];
+        }
+    };
+
+    float gkey = -FTA_INF, tkey = FTA_INF;
+    int gidx = 0, tidx = 0, curg = -1, next_start = 0;
+    const float adj_head = (pad_head > 0) ? fta_log2((float)bsz / (float)(bsz - pad_head)) : 0.f;
+    const float adj_tail = (pad_tail > 0) ? fta_log2((float)bsz / (float)(bsz - pad_tail)) : 0.f;
+
+#pragma unroll
+    for (int j = 0; j < NBUF - 1; ++j)
+        if (j < M) issue(j);
+    if (M >= 3)
+        fta_wait_vmcnt<2 * LQ>();
+    else if (M == 2)
+        fta_wait_vmcnt<LQ>();
+    else
+        fta_wait_vmcnt<0>();
+    __syncthreads();
+    f32x16 h0[2], h1[2];
+    mma_half(0, 0, h0);
+
+    for (int m = 0; m < M; ++m) {
+        // block m + 1 resident: blocks issued so far = min(M, m + 3)
+        if (m + 1 < M) {
+            if (m + 3 <= M)
+                fta_wait_vmcnt<LQ>();
+            else
+                fta_wait_vmcnt<0>();
+        }
+        __syncthreads();  // block m + 1 visible; every wave is past block m - 1
+        if (m + 3 < M) issue(m + 3);
+
+        float e0[2], e1[2];
+        const int kb = m * 64 - pad_head;
+        if (kb >= 0 && kb + 64 <= N && m + 1 < M) {
+            // interior block: no masking, so both stages are branch-free regions
+            // stage A: MFMAs of half 1 of block m, exps of half 0
+            stage(m, 1, h1, h0, e0);      // MFMAs of half 1 of block m, exps of half 0
+            stage(m + 1, 0, h0, h1, e1);  // MFMAs of half 0 of block m + 1, exps of half 1
+        } else {
+            edge_mask(m, 0, h0);
+            mma_half(m, 1, h1);
+            sums16(h0, R, e0);
+            edge_mask(m, 1, h1);
+            if (m + 1 < M) mma_half(m + 1, 0, h0);
+            sums16(h1, R, e1);
+        }
+        float tot[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const float part = e0[t] + e1[t];
+            tot[t] = part + fta_xor32(part);
+        }
+        const bool bad = !(tot[0] < 0x1p100f) || !(tot[1] < 0x1p100f);
+        if (__ballot(bad) != 0ull) {
+            // exact path: reference = this block's max (scores recomputed from LDS)
+            f32x16 x0[2], x1[2];
+            mma_half(m, 0, x0);
+            mma_half(m, 1, x1);
+            edge_mask(m, 0, x0);
+            edge_mask(m, 1, x1);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                float mx = x0[t][0];
+#pragma unroll
+                for (int i = 1; i < 16; ++i) mx = fmaxf(mx, x0[t][i]);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mx = fmaxf(mx, x1[t][i]);
+                mx = fmaxf(mx, fta_xor32(mx));
+                const float Rn = (mx == -FTA_INF) ? 0.f : mx * c;
+                L[t] = (L[t] > 0.f) ? L[t] * fta_exp2(R[t] - Rn) : 0.f;
+                R[t] = Rn;
+            }
+            float f0[2], f1[2];
+            sums16(x0, R, f0);
+            sums16(x1, R, f1);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const float part = f0[t] + f1[t];
+                tot[t] = part + fta_xor32(part);
+            }
+        }
+        float lse_b[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            lse_b[t] = (tot[t] > 0.f) ? R[t] + fta_log2(tot[t]) : -FTA_INF;
+            L[t] += tot[t];
+            if (tot[t] > 0x1p40f) {
+                const float Rn = lse_b[t];
+                L[t] *= fta_exp2(R[t] - Rn);
+                R[t] = Rn;
+            }
+        }
+        // lane owns query (lane & 31) of tile (lane >> 5)
+        const int qi = qbase + lane;
+        const float mine = (lane >= 32) ? lse_b[1] : lse_b[0];
+        if (qi < N) blk_lse[((int64_t)bh * M + m) * N + qi] = mine;
+        if (kgroups > 0) {
+            float key = mine;
+            if (m == 0) key += adj_head;
+            if (m == M - 1) key += adj_tail;
+            if (m == next_start) {
+                if (curg >= 0 && gkey < tkey) {
+                    tkey = gkey;
+                    tidx = gidx;
+                }
+                ++curg;
+                next_start = ((curg + 1) * M + kgroups - 1) / kgroups;  // first block of group curg + 1
+                gkey = key;
+                gidx = m;
+            } else if (key > gkey) {
+                gkey = key;
+                gidx = m;
+            }
+        }
+    }
+
+    const int qi = qbase + lane;
+    if (qi < N) {
+        const bool t1 = lane >= 32;
+        const float Rr = t1 ? R[1] : R[0];
+        const float Lr = t1 ? L[1] : L[0];
+        row_lse[(int64_t)bh * N + qi] = (Lr > 0.f) ? Rr + fta_log2(Lr) : -FTA_INF;
+        if (kgroups > 0) {
+            if (curg >= 0 && gkey < tkey) tidx = gidx;
+            tau_idx[(int64_t)bh * N + qi] = tidx;
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
 // Stage 2a: materialise scores[bh][n][m] = 2^{lse2[bh][m][n] - lse2[bh][n]}.
 // 64 x 64 tiles transposed through LDS.
 // ----------------------------------------------------------------------------
@@ -756,8 +1047,15 @@ int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D
     const int qtiles = (N + 255) / 256;
     const int total = qtiles * B * H;
     const float c = scale * 1.4426950408889634f;
+    // the pipelined kernel keeps 64-row offsets (row * k token stride) in 32-bit registers
+    const bool k_sn_ok = ks[2] >= 0 && ks[2] <= (1 << 24);
 #define FTA_LAUNCH_SCORE(DK)                                                                               \
-    if (bsz <= 64)                                                                                         \
+    if (bsz == 64 && (DK == 64 || DK == 128) && k_sn_ok)                                                   \
+        hipLaunchKernelGGL((fta_block_score_lse_pipe_kernel<DT, (DK == 64) ? 64 : 128>), dim3(total),     \
+                           dim3(256), 0, st, (const uint16_t*)q, (const uint16_t*)k, qs[0], qs[1], qs[2],  \
+                           ks[0], ks[1], ks[2], H, N, D, M, bsz, pad_head, pad_tail, c, blk_lse, row_lse,  \
+                           qtiles, total, kgroups, tau);                                                   \
+    else if (bsz <= 64)                                                                                    \
         hipLaunchKernelGGL((fta_block_score_lse_fast_kernel<DT, DK, (DK > 128) ? 1 : 2>), dim3(total),    \
                            dim3(256 * (2 / ((DK > 128) ? 1 : 2))), 0, st,                                \
                            (const uint16_t*)q, (const uint16_t*)k, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], H, \
