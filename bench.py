@@ -222,7 +222,7 @@ def main():
                    "global_batch": B, "seq_len": N, "heads": H, "head_dim": D, "parallelism": "none"},
         "stage_ms": {k2: round(v2, 3) for k2, v2 in stage.items()},
         "flops": {"score": f_score, "fwd": f_fwd, "bwd_10DP": f_bwd, "P_pairs": P},
-        "roofline": {"bound": "mfma", "kernel": "fta_block_score_lse_fast_kernel", "achieved": round(achieved, 2),
+        "roofline": {"bound": "mfma", "kernel": "fta_block_score_lse_pipe_kernel", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "kernel_ms": round(k_ms, 3),
                      "traffic": SCORE_TRAFFIC_BYTES if (B, N, H, D, b) == (1, 32768, 32, 128, 64) else None,

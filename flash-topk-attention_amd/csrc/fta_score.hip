@@ -614,8 +614,11 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     float R[2] = {-FTA_INF, -FTA_INF}, L[2] = {0.f, 0.f};
     // One pipeline stage, written in issue order: the MFMAs of half s of block mb
     // (into dst) interleaved with the exps of src, 32 / KS exps after each MFMA
-    // pair; sched_barrier freezes the order.  The sums use the same 16-term
-    // tree as fta_sum_exp2<16>.
+    // pair.  The sums use the same 16-term tree as fta_sum_exp2<16>.
+    // The order is pinned with empty volatile asm statements (kept in program
+    // order by the compiler): group g's K fragment and a scalar copy of the
+    // scale used by its exps pass through one, and its exp / add results feed
+    // the next group's, so each group's MFMAs, exps and adds stay in their window.
     auto stage = [&](int mb, int s, f32x16 (&dst)[2], const f32x16 (&src)[2], float* e_out) {
         const uint16_t* base = reinterpret_cast<const uint16_t*>(&sK[mb & (NBUF - 1)][0]) + s * 32 * QSEG * 8;
         const f32x16 zacc = {};
@@ -626,23 +629,38 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
         float ex[2][16];
 #pragma unroll
         for (int g = 0; g < KS; ++g) {
-            dst[0] = E::mma(a[g], qf[0][g], g ? dst[0] : zacc);
-            dst[1] = E::mma(a[g], qf[1][g], g ? dst[1] : zacc);
+            typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+            u32x4v agv = __builtin_bit_cast(u32x4v, a[g]);
+            float cg = c;  // a scalar copy: the group's exps depend on it
+            asm volatile("" : "+v"(agv), "+s"(cg));
+            const uint4 ag = __builtin_bit_cast(uint4, agv);
+            dst[0] = E::mma(ag, qf[0][g], g ? dst[0] : zacc);
+            dst[1] = E::mma(ag, qf[1][g], g ? dst[1] : zacc);
 #pragma unroll
             for (int u = 0; u < PER; ++u) {
                 const int idx = g * PER + u, t = idx >> 4, i = idx & 15;
-                ex[t][i] = fta_exp2(fmaf(src[t][i], c, -R[t]));
+                ex[t][i] = fta_exp2(fmaf(src[t][i], cg, -R[t]));
             }
-            __builtin_amdgcn_sched_barrier(0);
+            // tree adds whose subtree is complete after this group (same tree and
+            // order as fta_sum_exp2<16>: level w adds e[i] += e[i + w], i % 2w == 0)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int w = 1; w < 16; w <<= 1)
+#pragma unroll
+                    for (int i = 0; i + w < 16; i += 2 * w)
+                        if ((t * 16 + i + 2 * w - 1) / PER == g) {
+                            ex[t][i] += ex[t][i + w];
+                            asm volatile("" ::"v"(ex[t][i]));
+                        }
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const int idx = g * PER + u, t = idx >> 4, i = idx & 15;
+                if (i & 1) asm volatile("" ::"v"(ex[t][i]));  // odd leaves are consumed by level-1 adds
+            }
         }
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-#pragma unroll
-            for (int w = 1; w < 16; w <<= 1)
-#pragma unroll
-                for (int i = 0; i + w < 16; i += 2 * w) ex[t][i] += ex[t][i + w];
-            e_out[t] = ex[t][0];
-        }
+        e_out[0] = ex[0][0];
+        e_out[1] = ex[1][0];
     };
 
     float gkey = -FTA_INF, tkey = FTA_INF;
@@ -663,7 +681,7 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     f32x16 h0[2], h1[2];
     mma_half(0, 0, h0);
 
-    for (int m = 0; m < M; ++m) {
+    auto block = [&](int m) {
         // block m + 1 resident: blocks issued so far = min(M, m + 3)
         if (m + 1 < M) {
             if (m + 3 <= M)
@@ -686,7 +704,9 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
             mma_half(m, 1, h1);
             sums16(h0, R, e0);
             edge_mask(m, 1, h1);
-            if (m + 1 < M) mma_half(m + 1, 0, h0);
+            if (m + 1 < M) {
+                mma_half(m + 1, 0, h0);
+            }
             sums16(h1, R, e1);
         }
         float tot[2];
@@ -757,7 +777,11 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
                 gidx = m;
             }
         }
-    }
+    };
+    // every block but the last always produces the next block's half 0, so the
+    // loop-carried scores are written on all paths (no register copies)
+    for (int m = 0; m + 1 < M; ++m) block(m);
+    block(M - 1);
 
     const int qi = qbase + lane;
     if (qi < N) {
