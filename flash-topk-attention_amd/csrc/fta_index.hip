@@ -238,26 +238,35 @@ __global__ __launch_bounds__(256) void fta_delta_kernel(const uint16_t* __restri
                                                         int64_t o_sn, const uint16_t* __restrict__ dout,
                                                         int64_t d_sb, int64_t d_sh, int64_t d_sn, int B, int H,
                                                         int N, int D, float* __restrict__ delta) {
+    // 16 lanes per (b, n, h) row: each pass reads 256 contiguous bytes of o and
+    // of dO per row (8 elements per lane); partial sums meet in a 16-lane tree
     using E = Elem<DT>;
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (b, n, h)
-    if (gid >= (int64_t)B * N * H) return;
-    const int h = (int)(gid % H);
-    const int64_t bn = gid / H;
-    const int n = (int)(bn % N), b = (int)(bn / N);
-    const uint16_t* op = o + b * o_sb + h * o_sh + (int64_t)n * o_sn;
-    const uint16_t* dp = dout + b * d_sb + h * d_sh + (int64_t)n * d_sn;
+    const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;  // (b, n, h)
+    const int sub = threadIdx.x & 15;
+    const bool valid = row < (int64_t)B * N * H;
     float acc = 0.f;
-    for (int d = 0; d < D; d += 8) {
-        const uint4 a = *reinterpret_cast<const uint4*>(op + d);
-        const uint4 c = *reinterpret_cast<const uint4*>(dp + d);
-        const uint32_t av[4] = {a.x, a.y, a.z, a.w}, cv[4] = {c.x, c.y, c.z, c.w};
+    int b = 0, n = 0, h = 0;
+    if (valid) {
+        h = (int)(row % H);
+        const int64_t bn = row / H;
+        n = (int)(bn % N);
+        b = (int)(bn / N);
+        const uint16_t* op = o + b * o_sb + h * o_sh + (int64_t)n * o_sn;
+        const uint16_t* dp = dout + b * d_sb + h * d_sh + (int64_t)n * d_sn;
+        for (int d = sub * 8; d < D; d += 128) {
+            const uint4 a = *reinterpret_cast<const uint4*>(op + d);
+            const uint4 c = *reinterpret_cast<const uint4*>(dp + d);
+            const uint32_t av[4] = {a.x, a.y, a.z, a.w}, cv[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            acc = fmaf(E::to_f32((uint16_t)(av[e] & 0xffffu)), E::to_f32((uint16_t)(cv[e] & 0xffffu)), acc);
-            acc = fmaf(E::to_f32((uint16_t)(av[e] >> 16)), E::to_f32((uint16_t)(cv[e] >> 16)), acc);
+            for (int e = 0; e < 4; ++e) {
+                acc = fmaf(E::to_f32((uint16_t)(av[e] & 0xffffu)), E::to_f32((uint16_t)(cv[e] & 0xffffu)), acc);
+                acc = fmaf(E::to_f32((uint16_t)(av[e] >> 16)), E::to_f32((uint16_t)(cv[e] >> 16)), acc);
+            }
         }
     }
-    delta[((int64_t)b * H + h) * N + n] = acc;
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1) acc += __shfl_xor(acc, w, 16);
+    if (valid && sub == 0) delta[((int64_t)b * H + h) * N + n] = acc;
 }
 
 namespace fta {
@@ -346,7 +355,8 @@ int fta_preprocess_delta(const void* o, const int64_t* o_strides, const void* do
     FTA_TRY_BEGIN
     if (B <= 0 || H <= 0 || N <= 0 || D <= 0 || D % 8) return fta::arg_error("preprocess_delta: bad dims");
     const int64_t n = (int64_t)B * N * H;
-    const unsigned grid = (unsigned)((n + 255) / 256);
+    if (n > ((int64_t)1 << 35)) return fta::unsupported("preprocess_delta: too many rows");
+    const unsigned grid = (unsigned)((n * 16 + 255) / 256);  // 16 lanes per row
     hipStream_t st = (hipStream_t)stream;
     if (dtype == FTA_DTYPE_BF16)
         hipLaunchKernelGGL((fta_delta_kernel<FTA_DTYPE_BF16>), dim3(grid), dim3(256), 0, st, (const uint16_t*)o,

@@ -849,7 +849,8 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
     int N, int rows, int M, int m_out, int bsz, int pad_head, int pad_tail, float threshold,
     int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg,
     const int32_t* __restrict__ tau_idx) {
-    constexpr int CAP = 16;
+    constexpr int UNR = 8;              // blocks loaded per batch
+    constexpr int CAP = 16 + UNR;       // a batch starts with at most CAP - UNR parked candidates
     __shared__ float cand_v[4][CAP][64];
     __shared__ int cand_i[4][CAP][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -883,9 +884,14 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
     // bound is relaxed by 2^-20 relative so that the exact (avg, index) test
     // below decides every candidate.
     float thr_norm = -FTA_INF;
+    // MODE 1 tests x = lse2 - row_lse2 against log2(thr_norm) instead of
+    // 2^x >= thr_norm, with a 2^-12 margin far above exp2 / log2 rounding, so
+    // the test stays conservative and exp2 runs only for candidates.
+    float thr_log = -FTA_INF;
     auto set_thr = [&]() {
         const float t = tv * (float)bsz;
         thr_norm = t - fabsf(t) * 9.5367431640625e-07f;
+        thr_log = (thr_norm > 0.f) ? fta_log2(thr_norm) - 2.44140625e-04f : -FTA_INF;
     };
     if (MODE == 1 && tau_idx != nullptr && active) {
         const int t0 = tau_idx[row];
@@ -929,23 +935,32 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
         set_thr();
     };
 
-    for (int m = 0; m < M; ++m) {
-        float raw;
-        if (MODE == 0) {
-            raw = active ? src[m * stride_m] : 0.f;
-        } else {
-            raw = active ? fta_exp2(src[(int64_t)m * N] - rl) : 0.f;
+    for (int m0 = 0; m0 < M; m0 += UNR) {
+        float xs[UNR];
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int m = min(m0 + u, M - 1);
+            xs[u] = active ? ((MODE == 0) ? src[m * stride_m] : src[(int64_t)m * N]) : 0.f;
         }
-        const bool edge = (m == 0 && pad_head > 0) || (m == M - 1 && pad_tail > 0);
-        if (active && (raw >= thr_norm || edge)) {
-            const float avg = raw / (float)fta_valid_count(m, M, bsz, pad_head, pad_tail);
-            if (fta_better(avg, m, tv, ti)) {
-                cand_v[wave][cnt][lane] = avg;
-                cand_i[wave][cnt][lane] = m;
-                ++cnt;
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int m = m0 + u;
+            const bool edge = (m == 0 && pad_head > 0) || (m == M - 1 && pad_tail > 0);
+            const float x = (MODE == 0) ? xs[u] : xs[u] - rl;
+            const bool pass = (MODE == 0) ? (x >= thr_norm) : (x >= thr_log);
+            if (active && m < M && (pass || edge)) {
+                const float raw = (MODE == 0) ? x : fta_exp2(x);
+                if (raw >= thr_norm || edge) {
+                    const float avg = raw / (float)fta_valid_count(m, M, bsz, pad_head, pad_tail);
+                    if (fta_better(avg, m, tv, ti)) {
+                        cand_v[wave][cnt][lane] = avg;
+                        cand_i[wave][cnt][lane] = m;
+                        ++cnt;
+                    }
+                }
             }
         }
-        if (__ballot(cnt == CAP) != 0ull) flush();
+        if (__ballot(cnt > CAP - UNR) != 0ull) flush();
     }
     flush();
 
