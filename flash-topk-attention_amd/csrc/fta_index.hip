@@ -36,6 +36,8 @@ __device__ __forceinline__ int fta_block_scan256(int v, int* s_tmp, int* total) 
 //   acc[id] += score over the slice's g*K (id, score) pairs in (row, slot) order,
 //   positive entries sorted by (score desc, id asc), first W kept.
 // ----------------------------------------------------------------------------
+constexpr int kMergeChunk = 1024;  // staged (id, score) entries per step
+
 __global__ __launch_bounds__(256) void fta_qblock_merge_kernel(const int32_t* __restrict__ idx,
                                                                const float* __restrict__ scr, int g, int K, int Mt,
                                                                int W, int32_t* __restrict__ out_idx,
@@ -44,8 +46,10 @@ __global__ __launch_bounds__(256) void fta_qblock_merge_kernel(const int32_t* __
     __shared__ float acc[4096];
     __shared__ unsigned long long keys[4096];
     __shared__ int s_tmp[8];
-    // volatile: the clash test below must really re-read LDS after the store,
-    // and the fallback loop must see the previous lane's update.
+    __shared__ int s_id[kMergeChunk];
+    __shared__ float s_sc[kMergeChunk];
+    // volatile: the owner test must re-read LDS after the atomic, and each
+    // round must see the previous round's sums.
     volatile int* owner = reinterpret_cast<volatile int*>(keys);  // reused before the sort
     volatile float* vacc = acc;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -56,30 +60,38 @@ __global__ __launch_bounds__(256) void fta_qblock_merge_kernel(const int32_t* __
     for (int m = tid; m < Mt; m += 256) acc[m] = 0.f;
     __syncthreads();
 
-    if (wave == 0) {
-        for (int r = 0; r < g; ++r) {
-            for (int j0 = 0; j0 < K; j0 += 64) {
+    // Entries are consumed in position order (row-major (row, slot)), which
+    // keeps every id's fp32 sum in (row, slot) order.  All threads stage a
+    // chunk of entries in LDS; wave 0 then adds 64 consecutive entries per
+    // step (duplicates within a step are serialised in lane = position order).
+    const int total = g * K;
+    for (int e0 = 0; e0 < total; e0 += kMergeChunk) {
+        const int n = min(kMergeChunk, total - e0);
+        for (int e = tid; e < n; e += 256) {
+            s_id[e] = ip[e0 + e];
+            s_sc[e] = sp[e0 + e];
+        }
+        __syncthreads();
+        if (wave == 0) {
+            for (int j0 = 0; j0 < n; j0 += 64) {
                 const int j = j0 + lane;
-                int id = -1;
-                float s = 0.f;
-                if (j < K) {
-                    id = ip[r * K + j];
-                    s = sp[r * K + j];
-                }
-                const bool ok = id >= 0 && id < Mt;
-                if (ok) owner[id] = lane;
-                const bool clash = ok && owner[id] != lane;
-                if (__ballot(clash) == 0ull) {
-                    if (ok) vacc[id] = __fadd_rn(vacc[id], s);
-                } else {
-                    for (int l = 0; l < 64; ++l) {
-                        if (lane == l && ok) vacc[id] = __fadd_rn(vacc[id], s);
+                const int id = (j < n) ? s_id[j] : -1;
+                const float sc = (j < n) ? s_sc[j] : 0.f;
+                // rounds: in each, the lowest remaining lane of every id adds its
+                // entry, so an id's entries are added in lane (= position) order
+                bool pending = id >= 0 && id < Mt;
+                while (__ballot(pending) != 0ull) {
+                    if (pending) owner[id] = 64;
+                    if (pending) atomicMin(const_cast<int*>(&owner[id]), lane);
+                    if (pending && owner[id] == lane) {
+                        vacc[id] = __fadd_rn(vacc[id], sc);
+                        pending = false;
                     }
                 }
             }
         }
+        __syncthreads();
     }
-    __syncthreads();
 
     // compact positive entries in id order
     int P = 0;

@@ -849,8 +849,9 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
     int N, int rows, int M, int m_out, int bsz, int pad_head, int pad_tail, float threshold,
     int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg,
     const int32_t* __restrict__ tau_idx) {
-    constexpr int UNR = 8;              // blocks loaded per batch
-    constexpr int CAP = 16 + UNR;       // a batch starts with at most CAP - UNR parked candidates
+    constexpr int LDB = 32;             // blocks loaded per batch
+    constexpr int UNR = 8;              // blocks tested between candidate-list checks
+    constexpr int CAP = 16 + UNR;       // a sub-batch starts with at most CAP - UNR parked candidates
     __shared__ float cand_v[4][CAP][64];
     __shared__ int cand_i[4][CAP][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -935,32 +936,36 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
         set_thr();
     };
 
-    for (int m0 = 0; m0 < M; m0 += UNR) {
-        float xs[UNR];
+    for (int m1 = 0; m1 < M; m1 += LDB) {
+        float xs[LDB];
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int m = min(m0 + u, M - 1);
+        for (int u = 0; u < LDB; ++u) {
+            const int m = min(m1 + u, M - 1);
             xs[u] = active ? ((MODE == 0) ? src[m * stride_m] : src[(int64_t)m * N]) : 0.f;
         }
 #pragma unroll
-        for (int u = 0; u < UNR; ++u) {
-            const int m = m0 + u;
-            const bool edge = (m == 0 && pad_head > 0) || (m == M - 1 && pad_tail > 0);
-            const float x = (MODE == 0) ? xs[u] : xs[u] - rl;
-            const bool pass = (MODE == 0) ? (x >= thr_norm) : (x >= thr_log);
-            if (active && m < M && (pass || edge)) {
-                const float raw = (MODE == 0) ? x : fta_exp2(x);
-                if (raw >= thr_norm || edge) {
-                    const float avg = raw / (float)fta_valid_count(m, M, bsz, pad_head, pad_tail);
-                    if (fta_better(avg, m, tv, ti)) {
-                        cand_v[wave][cnt][lane] = avg;
-                        cand_i[wave][cnt][lane] = m;
-                        ++cnt;
+        for (int sb = 0; sb < LDB; sb += UNR) {
+            if (m1 + sb >= M) break;
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) {
+                const int m = m1 + sb + u;
+                const bool edge = (m == 0 && pad_head > 0) || (m == M - 1 && pad_tail > 0);
+                const float x = (MODE == 0) ? xs[sb + u] : xs[sb + u] - rl;
+                const bool pass = (MODE == 0) ? (x >= thr_norm) : (x >= thr_log);
+                if (active && m < M && (pass || edge)) {
+                    const float raw = (MODE == 0) ? x : fta_exp2(x);
+                    if (raw >= thr_norm || edge) {
+                        const float avg = raw / (float)fta_valid_count(m, M, bsz, pad_head, pad_tail);
+                        if (fta_better(avg, m, tv, ti)) {
+                            cand_v[wave][cnt][lane] = avg;
+                            cand_i[wave][cnt][lane] = m;
+                            ++cnt;
+                        }
                     }
                 }
             }
+            if (__ballot(cnt > CAP - UNR) != 0ull) flush();
         }
-        if (__ballot(cnt > CAP - UNR) != 0ull) flush();
     }
     flush();
 
