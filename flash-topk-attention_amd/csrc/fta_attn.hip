@@ -236,7 +236,6 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
             const int m = seg0 + ml;
             const int kb = m * a.kvb - a.kv_pad + ch * 64;
             const int rem = a.kvb - ch * 64;
-            const bool two = rem > 32;
             uint32_t mk[TPW];
             bool anyt = false;
 #pragma unroll
@@ -253,23 +252,19 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
 #pragma unroll
                         for (int i = 0; i < 16; ++i) s[tt][sb][i] = 0.f;
                 const uint16_t* kbase = &sK[buf][0];
+                // both 32-key halves in one loop: two independent MFMA chains
+                // (keys past a short chunk are zero rows, masked below)
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
-                    const uint4 a0 =
-                        *reinterpret_cast<const uint4*>(kbase + (lane & 31) * KROW + ks * 16 + hf * 8);
+                    const uint4 a0 = *reinterpret_cast<const uint4*>(kbase + (lane & 31) * KROW + ks * 16 + hf * 8);
+                    const uint4 a1 =
+                        *reinterpret_cast<const uint4*>(kbase + (32 + (lane & 31)) * KROW + ks * 16 + hf * 8);
 #pragma unroll
                     for (int tt = 0; tt < TPW; ++tt)
-                        if (mk[tt]) s[tt][0] = E::mma(a0, qf[tt][ks], s[tt][0]);
-                }
-                if (two) {
-#pragma unroll
-                    for (int ks = 0; ks < KS; ++ks) {
-                        const uint4 a1 = *reinterpret_cast<const uint4*>(kbase + (32 + (lane & 31)) * KROW +
-                                                                         ks * 16 + hf * 8);
-#pragma unroll
-                        for (int tt = 0; tt < TPW; ++tt)
-                            if (mk[tt]) s[tt][1] = E::mma(a1, qf[tt][ks], s[tt][1]);
-                    }
+                        if (mk[tt]) {
+                            s[tt][0] = E::mma(a0, qf[tt][ks], s[tt][0]);
+                            s[tt][1] = E::mma(a1, qf[tt][ks], s[tt][1]);
+                        }
                 }
                 const bool kmask = kb < 0 || kb + 64 > a.N || rem < 64;
 #pragma unroll
@@ -316,10 +311,8 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
                     }
                     l_run[tt] += ls;
                     const uint16_t* vbase = &sV[buf][0];
-                    const int nks = two ? 4 : 2;
 #pragma unroll
                     for (int ks = 0; ks < 4; ++ks) {
-                        if (ks >= nks) break;
 #pragma unroll
                         for (int dt = 0; dt < DT32; ++dt) {
                             const uint4 vf = fta_tr_frag(vbase, KROW, ks * 16, dt * 32, lane);
