@@ -1,0 +1,195 @@
+"""GPU parity at the full sizes of the benchmark configurations (C2-C5).
+
+The whole pipeline (score -> top-k -> merge -> sparse attention forward, and
+backward where the configuration trains) runs on the GPU at the real shape.
+The CPU oracle, which cannot afford the full shapes, checks sampled slices:
+
+* block scores of sampled query rows of sampled heads (float64 oracle);
+* top-k of those rows: bit-exact against the oracle fed the GPU's fp32 scores,
+  and against the float64 scores up to near-ties (gap < 1e-6);
+* fused top-k (no score tensor) == unfused, bit-exact, for every row;
+* merge: bit-exact against the oracle fed the GPU's top-k, on sampled q-blocks;
+* o / lse / dQ on sampled q-blocks, dK / dV on a sampled KV block per head
+  (all q-blocks that selected it), with the tolerances of test_gpu_parity.py.
+
+Size-independent properties are checked everywhere: merged lists are a
+prefix of distinct valid ids followed by -1, counts equal the prefix length,
+rows of the score tensor sum to 1.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import fta_oracle as O
+from _helpers import assert_close_frac, check_topk_gap, np32, say
+
+pytestmark = pytest.mark.gpu
+
+fta = pytest.importorskip("flash_topk_attn_v2")
+
+
+def _iid(shape, seed, dtype, scale=1.0):
+    # generated in fp32 on the CPU, then cast and moved (benchmark recipe)
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype).cuda()
+
+
+def _peaked(B, N, H, D, seed):
+    """Config 3 data: block-centred keys, queries near one of 8 blocks per 1024-query segment."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    C, b = H * D, 64
+    M = N // b
+    cent = torch.randn(B, M, C, generator=g)
+    k = 0.3 * torch.randn(B, N, C, generator=g) + cent.repeat_interleave(b, dim=1)
+    nseg = N // 1024
+    choice = torch.stack([torch.randperm(M, generator=g)[:8] for _ in range(B * nseg)]).view(B, nseg, 8)
+    pick_slot = torch.randint(0, 8, (B, N), generator=g)
+    seg = torch.arange(N) // 1024
+    pick = torch.gather(choice[:, seg, :], 2, pick_slot.unsqueeze(-1)).squeeze(-1)
+    q = 0.3 * torch.randn(B, N, C, generator=g) + torch.gather(cent, 1, pick.unsqueeze(-1).expand(B, N, C))
+    v = torch.randn(B, N, C, generator=g)
+    return (x.to(torch.bfloat16).cuda() for x in (q, k, v))
+
+
+def _head(x, h, D):
+    """[B, N, H*D] -> numpy float32 [B, N, D] of head h."""
+    return np32(x[:, :, h * D:(h + 1) * D])
+
+
+def _check_merged_structure(merged, counts, M):
+    m = merged.cpu().numpy()
+    c = counts.cpu().numpy()
+    valid = m >= 0
+    # valid ids form a prefix: no valid entry after the first -1
+    assert not np.any(valid[..., 1:] & ~valid[..., :-1]), "merged lists are not a prefix of valid ids"
+    np.testing.assert_array_equal(valid.sum(-1), c)
+    assert m.max() < M
+    # distinct ids per list
+    s = np.sort(np.where(valid, m, -1 - np.arange(m.shape[-1])), axis=-1)
+    assert not np.any((s[..., 1:] == s[..., :-1]) & (s[..., 1:] >= 0)), "duplicate ids in a merged list"
+
+
+CONFIGS = {
+    # name: B, N, H, D, dtype, b, topk, thr, g, W, score/kv padding, q padding, data, backward
+    "C2g1": (2, 8192, 16, 64, torch.float16, 64, 16, 1.0, 1, 16, (0, 0), (0, 0), "iid", False),
+    "C2g32": (2, 8192, 16, 64, torch.float16, 64, 16, 1.0, 32, 512, (0, 0), (0, 0), "iid", False),
+    "C4": (2, 10000, 12, 64, torch.float16, 64, 8, 1.0, 16, None, (24, 24), (0, 0), "iid", True),
+    "C5": (1, 16384, 16, 128, torch.bfloat16, 64, 16, 1.0, 32, 512, (0, 0), (0, 0), "iid_scaled", True),
+    "C3": (1, 32768, 32, 128, torch.bfloat16, 64, 16, 0.9, 32, 256, (0, 0), (0, 0), "peaked", True),
+}
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_config_full_size(name):
+    B, N, H, D, dt, b, topk, thr, g, W, pad, qpad, data, bwd = CONFIGS[name]
+    say(f"[config {name}] B{B} N{N} H{H} D{D} {dt} b{b} topk{topk} thr{thr} g{g} W{W} pad{pad}")
+    seed = {"C2g1": 1, "C2g32": 1, "C4": 4, "C5": 5, "C3": 2}[name]
+    C = H * D
+    if data == "peaked":
+        q, k, v = _peaked(B, N, H, D, seed)
+    else:
+        sc = 1.0 / math.sqrt(D) if data == "iid_scaled" else 1.0
+        q, k, v = (_iid((B, N, C), seed * 10 + i, dt, sc) for i in range(3))
+    rng = np.random.default_rng(seed)
+
+    # ---- scoring + top-k (fused and unfused) ----
+    fi, fr, fa = fta.flash_topk_score(q, k, H, b, topk, pad, thr)
+    scores = fta.flash_block_score(q, k, H, b, pad)
+    ui, ur, ua = fta.flash_topk_select(scores, thr, topk, b, pad)
+    torch.cuda.synchronize()
+    assert torch.equal(fi, ui) and torch.equal(fr, ur) and torch.equal(fa, ua), "fused != unfused top-k"
+    M = scores.shape[-1]
+    rows_sum = scores.sum(-1)
+    assert torch.allclose(rows_sum, torch.ones_like(rows_sum), rtol=1e-4, atol=1e-4)
+
+    heads = sorted({0, H - 1})
+    bs = sorted({0, B - 1})
+    rows = np.sort(rng.choice(N, size=48, replace=False))
+    rows = np.unique(np.concatenate([rows, [0, N - 1]]))
+    for bb in bs:
+        for h in heads:
+            qh, kh = _head(q[bb:bb + 1], h, D), _head(k[bb:bb + 1], h, D)
+            s64 = O.block_score(qh, kh, 1, b, pad, rows=rows)[0, 0]  # [R, M]
+            gs = scores[bb, h, torch.from_numpy(rows).cuda()].cpu().numpy()
+            np.testing.assert_allclose(gs, s64, rtol=2e-4, atol=2e-7)
+            ri, rr, ra = O.topk_select(gs[None, None], thr, topk, b, pad)
+            got = fi[bb, h, torch.from_numpy(rows).cuda()].cpu().numpy()
+            np.testing.assert_array_equal(got, ri[0, 0])
+            if thr >= 1.0:
+                # against float64 scores (with a threshold below 1 the fp32 / float64
+                # cumulative sums may cut one position apart at a sum that lands on
+                # the threshold; the bit-exact check above covers those rows)
+                vc = O.valid_counts(M, b, pad).astype(np.float64)
+                ri64, _, _ = O.topk_select(s64[None, None].astype(np.float32), thr, topk, b, pad)
+                bad, nd = check_topk_gap(got[None, None], (s64 / vc)[None, None], ri64)
+                assert bad == 0, f"{bad} of {nd} top-k indices differ beyond the 1e-6 gap rule"
+    del scores
+
+    # ---- merge ----
+    merged, counts, Wm = fta.build_qblock_topk_indices(fi, g, qpad, fa, W)
+    torch.cuda.synchronize()
+    QM = merged.shape[2]
+    _check_merged_structure(merged, counts, M)
+    nsb = int(fi.max().item()) + 1
+    qms = np.unique(np.concatenate([rng.choice(QM, size=12, replace=False), [0, QM - 1]]))
+    for bb in bs:
+        for h in heads:
+            idx_np = fi[bb:bb + 1, h:h + 1].cpu().numpy()
+            avg_np = fa[bb:bb + 1, h:h + 1].cpu().numpy()
+            if qpad != (0, 0):
+                idx_np = np.pad(idx_np, ((0, 0), (0, 0), qpad, (0, 0)), constant_values=-1)
+                avg_np = np.pad(avg_np, ((0, 0), (0, 0), qpad, (0, 0)))
+            sel_rows = np.concatenate([np.arange(qm * g, qm * g + g) for qm in qms])
+            ri, _ = O.qblock_merge(idx_np[:, :, sel_rows], avg_np[:, :, sel_rows], g, Wm, nsb)
+            np.testing.assert_array_equal(merged[bb, h, torch.from_numpy(qms).cuda()].cpu().numpy(), ri[0, 0])
+
+    # ---- sparse attention forward (+ backward) ----
+    if bwd:
+        for t in (q, k, v):
+            t.requires_grad_(True)
+    o, lse = fta.flash_topk_attn(q, k, v, merged, counts, H, g, b, None, None, pad, qpad)
+    if bwd:
+        do = _iid((B, N, C), seed * 10 + 7, o.dtype)
+        o.backward(do)
+    torch.cuda.synchronize()
+    mg = merged.cpu().numpy()
+    for bb in bs:
+        for h in heads:
+            qh, kh, vh = (_head(x[bb:bb + 1], h, D) for x in (q, k, v))
+            mh = mg[bb:bb + 1, h:h + 1]
+            trip = [(0, 0, int(qm)) for qm in qms]
+            ro, rl = O.sparse_attn(qh, kh, vh, mh, 1, g, b, None, qpad, pad, qblocks=trip)
+            rws = np.concatenate([np.arange(max(0, qm * g - qpad[0]), min(N, qm * g + g - qpad[0])) for qm in qms])
+            assert_close_frac(np32(o[bb, rws, h * D:(h + 1) * D]), ro[0, rws], atol=2e-3, rtol=1e-2, name="o")
+            gl = lse[bb, h, torch.from_numpy(rws).cuda()].cpu().numpy()
+            fin = np.isfinite(rl[0, 0, rws])
+            np.testing.assert_array_equal(np.isfinite(gl), fin)
+            np.testing.assert_allclose(gl[fin], rl[0, 0, rws][fin], rtol=1e-4, atol=1e-4)
+            if not bwd:
+                continue
+            doh = _head(do[bb:bb + 1], h, D)
+            rdq, _, _ = O.sparse_attn_bwd(qh, kh, vh, doh, mh, 1, g, b, None, qpad, pad, qblocks=trip)
+            scl = max(1.0, np.abs(rdq[0, rws]).max() / 4)
+            # dS is rounded to 16 bits before the dQ / dK MFMAs (as in the reference
+            # kernels).  On peaked data (C3) dS = P (dP - delta) is a small difference
+            # of large terms, so up to 0.1% of dQ elements exceed the soft bound;
+            # none may exceed the hard one.
+            frac = 0.999 if data == "peaked" else 0.9995
+            assert_close_frac(np32(q.grad[bb, rws, h * D:(h + 1) * D]), rdq[0, rws], atol=2e-3 * scl, rtol=1e-2,
+                              name="dq", min_frac=frac, hard_atol=1e-2 * scl)
+            # dK / dV of one sampled KV block: every q-block that selected it contributes
+            for m in rng.choice(M, size=1, replace=False):
+                sel = [(0, 0, int(qm)) for qm in range(QM) if (mh[0, 0, qm] == m).any()]
+                if not sel:
+                    continue
+                _, rdk, rdv = O.sparse_attn_bwd(qh, kh, vh, doh, mh, 1, g, b, None, qpad, pad, qblocks=sel)
+                t0, t1 = max(0, m * b - pad[0]), min(N, (m + 1) * b - pad[0])
+                for nm, got, ref in (("dk", k.grad, rdk), ("dv", v.grad, rdv)):
+                    r = ref[0, t0:t1]
+                    s2 = max(1.0, np.abs(r).max() / 4)
+                    assert_close_frac(np32(got[bb, t0:t1, h * D:(h + 1) * D]), r, atol=2e-3 * s2, rtol=1e-2,
+                                      name=nm, min_frac=frac, hard_atol=1e-2 * s2)
+    say(f"[config {name}] ok: M={M} QM={QM} W={Wm} mean count {counts.float().mean().item():.1f}")
