@@ -67,6 +67,15 @@ __device__ __forceinline__ float fta_log2(float x) { return __builtin_amdgcn_log
 // Value from lane (l ^ 32).
 __device__ __forceinline__ float fta_xor32(float x) { return __shfl_xor(x, 32, 64); }
 
+// gfx950 v_permlane32_swap on two registers (measured): afterwards
+//   a = [a_lo | b_lo], b = [a_hi | b_hi]   (lo = lanes 0..31, hi = lanes 32..63)
+// so for lane l, a + b = a_in[l] + a_in[l + 32] (l < 32) or b_in[l - 32] + b_in[l]
+// (l >= 32).  Issued through asm (the compiler builtin gave wrong results with
+// this toolchain); the s_nops keep it clear of VALU read/write hazards.
+__device__ __forceinline__ void fta_swap32(float& a, float& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
 // Row of the 32x32 C layout held in accumulator register i of lane l.
 __device__ __forceinline__ int c_row(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
 

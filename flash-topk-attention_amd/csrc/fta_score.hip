@@ -709,11 +709,19 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
             }
             sums16(h1, R, e1);
         }
+        // block totals: lanes l and l ^ 32 hold halves of the same query's sum;
+        // two lane-half swaps give every lane both tiles' totals (the same
+        // operand pairs as part + part[l ^ 32], so the results are identical)
         float tot[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const float part = e0[t] + e1[t];
-            tot[t] = part + fta_xor32(part);
+        {
+            float a = e0[0] + e1[0], b = e0[1] + e1[1];
+            fta_swap32(a, b);
+            const float mine = a + b;  // tile (lane >> 5), query (lane & 31)
+            float x = mine, y = mine;
+            fta_swap32(x, y);
+            const float other = (lane < 32) ? y : x;  // the other tile, same query
+            tot[0] = (lane < 32) ? mine : other;
+            tot[1] = (lane < 32) ? other : mine;
         }
         const bool bad = !(tot[0] < 0x1p100f) || !(tot[1] < 0x1p100f);
         if (__ballot(bad) != 0ull) {
