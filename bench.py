@@ -24,11 +24,12 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
-# HBM bytes per fta_block_score_lse launch on the default workload, from rocprofv3 --pmc
-# FETCH_SIZE (8.027e5 KiB, x2.0) and WRITE_SIZE (2.102e6 KiB, x1.0); the factors are what the
-# same counters read for a 128 MiB device copy (bench.py --only copy).  A PMC pass cannot run
-# inside this process, so the figure is the last measured one and is refreshed with the kernel.
-SCORE_TRAFFIC_BYTES = int((2.0 * 8.027e5 + 1.0 * 2.102e6) * 1024)
+# HBM bytes per fta_block_score_lse launch on the default workload (pipelined
+# kernel), from rocprofv3 --pmc FETCH_SIZE (6.544e5 KiB, x2.0) and WRITE_SIZE
+# (2.102e6 KiB, x1.0); the factors are what the same counters read for a 128 MiB
+# device copy (bench.py --only copy).  A PMC pass cannot run inside this process,
+# so the figure is the last measured one and is refreshed with the kernel.
+SCORE_TRAFFIC_BYTES = int((2.0 * 6.544e5 + 1.0 * 2.102e6) * 1024)
 
 
 def make_inputs(B, N, H, D, peaked, seed, dev):
