@@ -963,7 +963,10 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
                 if (active && m < M && (pass || edge)) {
                     const float raw = (MODE == 0) ? x : fta_exp2(x);
                     if (raw >= thr_norm || edge) {
-                        const float avg = raw / (float)fta_valid_count(m, M, bsz, pad_head, pad_tail);
+                        const int vc = fta_valid_count(m, M, bsz, pad_head, pad_tail);
+                    // x / 2^j == x * 2^-j exactly (same exact value, same rounding)
+                    const float avg = ((vc & (vc - 1)) == 0) ? raw * __builtin_amdgcn_ldexpf(1.f, -__builtin_ctz(vc))
+                                                              : raw / (float)vc;
                         if (fta_better(avg, m, tv, ti)) {
                             cand_v[wave][cnt][lane] = avg;
                             cand_i[wave][cnt][lane] = m;
