@@ -93,6 +93,8 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=8192)
     ap.add_argument("--only", choices=["score", "topk", "merge", "fwd", "bwd", "copy"], default=None,
                     help="profiling aid: run one stage of the C3 step --steps times and exit")
+    ap.add_argument("--iid", action="store_true",
+                    help="with --only: the C3-iid variant (iid q/k/v, threshold 1.0, qblock_topk 512)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); every stage is per (b, h) "
@@ -130,6 +132,10 @@ def main():
         return counts
 
     if args.only:
+        if args.iid:
+            thr, W = 1.0, 512
+            q, k, v = make_inputs(B, N, H, D, False, 3, dev)
+            ql, kl, vl = (t.detach().requires_grad_(True) for t in (q, k, v))
         idx, raw, avg = fta.flash_topk_score(q, k, H, b, topk, (0, 0), thr)
         merged, counts, Wd = fta.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
         o, lse = fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, b)

@@ -266,20 +266,20 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
                             s[tt][1] = E::mma(a1, qf[tt][ks], s[tt][1]);
                         }
                 }
-                const bool kmask = kb < 0 || kb + 64 > a.N || rem < 64;
 #pragma unroll
                 for (int tt = 0; tt < TPW; ++tt) {
                     if (!mk[tt]) continue;
                     const bool colok = (mk[tt] >> (lane & 31)) & 1u;
+                    const int klo = colok ? max(0, -kb) : 64;
+                    const int khi = colok ? min(min(rem, 64), a.N - kb) : 0;
+                    const unsigned kw = (unsigned)max(khi - klo, 0);  // a chunk past N has khi < klo
                     float mx = -FTA_INF;
 #pragma unroll
                     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
                         for (int i = 0; i < 16; ++i) {
                             const int rel = sb * 32 + c_row(i, lane);
-                            const int t = kb + rel;
-                            const bool ok = colok && (!kmask || (rel < rem && t >= 0 && t < a.N));
-                            const float v = ok ? s[tt][sb][i] : -FTA_INF;
+                            const float v = ((unsigned)(rel - klo) < kw) ? s[tt][sb][i] : -FTA_INF;
                             s[tt][sb][i] = v;
                             mx = fmaxf(mx, v);
                         }
@@ -350,6 +350,238 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
                 }
             }
     }
+}
+
+// ----------------------------------------------------------------------------
+// Forward, pipelined (D = 64 and 128).  Same tiling and arithmetic as
+// fta_sparse_fwd_kernel with one tile per wave, but the 64-key K and V chunks
+// are gathered by LDS DMA (global_load_lds_dwordx4) into NST stage buffers in
+// the swizzled row layout, NST - 1 chunks ahead of the MFMAs, so the gather
+// latency is hidden behind the work of the chunks in flight and no registers
+// stage the copies.
+// ----------------------------------------------------------------------------
+template <int D, int NW>
+struct FwdPipeShape {
+    static constexpr int QSEG = D / 8;
+    static constexpr int SLOTS = 64 * QSEG;         // 16-byte slots per 64-row tensor chunk
+    static constexpr int LQ = SLOTS / (64 * NW);    // DMA instructions per wave per tensor
+    static constexpr int TEN_B = SLOTS * 16;        // bytes per tensor chunk
+    static constexpr int STAGE_B = 2 * TEN_B;       // K then V
+    static constexpr int NST = (3 * STAGE_B <= 96 * 1024 && D <= 64) ? 4 : 3;
+    static_assert(SLOTS % (64 * NW) == 0, "whole DMA instructions per wave");
+    static_assert(NST * STAGE_B + NW * kSeg * 4 + kSeg * 4 <= 150 * 1024, "LDS budget");
+};
+
+template <int DT, int D, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArgs a) {
+    using E = Elem<DT>;
+    using Sh = FwdPipeShape<D, NW>;
+    constexpr int QSEG = Sh::QSEG, LQ = Sh::LQ, NST = Sh::NST;
+    using SW = FtaSwz<QSEG>;
+    constexpr int T = NW;
+    constexpr int KS = D / 16;
+    constexpr int DT32 = D / 32;
+    __shared__ __align__(1024) unsigned char sStage[NST][Sh::STAGE_B];
+    __shared__ uint32_t sMask[T][kSeg];
+    __shared__ int sList[kSeg];
+    __shared__ int s_tmp[8];
+
+    const int wgi = fta_xcd_remap(blockIdx.x, a.total);
+    const int bh = wgi / a.wg_per_bh;
+    const int wq = wgi - bh * a.wg_per_bh;
+    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hf = lane >> 5;
+    const int p0 = wq * 32 * T;
+
+    const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
+    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+
+    uint4 qf[KS];
+    {
+        const int t = p0 + 32 * wave + (lane & 31) - a.q_pad;
+        const bool ok = t >= 0 && t < a.N;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d = ks * 16 + hf * 8;
+            qf[ks] = (ok && d < a.Dreal) ? *reinterpret_cast<const uint4*>(qp + (int64_t)t * a.q_sn + d) : fta_zero4();
+        }
+    }
+    // complete the register loads: the DMAs below are invisible to the compiler
+    fta_wait_vmcnt<0>();
+
+    f32x16 oacc[DT32];
+#pragma unroll
+    for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[dt][i] = 0.f;
+    float m_run = -FTA_INF, l_run = 0.f;
+
+    // Per-lane DMA sources: instruction i of this wave fills the 1 KB block
+    // i * NW + wave of each tensor chunk; koff / voff = row * stride + column.
+    int koff[LQ], voff[LQ];
+#pragma unroll
+    for (int i = 0; i < LQ; ++i) {
+        const int sidx = (i * NW + wave) * 64 + lane;
+        const int row = sidx / QSEG;
+        int j = SW::slot(row, sidx - row * QSEG);
+        if (j * 8 >= a.Dreal) j = 0;  // columns past D: zero q columns / outputs never stored
+        koff[i] = row * (int)a.k_sn + j * 8;
+        voff[i] = row * (int)a.v_sn + j * 8;
+    }
+    const uint32_t lds0 = fta_lds_addr(&sStage[0][0]);
+    const int nch = (a.kvb + 63) >> 6;
+
+    for (int seg0 = 0; seg0 < a.Mkv; seg0 += kSeg) {
+        const int segn = min(kSeg, a.Mkv - seg0);
+        const int U = fta_build_q_masks<T>(a, bh, p0, seg0, segn, sMask, sList, s_tmp);
+        if (U == 0) continue;
+        const int iters = U * nch;
+
+        // gather chunk `it` (64 keys of union block it / nch) into stage buffer st
+        auto issue = [&](int st, int it) {
+            const uint32_t sb = lds0 + st * Sh::STAGE_B;
+            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int m = __builtin_amdgcn_readfirstlane(seg0 + sList[u]);
+            const int kb = m * a.kvb - a.kv_pad + ch * 64;
+            const int rem = a.kvb - ch * 64;
+            if (kb >= 0 && kb + 64 <= a.N && rem >= 64) {
+                const uint16_t* kbp = kp + (int64_t)kb * a.k_sn;
+                const uint16_t* vbp = vp + (int64_t)kb * a.v_sn;
+#pragma unroll
+                for (int i = 0; i < LQ; ++i) fta_dma16_at(kbp + koff[i], sb + (i * NW + wave) * 1024);
+#pragma unroll
+                for (int i = 0; i < LQ; ++i) fta_dma16_at(vbp + voff[i], sb + Sh::TEN_B + (i * NW + wave) * 1024);
+            } else {  // chunk at a sequence / block edge: clamp rows into [0, N) (masked below)
+#pragma unroll
+                for (int i = 0; i < LQ; ++i) {
+                    const int sidx = (i * NW + wave) * 64 + lane;
+                    const int row = sidx / QSEG;
+                    int j = SW::slot(row, sidx - row * QSEG);
+                    if (j * 8 >= a.Dreal) j = 0;
+                    const int t = min(max(kb + row, 0), a.N - 1);
+                    fta_dma16_at(kp + (int64_t)t * a.k_sn + j * 8, sb + (i * NW + wave) * 1024);
+                    fta_dma16_at(vp + (int64_t)t * a.v_sn + j * 8, sb + Sh::TEN_B + (i * NW + wave) * 1024);
+                }
+            }
+        };
+
+#pragma unroll
+        for (int k = 0; k < NST - 1; ++k)
+            if (k < iters) issue(k, k);
+        int cur = 0;
+        for (int it = 0; it < iters; ++it) {
+            // chunk it resident: chunks issued so far = min(iters, it + NST - 1)
+            if (it + NST - 2 < iters)
+                fta_wait_vmcnt<2 * LQ * (NST - 2)>();
+            else
+                fta_wait_vmcnt<0>();
+            __syncthreads();  // chunk it visible; every wave is past chunk it - 1
+            if (it + NST - 1 < iters) issue(cur == 0 ? NST - 1 : cur - 1, it + NST - 1);
+
+            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int ml = sList[u];
+            const int m = seg0 + ml;
+            const int kb = m * a.kvb - a.kv_pad + ch * 64;
+            const int rem = a.kvb - ch * 64;
+            const uint32_t mk = __builtin_amdgcn_readfirstlane(sMask[wave][ml]);
+            if (mk) {
+                const uint16_t* kbase = reinterpret_cast<const uint16_t*>(&sStage[cur][0]);
+                const uint16_t* vbase = kbase + Sh::TEN_B / 2;
+                f32x16 s[2];
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) s[sb][i] = 0.f;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const uint4 a0 = *reinterpret_cast<const uint4*>(kbase + SW::off(lane & 31, 2 * ks + hf));
+                    const uint4 a1 = *reinterpret_cast<const uint4*>(kbase + SW::off(32 + (lane & 31), 2 * ks + hf));
+                    s[0] = E::mma(a0, qf[ks], s[0]);
+                    s[1] = E::mma(a1, qf[ks], s[1]);
+                }
+                // valid keys of the chunk: [klo, khi) relative to kb (wave-uniform)
+                const int klo = max(0, -kb), khi = min(min(rem, 64), a.N - kb);
+                if (klo > 0 || khi < 64 || mk != 0xffffffffu) {
+                    // branch-free: one compare pair per element, the column bit per lane
+                    const bool colok = (mk >> (lane & 31)) & 1u;
+                    const int lo = colok ? klo : 64, hi = colok ? max(khi, klo) : 64;  // empty if past N
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            const int rel = sb * 32 + c_row(i, lane);
+                            s[sb][i] = ((unsigned)(rel - lo) < (unsigned)(hi - lo)) ? s[sb][i] : -FTA_INF;
+                        }
+                }
+                float mx = s[0][0];
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                    for (int i = (sb == 0); i < 16; ++i) mx = fmaxf(mx, s[sb][i]);
+                mx = fmaxf(mx, fta_xor32(mx));
+                const float mn = fmaxf(m_run, mx);
+                const bool grow = (mn - m_run) * a.c > 8.f;
+                if (__ballot(grow) != 0ull) {
+                    const float alpha = grow ? fta_exp2((m_run - mn) * a.c) : 1.f;
+#pragma unroll
+                    for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) oacc[dt][i] *= alpha;
+                    l_run *= alpha;
+                    if (grow) m_run = mn;
+                }
+                const float mc = (m_run == -FTA_INF) ? 0.f : m_run * a.c;
+                float ls = 0.f;
+                uint4 pf[4];
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    float pv[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        pv[e] = fta_exp2(fmaf(s[ks >> 1][8 * (ks & 1) + e], a.c, -mc));
+                        ls += pv[e];
+                    }
+                    pf[ks] = make_uint4(E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
+                                        E::pack2(pv[6], pv[7]));
+                }
+                l_run += ls;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+                    for (int dt = 0; dt < DT32; ++dt) {
+                        const uint4 vf = fta_tr_frag_sw<QSEG>(vbase, ks * 16, dt * 32, lane);
+                        oacc[dt] = E::mma(vf, pf[ks], oacc[dt]);
+                    }
+                }
+            }
+            cur = (cur == NST - 1) ? 0 : cur + 1;
+        }
+        __syncthreads();  // every wave is done with sMask / sList before the next segment rebuilds them
+    }
+
+    // finalize: O = O^T / L, lse = ln(sum) + max
+    const float L = l_run + fta_xor32(l_run);
+    const float inv = (L > 0.f) ? 1.f / L : 0.f;
+    const int t = p0 + 32 * wave + (lane & 31) - a.q_pad;
+    if (t < 0 || t >= a.N) return;
+    if (lane < 32)
+        a.lse[(int64_t)bh * a.N + t] = (L > 0.f) ? (fmaf(m_run, a.c, fta_log2(L))) * 0.69314718055994531f : -FTA_INF;
+    uint16_t* op = a.out0 + b * a.o0_sb + h * a.o0_sh + (int64_t)t * a.o0_sn;
+#pragma unroll
+    for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const int d = dt * 32 + c_row(i, lane);
+            if (d < a.Dreal) {
+                uint2 w;
+                w.x = E::pack2(oacc[dt][i] * inv, oacc[dt][i + 1] * inv);
+                w.y = E::pack2(oacc[dt][i + 2] * inv, oacc[dt][i + 3] * inv);
+                *reinterpret_cast<uint2*>(op + d) = w;
+            }
+        }
 }
 
 // ----------------------------------------------------------------------------
@@ -480,8 +712,12 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
                         dpv[sb] = E::mma(*reinterpret_cast<const uint4*>(vbase + off), df[ks], dpv[sb]);
                     }
                 }
+                // valid keys [klo, khi) relative to kb; a lane whose query column
+                // is not selected gets the empty range (branch-free masking)
                 const bool colok = rowlive && ((mk >> (lane & 31)) & 1u);
-                const bool kmask = kb < 0 || kb + 64 > a.N || rem < 64;
+                const int klo = colok ? max(0, -kb) : 64;
+                const int khi = colok ? min(min(rem, 64), a.N - kb) : 0;
+                const unsigned kw = (unsigned)max(khi - klo, 0);  // a chunk past N has khi < klo
                 uint4 dsf[4];
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
@@ -490,9 +726,9 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
                     for (int e = 0; e < 8; ++e) {
                         const int sb = ks >> 1, i = 8 * (ks & 1) + e;
                         const int rel = sb * 32 + c_row(i, lane);
-                        const int t = kb + rel;
-                        const bool ok = colok && (!kmask || (rel < rem && t >= 0 && t < a.N));
-                        const float p = ok ? fta_exp2(fmaf(s[sb][i], a.c, -lse2)) : 0.f;
+                        const bool ok = (unsigned)(rel - klo) < kw;
+                        const float ex = fta_exp2(fmaf(s[sb][i], a.c, -lse2));
+                        const float p = ok ? ex : 0.f;
                         dsv[e] = p * (dpv[sb][i] - dl);
                     }
                     dsf[ks] = make_uint4(E::pack2(dsv[0], dsv[1]), E::pack2(dsv[2], dsv[3]),
@@ -951,15 +1187,27 @@ void fill_common(AttnArgs& a, int H, int N, int D, int g, int kvb, int qph, int 
 
 template <int DT>
 int launch_fwd_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
+    // the pipelined kernel keeps per-lane row offsets (64 rows x stride) in 32 bits
+    const bool pipe_ok = a.k_sn <= (1 << 24) && a.v_sn <= (1 << 24);
     switch (Dk) {
 #define FTA_FWD(DK, TPW, NW)                                                                              \
     case DK:                                                                                              \
         hipLaunchKernelGGL((fta_sparse_fwd_kernel<DT, DK, TPW, NW>), dim3(grid), dim3(NW * 64), 0, st, a); \
         break;
         FTA_FWD(32, 1, 8)
-        FTA_FWD(64, 1, 8)
+        case 64:
+            if (pipe_ok)
+                hipLaunchKernelGGL((fta_sparse_fwd_pipe_kernel<DT, 64, 8>), dim3(grid), dim3(512), 0, st, a);
+            else
+                hipLaunchKernelGGL((fta_sparse_fwd_kernel<DT, 64, 1, 8>), dim3(grid), dim3(512), 0, st, a);
+            break;
         FTA_FWD(96, 1, 8)
-        FTA_FWD(128, 1, 8)
+        case 128:
+            if (pipe_ok)
+                hipLaunchKernelGGL((fta_sparse_fwd_pipe_kernel<DT, 128, 8>), dim3(grid), dim3(512), 0, st, a);
+            else
+                hipLaunchKernelGGL((fta_sparse_fwd_kernel<DT, 128, 1, 8>), dim3(grid), dim3(512), 0, st, a);
+            break;
         FTA_FWD(160, 1, 8)
         FTA_FWD(256, 1, 4)
 #undef FTA_FWD
