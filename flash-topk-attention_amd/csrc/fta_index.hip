@@ -39,10 +39,14 @@ __device__ __forceinline__ int fta_block_scan256(int v, int* s_tmp, int* total) 
 constexpr int kMergeChunk = 1024;  // staged (id, score) entries per step
 
 __global__ __launch_bounds__(256) void fta_qblock_merge_kernel(const int32_t* __restrict__ idx,
-                                                               const float* __restrict__ scr, int g, int K, int Mt,
+                                                               const float* __restrict__ scr, int g, int K,
+                                                               int Mt_arg, const int32_t* __restrict__ max_id,
                                                                int W, int32_t* __restrict__ out_idx,
                                                                float* __restrict__ out_scr,
                                                                int32_t* __restrict__ counts) {
+    // block count: the argument, or (max id + 1) read from device memory, kept
+    // within the 4096-entry histogram (a larger max is an error the host reports)
+    const int Mt = max_id ? min(max(*max_id + 1, 1), 4096) : Mt_arg;
     __shared__ float acc[4096];
     __shared__ unsigned long long keys[4096];
     __shared__ int s_tmp[8];
@@ -314,7 +318,23 @@ int fta_qblock_merge(const int32_t* topk_indices, const float* topk_scores, int6
     if (qblock_topk <= 0) return fta::arg_error("qblock_topk must be positive");
     if (num_slices == 0) return FTA_OK;
     hipLaunchKernelGGL(fta_qblock_merge_kernel, dim3((unsigned)num_slices), dim3(256), 0, (hipStream_t)stream,
-                       topk_indices, topk_scores, q_block_size, k_per_query, num_score_blocks, qblock_topk,
+                       topk_indices, topk_scores, q_block_size, k_per_query, num_score_blocks, (const int32_t*)nullptr,
+                       qblock_topk, merged_indices, merged_scores, counts);
+    return fta::check_launch("fta_qblock_merge_kernel");
+    FTA_TRY_END
+}
+
+int fta_qblock_merge_maxid(const int32_t* topk_indices, const float* topk_scores, int64_t num_slices,
+                           int q_block_size, int k_per_query, const int32_t* max_index, int qblock_topk,
+                           int32_t* merged_indices, float* merged_scores, int32_t* counts, void* stream) {
+    FTA_TRY_BEGIN
+    if (num_slices < 0 || num_slices > 0x7fffffff) return fta::arg_error("qblock_merge: bad slice count");
+    if (q_block_size <= 0 || k_per_query < 0) return fta::arg_error("qblock_merge: bad q_block_size / K");
+    if (max_index == nullptr) return fta::arg_error("qblock_merge: max_index is NULL");
+    if (qblock_topk <= 0) return fta::arg_error("qblock_topk must be positive");
+    if (num_slices == 0) return FTA_OK;
+    hipLaunchKernelGGL(fta_qblock_merge_kernel, dim3((unsigned)num_slices), dim3(256), 0, (hipStream_t)stream,
+                       topk_indices, topk_scores, q_block_size, k_per_query, 0, max_index, qblock_topk,
                        merged_indices, merged_scores, counts);
     return fta::check_launch("fta_qblock_merge_kernel");
     FTA_TRY_END

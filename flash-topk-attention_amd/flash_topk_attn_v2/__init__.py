@@ -113,10 +113,6 @@ def build_qblock_topk_indices(
     if qblock_topk is None:
         qblock_topk = q_block_size * topk_width
 
-    # num_score_blocks = max id + 1 (host sync, as in the reference :101-105)
-    mx = int(indices_int.max().item()) if indices_int.numel() > 0 else -1
-    num_score_blocks = mx + 1 if mx >= 0 else 1
-
     if topk_scores is not None:
         scores_float = topk_scores.float().contiguous()
         if q_pad_head > 0 or q_pad_tail > 0:
@@ -127,14 +123,33 @@ def build_qblock_topk_indices(
     B, H = indices_int.shape[:2]
     QM = padded_sequence_length // q_block_size
     counts = torch.empty(B, H, QM, device=device, dtype=torch.int32)
-    merged_indices, _merged_scores = flash_qblock_merge(
-        indices_int,
-        scores_float,
-        q_block_size=q_block_size,
-        qblock_topk=qblock_topk,
-        num_score_blocks=num_score_blocks,
-        counts_out=counts,
+    if indices_int.numel() == 0:
+        merged_indices, _ = flash_qblock_merge(indices_int, scores_float, q_block_size=q_block_size,
+                                               qblock_topk=qblock_topk, num_score_blocks=1, counts_out=counts)
+        return merged_indices, counts, merged_indices.shape[-1]
+    if qblock_topk <= 0:
+        raise ValueError("qblock_topk must be positive")
+    if indices_int.device.type != "cuda":
+        raise ValueError("flash_qblock_merge requires CUDA tensors")
+
+    # num_score_blocks = max id + 1, as in the reference (:101-105).  The max is
+    # taken on the device and read by the merge kernel, and the host reads it
+    # (to report ids past the 4096-block limit) only after the merge is queued,
+    # so the GPU does not idle through the host round trip.
+    max_id = indices_int.max().reshape(1)
+    merged_indices = torch.empty(B, H, QM, qblock_topk, device=device, dtype=torch.int32)
+    merged_scores = torch.empty(B, H, QM, qblock_topk, device=device, dtype=torch.float32)
+    rc = _lib.lib().fta_qblock_merge_maxid(
+        _lib.ptr(indices_int), _lib.ptr(scores_float), B * H * QM, q_block_size, topk_width,
+        _lib.ptr(max_id), qblock_topk, _lib.ptr(merged_indices), _lib.ptr(merged_scores), _lib.ptr(counts),
+        _lib.stream_ptr(device),
     )
+    _lib.check(rc, "flash_qblock_merge")
+    num_score_blocks = int(max_id.item()) + 1
+    if num_score_blocks > 4096:
+        raise NotImplementedError(
+            f"num_score_blocks={num_score_blocks} exceeds CUDA block sort limit 4096"
+        )
     max_merged_width = merged_indices.shape[-1]
     return merged_indices, counts, max_merged_width
 

@@ -123,6 +123,19 @@ int fta_qblock_merge(const int32_t* topk_indices, const float* topk_scores, int6
                      int q_block_size, int k_per_query, int num_score_blocks, int qblock_topk,
                      int32_t* merged_indices, float* merged_scores, int32_t* counts, void* stream);
 
+/*
+ * fta_qblock_merge with num_score_blocks = *max_index + 1 read on the device
+ * (max_index: a device int32, the largest id in topk_indices, -1 if none),
+ * so the caller need not synchronise before launching the merge.  Ids past
+ * 4096 are outside the supported range; the caller checks the max on the host
+ * (after this launch) and reports that case as an error.
+ * Replaces the host-side max of build_qblock_topk_indices
+ * (flash_topk_attn_v2/__init__.py:101-105) followed by qblock_merge_launch.
+ */
+int fta_qblock_merge_maxid(const int32_t* topk_indices, const float* topk_scores, int64_t num_slices,
+                           int q_block_size, int k_per_query, const int32_t* max_index, int qblock_topk,
+                           int32_t* merged_indices, float* merged_scores, int32_t* counts, void* stream);
+
 size_t fta_build_reverse_indices_workspace_size(int B, int H, int QM, int M);
 
 /*

@@ -120,6 +120,24 @@ def test_merge_bit_exact(g, K, Mt, W, pad, with_scores):
     np.testing.assert_array_equal(c.cpu().numpy(), rc)
 
 
+def test_merge_device_max_edge_cases():
+    """build_qblock_topk_indices reads the max id on the device: all -1 rows give
+    empty lists, and an id past the 4096-block sort limit raises as in the
+    reference (flash_topk_attn_v2/__init__.py:101-105, qblock_merge.py:55-59)."""
+    say("[merge] device max: empty rows, id limit")
+    ti = torch.full((1, 2, 64, 4), -1, dtype=torch.int32, device="cuda")
+    m, c, w = fta.build_qblock_topk_indices(ti, 32, (0, 0), None, 8)
+    torch.cuda.synchronize()
+    assert w == 8 and bool((m == -1).all()) and bool((c == 0).all())
+    ti[0, 1, 5, 0] = 4095  # the largest id that is allowed
+    m, c, _ = fta.build_qblock_topk_indices(ti, 32, (0, 0), None, 8)
+    assert m[0, 1, 0, 0].item() == 4095 and c[0, 1, 0].item() == 1 and c.sum().item() == 1
+    ti[0, 0, 7, 1] = 4096
+    with pytest.raises(NotImplementedError, match="4096"):
+        fta.build_qblock_topk_indices(ti, 32, (0, 0), None, 8)
+    torch.cuda.synchronize()
+
+
 ATTN_CASES = [
     # B, N, H, D, g, b, qpad, kvpad, W, dtype
     (1, 1024, 2, 64, 32, 64, (0, 0), (0, 0), 12, torch.float16),
