@@ -944,12 +944,28 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
         set_thr();
     };
 
-    for (int m1 = 0; m1 < M; m1 += LDB) {
-        float xs[LDB];
+    // Unconditional loads (an inactive lane reads row 0), clamped past M, two
+    // batches in flight: batch k + 1 loads while batch k is tested.
+    auto load_batch = [&](int m1, float (&xs)[LDB]) {
 #pragma unroll
         for (int u = 0; u < LDB; ++u) {
             const int m = min(m1 + u, M - 1);
-            xs[u] = active ? ((MODE == 0) ? src[m * stride_m] : src[(int64_t)m * N]) : 0.f;
+            xs[u] = (MODE == 0) ? src[m * stride_m] : src[(int64_t)m * N];
+        }
+    };
+    auto test_batch = [&](int m1, const float (&xs)[LDB]) {
+        // Skip the batch when no lane can find a candidate in it: the largest
+        // value of each lane's batch is below its pre-filter bound, and the
+        // batch holds no partial (always tested) edge block.  Exact: the
+        // per-block tests below would reject every block of such a batch.
+        {
+            float bm = xs[0];
+#pragma unroll
+            for (int u = 1; u < LDB; ++u) bm = fmaxf(bm, xs[u]);
+            const float bx = (MODE == 0) ? bm : bm - rl;
+            const bool may = active && ((MODE == 0) ? (bx >= thr_norm) : (bx >= thr_log));
+            const bool edges = (m1 == 0 && pad_head > 0) || (m1 + LDB >= M && pad_tail > 0);
+            if (!edges && __ballot(may) == 0ull) return;
         }
 #pragma unroll
         for (int sb = 0; sb < LDB; sb += UNR) {
@@ -964,9 +980,10 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
                     const float raw = (MODE == 0) ? x : fta_exp2(x);
                     if (raw >= thr_norm || edge) {
                         const int vc = fta_valid_count(m, M, bsz, pad_head, pad_tail);
-                    // x / 2^j == x * 2^-j exactly (same exact value, same rounding)
-                    const float avg = ((vc & (vc - 1)) == 0) ? raw * __builtin_amdgcn_ldexpf(1.f, -__builtin_ctz(vc))
-                                                              : raw / (float)vc;
+                        // x / 2^j == x * 2^-j exactly (same exact value, same rounding)
+                        const float avg = ((vc & (vc - 1)) == 0)
+                                              ? raw * __builtin_amdgcn_ldexpf(1.f, -__builtin_ctz(vc))
+                                              : raw / (float)vc;
                         if (fta_better(avg, m, tv, ti)) {
                             cand_v[wave][cnt][lane] = avg;
                             cand_i[wave][cnt][lane] = m;
@@ -977,6 +994,15 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
             }
             if (__ballot(cnt > CAP - UNR) != 0ull) flush();
         }
+    };
+    float xa[LDB], xb[LDB];
+    load_batch(0, xa);
+    for (int m1 = 0; m1 < M; m1 += 2 * LDB) {
+        load_batch(m1 + LDB, xb);  // clamped: a batch past M rereads block M - 1
+        test_batch(m1, xa);
+        if (m1 + LDB >= M) break;
+        load_batch(m1 + 2 * LDB, xa);
+        test_batch(m1 + LDB, xb);
     }
     flush();
 
