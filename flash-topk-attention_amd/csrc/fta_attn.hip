@@ -27,7 +27,9 @@ namespace fta {
 int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint32_t* sel, hipStream_t st);
 }  // namespace fta
 
-constexpr int kSeg = 512;  // KV blocks (forward / dQ) or q-chunks (dK/dV) per mask segment
+constexpr int kSeg = 512;    // KV blocks per mask segment (forward / dQ)
+constexpr int kSegC = 1024;  // 32-query chunks per mask segment (dK/dV): N <= 32768 in one pass
+constexpr int kBitsW = 64;   // bitmap words per KV block staged in LDS by dK/dV (QM <= 2048)
 
 struct AttnArgs {
     const uint16_t* q;
@@ -784,6 +786,96 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
 // addresses (finite data); the masks zero their P and dS, and the columns are
 // never stored.
 // ----------------------------------------------------------------------------
+// dK/dV masks.  The membership rows (one per KV block of the WG's TT tiles)
+// are small: with QW <= kBitsW words they are staged in LDS once, so the masks
+// are built from LDS instead of one global round trip per chunk batch.
+template <int TT>
+__device__ bool fta_stage_kv_bits(const AttnArgs& a, int bh, int wk, int Tb, uint32_t (*sBits)[kBitsW]) {
+    const int qw = a.QW;
+    const bool bits_lds = qw <= kBitsW;
+    if (bits_lds) {
+        for (int i = threadIdx.x; i < TT * qw; i += blockDim.x) {
+            const int t = i / qw, w = i - (i / qw) * qw;
+            const int mt = (wk * TT + t) / Tb;
+            sBits[t][w] = (mt < a.Mkv) ? a.sel[((int64_t)bh * a.Mkv + mt) * qw + w] : 0u;
+        }
+        __syncthreads();
+    }
+    return bits_lds;
+}
+
+// Column masks of the WG's TT key tiles over 32-query chunks [seg0, seg0 + segn)
+// (tile t x chunk cl -> bits over the chunk's 32 queries), then the ascending
+// list of chunks any tile needs.  Returns the list length.
+template <int TT>
+__device__ int fta_build_kv_masks(const AttnArgs& a, int bh, int wk, int Tb, int seg0, int segn, bool bits_lds,
+                                  const uint32_t (*sBits)[kBitsW], uint32_t (*sMask)[kSegC], int* sList,
+                                  int* s_tmp) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int NTHR = blockDim.x, NW = NTHR >> 6;
+    const int qw = a.QW;
+    // masks: tile t x chunk (seg0 + cl) -> bits over the chunk's 32 queries.
+    // A chunk overlaps at most 33 q-blocks, i.e. two bitmap words per tile.
+    for (int cl = tid; cl < segn; cl += NTHR) {
+        const int pc = 32 * (seg0 + cl);
+        const int qb_a = pc / a.g;
+        const int qb_b = min((pc + 31) / a.g, a.QM - 1);
+        const int w_a = qb_a >> 5, w_b = qb_b >> 5;
+        uint32_t w0[TT], w1[TT];
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            if (bits_lds) {
+                w0[t] = sBits[t][w_a];
+                w1[t] = (w_b > w_a) ? sBits[t][w_b] : 0u;
+            } else {
+                const int mt = (wk * TT + t) / Tb;
+                const uint32_t* srow = a.sel + ((int64_t)bh * a.Mkv + min(mt, a.Mkv - 1)) * qw;
+                w0[t] = (mt < a.Mkv) ? srow[w_a] : 0u;
+                w1[t] = (mt < a.Mkv && w_b > w_a) ? srow[w_b] : 0u;
+            }
+        }
+        const uint32_t valid = fta_range_bits(a.q_pad - pc, a.q_pad + a.N - pc);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            uint32_t bits = 0u;
+            for (int qb = qb_a; qb <= qb_b; ++qb) {
+                const uint32_t w = ((qb >> 5) == w_a) ? w0[t] : w1[t];
+                if ((w >> (qb & 31)) & 1u) bits |= fta_range_bits(qb * a.g - pc, qb * a.g + a.g - pc);
+            }
+            sMask[t][cl] = bits & valid;
+        }
+    }
+    __syncthreads();
+    int U = 0;
+    for (int base = 0; base < segn; base += NTHR) {
+        const int cl = base + tid;
+        int any = 0;
+        if (cl < segn) {
+#pragma unroll
+            for (int t = 0; t < TT; ++t) any |= (sMask[t][cl] != 0u);
+        }
+        int x = any;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(x, off, 64);
+            if (lane >= off) x += y;
+        }
+        if (lane == 63) s_tmp[wave] = x;
+        __syncthreads();
+        int wbase = 0, tot = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const int t = s_tmp[w];
+            if (w < wave) wbase += t;
+            tot += t;
+        }
+        if (any) sList[U + wbase + x - any] = cl;
+        __syncthreads();
+        U += tot;
+    }
+    return U;
+}
+
 template <int D, int TT, int CS>
 struct DkvShape {
     static constexpr int NW = TT * CS;
@@ -794,7 +886,7 @@ struct DkvShape {
     static constexpr int L = LQ + 1;                              // + one for lse / delta
     static constexpr int LD_OFF = LQ * NW * 1024;                 // byte offset of lse / delta in a step
     static constexpr int STAGE_B = LD_OFF + NW * 256;
-    static constexpr int FIXED_B = TT * kSeg * 4 + kSeg * 4 + 64;
+    static constexpr int FIXED_B = TT * kSegC * 4 + kSegC * 4 + TT * kBitsW * 4 + 64;
     static constexpr int NST_FIT = (150 * 1024 - FIXED_B) / STAGE_B;
     static constexpr int NST = NST_FIT > 4 ? 4 : NST_FIT;
     static_assert(NST >= 2, "two steps must fit in LDS");
@@ -811,8 +903,9 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
     constexpr int DT32 = D / 32;
     static_assert(CS == 1 || TT * 32 * D * 4 <= NST * Sh::STAGE_B, "reduction tile must fit the staging buffers");
     __shared__ __align__(1024) unsigned char sStage[NST][Sh::STAGE_B];
-    __shared__ uint32_t sMask[TT][kSeg];
-    __shared__ int sList[kSeg];
+    __shared__ uint32_t sMask[TT][kSegC];
+    __shared__ int sList[kSegC];
+    __shared__ uint32_t sBits[TT][kBitsW];
     __shared__ int s_tmp[8];
 
     const int wgi = fta_xcd_remap(blockIdx.x, a.total);
@@ -887,64 +980,10 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
             dva[dt][i] = 0.f;
         }
 
-    const int qw = a.QW;
-    for (int seg0 = 0; seg0 < a.NC; seg0 += kSeg) {
-        const int segn = min(kSeg, a.NC - seg0);
-        // masks: tile t x chunk (seg0 + cl) -> bits over the chunk's 32 queries.
-        // A chunk overlaps at most 33 q-blocks, i.e. two bitmap words per tile;
-        // each thread loads its chunk's words for all tiles first (one latency).
-        for (int cl = tid; cl < segn; cl += Sh::NTHR) {
-            const int pc = 32 * (seg0 + cl);
-            const int qb_a = pc / a.g;
-            const int qb_b = min((pc + 31) / a.g, a.QM - 1);
-            const int w_a = qb_a >> 5, w_b = qb_b >> 5;
-            uint32_t w0[TT], w1[TT];
-#pragma unroll
-            for (int t = 0; t < TT; ++t) {
-                const int mt = (wk * TT + t) / Tb;
-                const uint32_t* srow = a.sel + ((int64_t)bh * a.Mkv + min(mt, a.Mkv - 1)) * qw;
-                w0[t] = (mt < a.Mkv) ? srow[w_a] : 0u;
-                w1[t] = (mt < a.Mkv && w_b > w_a) ? srow[w_b] : 0u;
-            }
-            const uint32_t valid = fta_range_bits(a.q_pad - pc, a.q_pad + a.N - pc);
-#pragma unroll
-            for (int t = 0; t < TT; ++t) {
-                uint32_t bits = 0u;
-                for (int qb = qb_a; qb <= qb_b; ++qb) {
-                    const uint32_t w = ((qb >> 5) == w_a) ? w0[t] : w1[t];
-                    if ((w >> (qb & 31)) & 1u) bits |= fta_range_bits(qb * a.g - pc, qb * a.g + a.g - pc);
-                }
-                sMask[t][cl] = bits & valid;
-            }
-        }
-        __syncthreads();
-        int U = 0;
-        for (int base = 0; base < segn; base += Sh::NTHR) {
-            const int cl = base + tid;
-            int any = 0;
-            if (cl < segn) {
-#pragma unroll
-                for (int t = 0; t < TT; ++t) any |= (sMask[t][cl] != 0u);
-            }
-            int x = any;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const int y = __shfl_up(x, off, 64);
-                if (lane >= off) x += y;
-            }
-            if (lane == 63) s_tmp[wave] = x;
-            __syncthreads();
-            int wbase = 0, tot = 0;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                const int t = s_tmp[w];
-                if (w < wave) wbase += t;
-                tot += t;
-            }
-            if (any) sList[U + wbase + x - any] = cl;
-            __syncthreads();
-            U += tot;
-        }
+    const bool bits_lds = fta_stage_kv_bits<TT>(a, bh, wk, Tb, sBits);
+    for (int seg0 = 0; seg0 < a.NC; seg0 += kSegC) {
+        const int segn = min(kSegC, a.NC - seg0);
+        const int U = fta_build_kv_masks<TT>(a, bh, wk, Tb, seg0, segn, bits_lds, sBits, sMask, sList, s_tmp);
         if (U == 0) continue;
         const int nsteps = (U + CS - 1) / CS;
 
@@ -1138,6 +1177,243 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
 }
 
 // ----------------------------------------------------------------------------
+// dK / dV with the work of each key tile split over two waves (KV blocks of 33
+// to 64 keys, D = 64 or 128).  The WG owns the two 32-key tiles of one KV block;
+// wave (tt, hv) holds K (hv = 0) or V (hv = 1) of tile tt and the dK / dV
+// accumulators of the d-half hv.  Per chunk of 32 queries:
+//   hv = 0:  S = Q K^T,  P = 2^{c S - lse2}   -> LDS
+//   hv = 1:  dP = dO V^T                       -> LDS
+//   both:    dS = P (dP - delta) from the exchanged values (same fp32 operations
+//            in both waves), dV[:, half] += P^T dO[:, half], dK[:, half] += dS^T Q[:, half].
+// Each wave keeps half the accumulators and one of K / V, so a WG fits twice on
+// a CU (registers <= 256 per lane, LDS < 80 KB): one WG's mask building and
+// gather latency overlap the other's MFMAs.  One chunk per step; NST steps of Q,
+// dO, lse and delta in flight through LDS DMA, as in fta_sparse_dkv_kernel.
+// ----------------------------------------------------------------------------
+template <int D>
+struct DkvSplitShape {
+    static constexpr int NW = 4;
+    static constexpr int NTHR = 256;
+    static constexpr int QSEG = D / 8;
+    static constexpr int TILE = 32 * QSEG;              // 16-byte slots per 32-row tile
+    static constexpr int LQ = 2 * TILE / NTHR;          // DMA instructions per wave per step (Q, dO)
+    static constexpr int L = LQ + 1;                    // + lse / delta
+    static constexpr int LD_OFF = 2 * TILE * 16;        // byte offset of lse / delta in a step
+    static constexpr int STAGE_B = LD_OFF + NW * 256;
+    static constexpr int NST = (D <= 64) ? 4 : 3;
+    static_assert(2 * TILE % NTHR == 0, "whole DMA instructions per wave");
+    static_assert(NST * STAGE_B + 2 * 2 * 32 * 32 * 4 + 3 * kSegC * 4 + 2 * kBitsW * 4 + 64 <= 80 * 1024,
+                  "two WGs per CU");
+};
+
+template <int DT, int D>
+__global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a) {
+    using E = Elem<DT>;
+    using Sh = DkvSplitShape<D>;
+    constexpr int NW = Sh::NW, QSEG = Sh::QSEG, TILE = Sh::TILE, LQ = Sh::LQ, NST = Sh::NST;
+    using SW = FtaSwz<QSEG>;
+    constexpr int KS = D / 16;
+    constexpr int DH = D / 64;  // 32-column d tiles per half
+    constexpr int TT = 2;
+    __shared__ __align__(1024) unsigned char sStage[NST][Sh::STAGE_B];
+    __shared__ float sX[TT][2][16][64];  // [tile][P, dP][i][lane]
+    __shared__ uint32_t sMask[TT][kSegC];
+    __shared__ int sList[kSegC];
+    __shared__ uint32_t sBits[TT][kBitsW];
+    __shared__ int s_tmp[8];
+
+    const int wgi = fta_xcd_remap(blockIdx.x, a.total);
+    const int bh = wgi / a.wg_per_bh;
+    const int wk = wgi - bh * a.wg_per_bh;  // KV block
+    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hf = lane >> 5;
+    const int tt = wave & 1, hv = wave >> 1;
+    const int Tb = 2;
+
+    const int krel = 32 * tt + (lane & 31);  // key of this lane's column, relative to block start
+    const int tk = wk * a.kvb - a.kv_pad + krel;
+    const bool kok = krel < a.kvb && tk >= 0 && tk < a.N;
+
+    const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
+    const uint16_t* dp = a.dout + b * a.d_sb + h * a.d_sh;
+    const float* lsep = a.lse_in + (int64_t)bh * a.N;
+    const float* dlp = a.delta_in + (int64_t)bh * a.N;
+
+    // K (hv = 0) or V (hv = 1) rows of this tile, full D
+    uint4 kv[KS];
+    {
+        const uint16_t* src = hv ? a.v + b * a.v_sb + h * a.v_sh : a.k + b * a.k_sb + h * a.k_sh;
+        const int64_t sn = hv ? a.v_sn : a.k_sn;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int d = ks * 16 + hf * 8;
+            kv[ks] = (kok && d < a.Dreal) ? *reinterpret_cast<const uint4*>(src + (int64_t)tk * sn + d) : fta_zero4();
+        }
+    }
+    const bool bits_lds = fta_stage_kv_bits<TT>(a, bh, wk, Tb, sBits);  // completes the loads above too
+    fta_wait_vmcnt<0>();
+
+    // Per-lane DMA sources (as in fta_sparse_dkv_kernel with one chunk slot):
+    // instruction i of this wave fills 1 KB block blk = i * NW + wave of the
+    // [Q tile][dO tile] step; roff[i] = row * stride + column, in bytes.
+    int64_t roff[LQ];
+#pragma unroll
+    for (int i = 0; i < LQ; ++i) {
+        const int blk = i * NW + wave;
+        const int ten = (blk * 64) / TILE;
+        const int r2 = (blk * 64 + lane) % TILE;
+        const int row = r2 / QSEG;
+        int j = SW::slot(row, r2 - row * QSEG);
+        if (j * 8 >= a.Dreal) j = 0;  // columns past D: any finite data (never stored)
+        roff[i] = 2 * ((int64_t)row * (ten == 1 ? a.d_sn : a.q_sn) + j * 8);
+    }
+    // lse / delta: wave 0's 256 bytes hold [lse 32][delta 32] (other waves load a duplicate)
+    const int lv = wave * 64 + lane;
+    const bool l_isd = lv >= 32 && lv < 64;
+    const float* l_base = l_isd ? dlp : lsep;
+    const int l_row = lv & 31;
+    const uint32_t lds0 = fta_lds_addr(&sStage[0][0]);
+
+    f32x16 dka[DH], dva[DH];
+#pragma unroll
+    for (int dt = 0; dt < DH; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            dka[dt][i] = 0.f;
+            dva[dt][i] = 0.f;
+        }
+
+    for (int seg0 = 0; seg0 < a.NC; seg0 += kSegC) {
+        const int segn = min(kSegC, a.NC - seg0);
+        const int U = fta_build_kv_masks<TT>(a, bh, wk, Tb, seg0, segn, bits_lds, sBits, sMask, sList, s_tmp);
+        if (U == 0) continue;
+
+        // gather chunk list entry k into stage buffer st
+        auto issue = [&](int st, int k) {
+            const uint32_t sbase = lds0 + st * Sh::STAGE_B;
+            const int c = __builtin_amdgcn_readfirstlane(seg0 + sList[k]);
+            const int t0 = 32 * c - a.q_pad;
+            if (t0 >= 0 && t0 + 31 < a.N) {
+#pragma unroll
+                for (int i = 0; i < LQ; ++i) {
+                    const int blk = i * NW + wave;
+                    const int ten = (blk * 64) / TILE;
+                    const char* base =
+                        reinterpret_cast<const char*>(ten == 1 ? dp + (int64_t)t0 * a.d_sn : qp + (int64_t)t0 * a.q_sn);
+                    fta_dma16_at(base + roff[i], sbase + blk * 1024);
+                }
+            } else {  // a chunk at a sequence edge: clamp its rows (masked off) into [0, N)
+#pragma unroll
+                for (int i = 0; i < LQ; ++i) {
+                    const int blk = i * NW + wave;
+                    const int ten = (blk * 64) / TILE;
+                    const int r2 = (blk * 64 + lane) % TILE;
+                    const int row = r2 / QSEG;
+                    int j = SW::slot(row, r2 - row * QSEG);
+                    if (j * 8 >= a.Dreal) j = 0;
+                    const int t = min(max(t0 + row, 0), a.N - 1);
+                    fta_dma16_at((ten == 1 ? dp + (int64_t)t * a.d_sn : qp + (int64_t)t * a.q_sn) + j * 8,
+                                 sbase + blk * 1024);
+                }
+            }
+            const int t = min(max(t0 + l_row, 0), a.N - 1);
+            fta_dma4_at(l_base + t, sbase + Sh::LD_OFF + wave * 256);
+        };
+
+#pragma unroll
+        for (int k = 0; k < NST - 1; ++k)
+            if (k < U) issue(k, k);
+        int cur = 0;
+        for (int k = 0; k < U; ++k) {
+            if (k + NST - 2 < U)
+                fta_wait_vmcnt<Sh::L * (NST - 2)>();
+            else
+                fta_wait_vmcnt<0>();
+            __syncthreads();  // step k visible; step k - 1's buffer and the exchange area are free
+            if (k + NST - 1 < U) issue(cur == 0 ? NST - 1 : cur - 1, k + NST - 1);
+            const uint32_t mk = __builtin_amdgcn_readfirstlane(sMask[tt][sList[k]]);
+            const uint16_t* qb = reinterpret_cast<const uint16_t*>(&sStage[cur][0]);
+            const uint16_t* ob = qb + TILE * 8;
+            const float* ld = reinterpret_cast<const float*>(&sStage[cur][Sh::LD_OFF]);
+            f32x16 own;  // P (hv = 0) or dP (hv = 1)
+            if (mk) {
+                const uint16_t* ab = hv ? ob : qb;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) own[i] = 0.f;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    own = E::mma(*reinterpret_cast<const uint4*>(ab + SW::off(lane & 31, 2 * ks + hf)), kv[ks], own);
+                if (hv == 0) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int r = c_row(i, lane);
+                        // a selected row with a valid key has a finite lse
+                        const bool ok = kok && ((mk >> r) & 1u);
+                        const float ex = fta_exp2(fmaf(own[i], a.c, -ld[r] * 1.4426950408889634f));
+                        own[i] = ok ? ex : 0.f;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sX[tt][hv][i][lane] = own[i];
+            }
+            __syncthreads();  // both halves of every tile exchanged
+            if (mk) {
+                uint4 pf[2], dsf[2];
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    float pv[8], dv8[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int i = 8 * ks + e;
+                        const float other = sX[tt][hv ^ 1][i][lane];
+                        const float p = hv ? other : own[i];
+                        const float dpv = hv ? own[i] : other;
+                        pv[e] = p;
+                        dv8[e] = p * (dpv - ld[32 + c_row(i, lane)]);
+                    }
+                    pf[ks] = make_uint4(E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
+                                        E::pack2(pv[6], pv[7]));
+                    dsf[ks] = make_uint4(E::pack2(dv8[0], dv8[1]), E::pack2(dv8[2], dv8[3]),
+                                         E::pack2(dv8[4], dv8[5]), E::pack2(dv8[6], dv8[7]));
+                }
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                    for (int dt = 0; dt < DH; ++dt) {
+                        const int d0 = (hv * DH + dt) * 32;
+                        dva[dt] = E::mma(pf[ks], fta_tr_frag_sw<QSEG>(ob, ks * 16, d0, lane), dva[dt]);
+                        dka[dt] = E::mma(dsf[ks], fta_tr_frag_sw<QSEG>(qb, ks * 16, d0, lane), dka[dt]);
+                    }
+                }
+            }
+            cur = (cur == NST - 1) ? 0 : cur + 1;
+        }
+        __syncthreads();  // all waves done with the stage buffers, sMask and sList
+    }
+
+    // C layout: lane column = d, rows = keys c_row(i, lane)
+    uint16_t* kout = a.out0 + b * a.o0_sb + h * a.o0_sh;
+    uint16_t* vout = a.out1 + b * a.o1_sb + h * a.o1_sh;
+#pragma unroll
+    for (int dt = 0; dt < DH; ++dt) {
+        const int d = (hv * DH + dt) * 32 + (lane & 31);
+        if (d >= a.Dreal) continue;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int kr = 32 * tt + c_row(i, lane);
+            const int t = wk * a.kvb - a.kv_pad + kr;
+            if (kr < a.kvb && t >= 0 && t < a.N) {
+                const uint32_t pk = E::pack2(dka[dt][i] * a.scale, dva[dt][i]);
+                kout[(int64_t)t * a.o0_sn + d] = (uint16_t)(pk & 0xffffu);
+                vout[(int64_t)t * a.o1_sn + d] = (uint16_t)(pk >> 16);
+            }
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
 // Host side
 // ----------------------------------------------------------------------------
 namespace {
@@ -1261,9 +1537,23 @@ int launch_dkv_dt(AttnArgs& a, int Dk, int Tb, int B, int H, int ntiles, hipStre
             go(fta_sparse_dkv_kernel<DT, DK, NW, 1>, NW, NW);                                \
         break;
         FTA_DKV(32, 8, 1, 4, 2, 4)
-        FTA_DKV(64, 8, 1, 4, 2, 4)
+        case 64:
+            if (Tb == 2)
+                go(fta_sparse_dkv_split_kernel<DT, 64>, 2, 4);
+            else if (Tb == 1)
+                go(fta_sparse_dkv_kernel<DT, 64, 1, 4>, 1, 4);
+            else
+                go(fta_sparse_dkv_kernel<DT, 64, 8, 1>, 8, 8);
+            break;
         FTA_DKV(96, 4, 1, 4, 2, 2)
-        FTA_DKV(128, 4, 1, 4, 2, 2)
+        case 128:
+            if (Tb == 2)
+                go(fta_sparse_dkv_split_kernel<DT, 128>, 2, 4);
+            else if (Tb == 1)
+                go(fta_sparse_dkv_kernel<DT, 128, 1, 4>, 1, 4);
+            else
+                go(fta_sparse_dkv_kernel<DT, 128, 4, 1>, 4, 4);
+            break;
         FTA_DKV(160, 4, 2, 2, 2, 2)
         FTA_DKV(256, 4, 4, 1, 4, 1)
 #undef FTA_DKV
