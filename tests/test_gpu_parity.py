@@ -28,6 +28,7 @@ SCORE_CASES = [
     (1, 520, 1, 96, 128, (0, 120), torch.bfloat16, "bnc"),
     (1, 256, 2, 40, 64, (0, 0), torch.float32, "bnc"),
     (1, 200, 2, 256, 64, (30, 26), torch.bfloat16, "bnc"),
+    (1, 40, 2, 80, 64, (0, 24), torch.bfloat16, "bnc"),
 ]
 
 
@@ -156,6 +157,14 @@ ATTN_CASES = [
     # more than 512 query chunks / KV blocks: masks are built in several segments
     (1, 17024, 1, 64, 32, 64, (0, 0), (0, 0), 4, torch.bfloat16),
     (1, 16448, 1, 32, 32, 16, (0, 0), (0, 0), 3, torch.bfloat16),
+    # more than 1024 query chunks (dK/dV segments) and membership rows wider than
+    # the 64 words staged in LDS (QM = 2063 q-blocks -> 65 words)
+    (1, 33000, 1, 64, 16, 64, (0, 8), (0, 24), 3, torch.bfloat16),
+    (1, 33000, 1, 32, 16, 64, (0, 8), (0, 24), 3, torch.float16),
+    # head dims padded up to the kernel's (48 -> 64, 80 -> 96), and N below one block
+    (1, 700, 2, 48, 32, 64, (0, 4), (0, 4), 8, torch.bfloat16),
+    (1, 500, 2, 80, 20, 64, (0, 0), (0, 12), 6, torch.float16),
+    (1, 40, 2, 64, 8, 64, (0, 0), (0, 24), 2, torch.bfloat16),
 ]
 
 
