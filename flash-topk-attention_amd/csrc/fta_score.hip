@@ -752,20 +752,23 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
                 tot[t] = part + fta_xor32(part);
             }
         }
-        float lse_b[2];
+        // lane owns query (lane & 31) of tile (lane >> 5): only its block lse is stored
+        const float tot_m = (lane >= 32) ? tot[1] : tot[0];
+        const float R_m = (lane >= 32) ? R[1] : R[0];
+        const float mine = (tot_m > 0.f) ? R_m + fta_log2(tot_m) : -FTA_INF;
+        L[0] += tot[0];
+        L[1] += tot[1];
+        if (__ballot(tot[0] > 0x1p40f || tot[1] > 0x1p40f) != 0ull) {
+            // rare: rebase a large row total on this block's lse
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            lse_b[t] = (tot[t] > 0.f) ? R[t] + fta_log2(tot[t]) : -FTA_INF;
-            L[t] += tot[t];
-            if (tot[t] > 0x1p40f) {
-                const float Rn = lse_b[t];
-                L[t] *= fta_exp2(R[t] - Rn);
-                R[t] = Rn;
-            }
+            for (int t = 0; t < 2; ++t)
+                if (tot[t] > 0x1p40f) {
+                    const float Rn = R[t] + fta_log2(tot[t]);
+                    L[t] *= fta_exp2(R[t] - Rn);
+                    R[t] = Rn;
+                }
         }
-        // lane owns query (lane & 31) of tile (lane >> 5)
         const int qi = qbase + lane;
-        const float mine = (lane >= 32) ? lse_b[1] : lse_b[0];
         if (qi < N) blk_lse[((int64_t)bh * M + m) * N + qi] = mine;
         if (kgroups > 0) {
             float key = mine;
@@ -786,8 +789,7 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
             }
         }
     };
-    // every block but the last always produces the next block's half 0, so the
-    // loop-carried scores are written on all paths (no register copies)
+    // every block but the last always produces the next block's half 0
     for (int m = 0; m + 1 < M; ++m) block(m);
     block(M - 1);
 
