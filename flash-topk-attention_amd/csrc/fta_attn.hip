@@ -770,6 +770,207 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// dQ, pipelined (D = 64 and 128).  The arithmetic of fta_sparse_dq_kernel; the
+// 64-key K and V chunks are gathered by LDS DMA into NST swizzled stage buffers
+// (as in fta_sparse_fwd_pipe_kernel), NST - 1 chunks ahead, so the gather
+// latency is hidden and the operand reads (K and V rows, K^T transposed) are
+// free of LDS bank conflicts.
+// ----------------------------------------------------------------------------
+template <int DT, int D>
+__global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) {
+    using E = Elem<DT>;
+    constexpr int NW = 8, T = 8;
+    using Sh = FwdPipeShape<D, NW>;
+    constexpr int QSEG = Sh::QSEG, LQ = Sh::LQ, NST = Sh::NST;
+    using SW = FtaSwz<QSEG>;
+    constexpr int KS = D / 16;
+    constexpr int DT32 = D / 32;
+    __shared__ __align__(1024) unsigned char sStage[NST][Sh::STAGE_B];
+    __shared__ uint32_t sMask[T][kSeg];
+    __shared__ int sList[kSeg];
+    __shared__ int s_tmp[8];
+
+    const int wgi = fta_xcd_remap(blockIdx.x, a.total);
+    const int bh = wgi / a.wg_per_bh;
+    const int wq = wgi - bh * a.wg_per_bh;
+    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hf = lane >> 5;
+    const int p0 = wq * 32 * T;
+
+    const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
+    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+    const uint16_t* dp = a.dout + b * a.d_sb + h * a.d_sh;
+
+    const int tq = p0 + 32 * wave + (lane & 31) - a.q_pad;
+    const bool qok = tq >= 0 && tq < a.N;
+    uint4 qf[KS], df[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const int d = ks * 16 + hf * 8;
+        const bool ok = qok && d < a.Dreal;
+        qf[ks] = ok ? *reinterpret_cast<const uint4*>(qp + (int64_t)tq * a.q_sn + d) : fta_zero4();
+        df[ks] = ok ? *reinterpret_cast<const uint4*>(dp + (int64_t)tq * a.d_sn + d) : fta_zero4();
+    }
+    float lse2 = -FTA_INF, dl = 0.f;
+    if (qok) {
+        lse2 = a.lse_in[(int64_t)bh * a.N + tq] * 1.4426950408889634f;
+        dl = a.delta_in[(int64_t)bh * a.N + tq];
+    }
+    const bool rowlive = lse2 != -FTA_INF;
+    // complete the register loads: the DMAs below are invisible to the compiler
+    fta_wait_vmcnt<0>();
+
+    f32x16 acc[DT32];
+#pragma unroll
+    for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+
+    // Per-lane DMA sources: instruction i of this wave fills the 1 KB block
+    // i * NW + wave of each tensor chunk; koff / voff = row * stride + column.
+    int koff[LQ], voff[LQ];
+#pragma unroll
+    for (int i = 0; i < LQ; ++i) {
+        const int sidx = (i * NW + wave) * 64 + lane;
+        const int row = sidx / QSEG;
+        int j = SW::slot(row, sidx - row * QSEG);
+        if (j * 8 >= a.Dreal) j = 0;  // columns past D: zero q / dO columns, outputs never stored
+        koff[i] = row * (int)a.k_sn + j * 8;
+        voff[i] = row * (int)a.v_sn + j * 8;
+    }
+    const uint32_t lds0 = fta_lds_addr(&sStage[0][0]);
+    const int nch = (a.kvb + 63) >> 6;
+
+    for (int seg0 = 0; seg0 < a.Mkv; seg0 += kSeg) {
+        const int segn = min(kSeg, a.Mkv - seg0);
+        const int U = fta_build_q_masks<T>(a, bh, p0, seg0, segn, sMask, sList, s_tmp);
+        if (U == 0) continue;
+        const int iters = U * nch;
+
+        auto issue = [&](int st, int it) {
+            const uint32_t sb = lds0 + st * Sh::STAGE_B;
+            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int m = __builtin_amdgcn_readfirstlane(seg0 + sList[u]);
+            const int kb = m * a.kvb - a.kv_pad + ch * 64;
+            const int rem = a.kvb - ch * 64;
+            if (kb >= 0 && kb + 64 <= a.N && rem >= 64) {
+                const uint16_t* kbp = kp + (int64_t)kb * a.k_sn;
+                const uint16_t* vbp = vp + (int64_t)kb * a.v_sn;
+#pragma unroll
+                for (int i = 0; i < LQ; ++i) fta_dma16_at(kbp + koff[i], sb + (i * NW + wave) * 1024);
+#pragma unroll
+                for (int i = 0; i < LQ; ++i) fta_dma16_at(vbp + voff[i], sb + Sh::TEN_B + (i * NW + wave) * 1024);
+            } else {  // chunk at a sequence / block edge: clamp rows into [0, N) (masked below)
+#pragma unroll
+                for (int i = 0; i < LQ; ++i) {
+                    const int sidx = (i * NW + wave) * 64 + lane;
+                    const int row = sidx / QSEG;
+                    int j = SW::slot(row, sidx - row * QSEG);
+                    if (j * 8 >= a.Dreal) j = 0;
+                    const int t = min(max(kb + row, 0), a.N - 1);
+                    fta_dma16_at(kp + (int64_t)t * a.k_sn + j * 8, sb + (i * NW + wave) * 1024);
+                    fta_dma16_at(vp + (int64_t)t * a.v_sn + j * 8, sb + Sh::TEN_B + (i * NW + wave) * 1024);
+                }
+            }
+        };
+
+#pragma unroll
+        for (int k = 0; k < NST - 1; ++k)
+            if (k < iters) issue(k, k);
+        int cur = 0;
+        for (int it = 0; it < iters; ++it) {
+            if (it + NST - 2 < iters)
+                fta_wait_vmcnt<2 * LQ * (NST - 2)>();
+            else
+                fta_wait_vmcnt<0>();
+            __syncthreads();  // chunk it visible; every wave is past chunk it - 1
+            if (it + NST - 1 < iters) issue(cur == 0 ? NST - 1 : cur - 1, it + NST - 1);
+
+            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int ml = sList[u];
+            const int m = seg0 + ml;
+            const int kb = m * a.kvb - a.kv_pad + ch * 64;
+            const int rem = a.kvb - ch * 64;
+            const bool two = rem > 32;
+            const uint32_t mk = __builtin_amdgcn_readfirstlane(sMask[wave][ml]);
+            if (mk) {
+                const uint16_t* kbase = reinterpret_cast<const uint16_t*>(&sStage[cur][0]);
+                const uint16_t* vbase = kbase + Sh::TEN_B / 2;
+                f32x16 s[2], dpv[2];
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        s[sb][i] = 0.f;
+                        dpv[sb][i] = 0.f;
+                    }
+                const int nsb = two ? 2 : 1;
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    if (sb >= nsb) break;
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        const int off = SW::off(sb * 32 + (lane & 31), 2 * ks + hf);
+                        s[sb] = E::mma(*reinterpret_cast<const uint4*>(kbase + off), qf[ks], s[sb]);
+                        dpv[sb] = E::mma(*reinterpret_cast<const uint4*>(vbase + off), df[ks], dpv[sb]);
+                    }
+                }
+                // valid keys [klo, khi) relative to kb; a lane whose query column
+                // is not selected gets the empty range (branch-free masking)
+                const bool colok = rowlive && ((mk >> (lane & 31)) & 1u);
+                const int klo = colok ? max(0, -kb) : 64;
+                const int khi = colok ? min(min(rem, 64), a.N - kb) : 0;
+                const unsigned kw = (unsigned)max(khi - klo, 0);  // a chunk past N has khi < klo
+                uint4 dsf[4];
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    float dsv[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int sb = ks >> 1, i = 8 * (ks & 1) + e;
+                        const int rel = sb * 32 + c_row(i, lane);
+                        const bool ok = (unsigned)(rel - klo) < kw;
+                        const float ex = fta_exp2(fmaf(s[sb][i], a.c, -lse2));
+                        const float p = ok ? ex : 0.f;
+                        dsv[e] = p * (dpv[sb][i] - dl);
+                    }
+                    dsf[ks] = make_uint4(E::pack2(dsv[0], dsv[1]), E::pack2(dsv[2], dsv[3]),
+                                         E::pack2(dsv[4], dsv[5]), E::pack2(dsv[6], dsv[7]));
+                }
+                const int nks = two ? 4 : 2;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    if (ks >= nks) break;
+#pragma unroll
+                    for (int dt = 0; dt < DT32; ++dt)
+                        acc[dt] = E::mma(fta_tr_frag_sw<QSEG>(kbase, ks * 16, dt * 32, lane), dsf[ks], acc[dt]);
+                }
+            }
+            cur = (cur == NST - 1) ? 0 : cur + 1;
+        }
+        __syncthreads();  // every wave is done with sMask / sList before the next segment rebuilds them
+    }
+
+    if (!qok) return;
+    uint16_t* op = a.out0 + b * a.o0_sb + h * a.o0_sh + (int64_t)tq * a.o0_sn;
+#pragma unroll
+    for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const int d = dt * 32 + c_row(i, lane);
+            if (d < a.Dreal) {
+                uint2 w;
+                w.x = E::pack2(acc[dt][i] * a.scale, acc[dt][i + 1] * a.scale);
+                w.y = E::pack2(acc[dt][i + 2] * a.scale, acc[dt][i + 3] * a.scale);
+                *reinterpret_cast<uint2*>(op + d) = w;
+            }
+        }
+}
+
+// ----------------------------------------------------------------------------
 // dK / dV.  WG = TT x CS waves.  The WG owns TT 32-key tiles (consecutive
 // (KV block, 32-key sub-tile) pairs); wave w works on tile w % TT and chunk
 // slot w / TT.  Column masks over 32-query chunks come from the membership
@@ -1495,15 +1696,27 @@ int launch_fwd_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
 
 template <int DT>
 int launch_dq_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
+    // the pipelined kernel keeps per-lane row offsets (64 rows x stride) in 32 bits
+    const bool pipe_ok = a.k_sn <= (1 << 24) && a.v_sn <= (1 << 24);
     switch (Dk) {
 #define FTA_DQ(DK, NW)                                                                                  \
     case DK:                                                                                             \
         hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, DK, NW>), dim3(grid), dim3(NW * 64), 0, st, a);     \
         break;
         FTA_DQ(32, 8)
-        FTA_DQ(64, 8)
+        case 64:
+            if (pipe_ok)
+                hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 64>), dim3(grid), dim3(512), 0, st, a);
+            else
+                hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, 64, 8>), dim3(grid), dim3(512), 0, st, a);
+            break;
         FTA_DQ(96, 8)
-        FTA_DQ(128, 8)
+        case 128:
+            if (pipe_ok)
+                hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 128>), dim3(grid), dim3(512), 0, st, a);
+            else
+                hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, 128, 8>), dim3(grid), dim3(512), 0, st, a);
+            break;
         FTA_DQ(160, 4)
         FTA_DQ(256, 4)
 #undef FTA_DQ
