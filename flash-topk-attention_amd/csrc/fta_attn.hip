@@ -51,6 +51,7 @@ struct AttnArgs {
     const float* lse_in;    // backward input
     const float* delta_in;  // backward input
     int H, N, Dreal, g, kvb, q_pad, kv_pad, Mkv, NC;
+    int Hk, G;  // K/V heads and query heads per K/V head (G = H / Hk; 1 without GQA)
     float c, scale;
     int wg_per_bh, total;
 };
@@ -161,8 +162,8 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_kernel(AttnArgs a) 
     const int p0 = wq * 32 * T;
 
     const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
-    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
-    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + (h / a.G) * a.k_sh;
+    const uint16_t* vp = a.v + b * a.v_sb + (h / a.G) * a.v_sh;
 
     uint4 qf[TPW][KS];
 #pragma unroll
@@ -398,8 +399,8 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
     const int p0 = wq * 32 * T;
 
     const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
-    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
-    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + (h / a.G) * a.k_sh;
+    const uint16_t* vp = a.v + b * a.v_sb + (h / a.G) * a.v_sh;
 
     uint4 qf[KS];
     {
@@ -617,8 +618,8 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
     const int p0 = wq * 32 * T;
 
     const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
-    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
-    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + (h / a.G) * a.k_sh;
+    const uint16_t* vp = a.v + b * a.v_sb + (h / a.G) * a.v_sh;
     const uint16_t* dp = a.dout + b * a.d_sb + h * a.d_sh;
 
     const int tq = p0 + 32 * wave + (lane & 31) - a.q_pad;
@@ -800,8 +801,8 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
     const int p0 = wq * 32 * T;
 
     const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
-    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
-    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
+    const uint16_t* kp = a.k + b * a.k_sb + (h / a.G) * a.k_sh;
+    const uint16_t* vp = a.v + b * a.v_sb + (h / a.G) * a.v_sh;
     const uint16_t* dp = a.dout + b * a.d_sb + h * a.d_sh;
 
     const int tq = p0 + 32 * wave + (lane & 31) - a.q_pad;
@@ -1094,7 +1095,7 @@ struct DkvShape {
     static_assert((NST - 2) * L < 64, "vmcnt range");
 };
 
-template <int DT, int D, int TT, int CS>
+template <int DT, int D, int TT, int CS, bool GQA = false>
 __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArgs a) {
     using E = Elem<DT>;
     using Sh = DkvShape<D, TT, CS>;
@@ -1110,9 +1111,9 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
     __shared__ int s_tmp[8];
 
     const int wgi = fta_xcd_remap(blockIdx.x, a.total);
-    const int bh = wgi / a.wg_per_bh;
-    const int wk = wgi - bh * a.wg_per_bh;
-    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    const int bhk = wgi / a.wg_per_bh;  // (b, K/V head)
+    const int wk = wgi - bhk * a.wg_per_bh;
+    const int b = bhk / a.Hk, hk = bhk - (bhk / a.Hk) * a.Hk;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hf = lane >> 5;
@@ -1128,12 +1129,13 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
     const int tk = mblk * a.kvb - a.kv_pad + krel;
     const bool kok = tile_live && krel < a.kvb && tk >= 0 && tk < a.N;
 
-    const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
-    const uint16_t* kp = a.k + b * a.k_sb + h * a.k_sh;
-    const uint16_t* vp = a.v + b * a.v_sb + h * a.v_sh;
-    const uint16_t* dp = a.dout + b * a.d_sb + h * a.d_sh;
-    const float* lsep = a.lse_in + (int64_t)bh * a.N;
-    const float* dlp = a.delta_in + (int64_t)bh * a.N;
+    const uint16_t* kp = a.k + b * a.k_sb + hk * a.k_sh;
+    const uint16_t* vp = a.v + b * a.v_sb + hk * a.v_sh;
+    // query-side operands of the query head being walked (set per head below)
+    const uint16_t* qp = nullptr;
+    const uint16_t* dp = nullptr;
+    const float* lsep = nullptr;
+    const float* dlp = nullptr;
 
     uint4 kf[KS], vf[KS];
 #pragma unroll
@@ -1169,7 +1171,7 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
     const bool l_isd = lv >= 32 * CS && lv < 64 * CS;
     const int l_sl = (lv < 64 * CS) ? ((lv >> 5) % CS) : 0;
     const int l_row = lv & 31;
-    const float* l_base = l_isd ? dlp : lsep;
+    const float* l_base = nullptr;
     const uint32_t lds0 = fta_lds_addr(&sStage[0][0]);
 
     f32x16 dka[DT32], dva[DT32];
@@ -1181,146 +1183,159 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
             dva[dt][i] = 0.f;
         }
 
-    const bool bits_lds = fta_stage_kv_bits<TT>(a, bh, wk, Tb, sBits);
-    for (int seg0 = 0; seg0 < a.NC; seg0 += kSegC) {
-        const int segn = min(kSegC, a.NC - seg0);
-        const int U = fta_build_kv_masks<TT>(a, bh, wk, Tb, seg0, segn, bits_lds, sBits, sMask, sList, s_tmp);
-        if (U == 0) continue;
-        const int nsteps = (U + CS - 1) / CS;
+    // the query heads that share this K/V head (one without GQA): their
+    // membership, Q, dO, lse and delta; dK / dV accumulate over all of them
+    const int ngq = GQA ? a.G : 1;  // a constant 1 without GQA: no head loop in that code
+    for (int gq = 0; gq < ngq; ++gq) {
+        const int h = hk * a.G + gq;
+        const int bh = b * a.H + h;
+        qp = a.q + b * a.q_sb + h * a.q_sh;
+        dp = a.dout + b * a.d_sb + h * a.d_sh;
+        lsep = a.lse_in + (int64_t)bh * a.N;
+        dlp = a.delta_in + (int64_t)bh * a.N;
+        l_base = l_isd ? dlp : lsep;
+        if (gq > 0) __syncthreads();  // the previous head's membership rows are no longer read
+        const bool bits_lds = fta_stage_kv_bits<TT>(a, bh, wk, Tb, sBits);
+        for (int seg0 = 0; seg0 < a.NC; seg0 += kSegC) {
+            const int segn = min(kSegC, a.NC - seg0);
+            const int U = fta_build_kv_masks<TT>(a, bh, wk, Tb, seg0, segn, bits_lds, sBits, sMask, sList, s_tmp);
+            if (U == 0) continue;
+            const int nsteps = (U + CS - 1) / CS;
 
-        // gather step k (chunks k*CS .. k*CS + CS - 1 of the union list) into stage buffer st
-        auto issue = [&](int st, int k) {
-            const uint32_t sbase = lds0 + st * Sh::STAGE_B;
-            const int u0 = k * CS;
-            int cs[CS];
-            bool inner = true;  // every row of every chunk lies in [0, N)
+            // gather step k (chunks k*CS .. k*CS + CS - 1 of the union list) into stage buffer st
+            auto issue = [&](int st, int k) {
+                const uint32_t sbase = lds0 + st * Sh::STAGE_B;
+                const int u0 = k * CS;
+                int cs[CS];
+                bool inner = true;  // every row of every chunk lies in [0, N)
 #pragma unroll
-            for (int sl = 0; sl < CS; ++sl) {
-                cs[sl] = __builtin_amdgcn_readfirstlane(seg0 + sList[min(u0 + sl, U - 1)]);
-                const int t0 = 32 * cs[sl] - a.q_pad;
-                inner = inner && t0 >= 0 && t0 + 31 < a.N;
-            }
-            if (inner) {
-#pragma unroll
-                for (int i = 0; i < LQ; ++i) {
-                    const int blk = i * NW + wave;
-                    const int ten = (blk * 64) / (CS * TILE);
-                    const int sl = ((blk * 64) / TILE) % CS;
-                    const int64_t t0 = 32 * cs[sl] - a.q_pad;
-                    const char* base = reinterpret_cast<const char*>(ten == 1 ? dp + t0 * a.d_sn : qp + t0 * a.q_sn);
-                    fta_dma16_at(base + roff[i], sbase + blk * 1024);
+                for (int sl = 0; sl < CS; ++sl) {
+                    cs[sl] = __builtin_amdgcn_readfirstlane(seg0 + sList[min(u0 + sl, U - 1)]);
+                    const int t0 = 32 * cs[sl] - a.q_pad;
+                    inner = inner && t0 >= 0 && t0 + 31 < a.N;
                 }
-            } else {  // a chunk at a sequence edge: clamp its rows (masked off) into [0, N)
+                if (inner) {
 #pragma unroll
-                for (int i = 0; i < LQ; ++i) {
-                    const int blk = i * NW + wave;
-                    const int ten = (blk * 64) / (CS * TILE);
-                    const int sl = ((blk * 64) / TILE) % CS;
-                    const int r2 = (blk * 64 + lane) % TILE;
-                    const int row = r2 / QSEG;
-                    int j = SW::slot(row, r2 - row * QSEG);
-                    if (j * 8 >= a.Dreal) j = 0;
-                    const int t = min(max(32 * cs[sl] - a.q_pad + row, 0), a.N - 1);
-                    fta_dma16_at((ten == 1 ? dp + (int64_t)t * a.d_sn : qp + (int64_t)t * a.q_sn) + j * 8,
-                                 sbase + blk * 1024);
-                }
-            }
-            int c = cs[0];
-#pragma unroll
-            for (int sl = 1; sl < CS; ++sl) c = (l_sl == sl) ? cs[sl] : c;
-            const int t = min(max(32 * c - a.q_pad + l_row, 0), a.N - 1);
-            fta_dma4_at(l_base + t, sbase + Sh::LD_OFF + wave * 256);
-        };
-
-#pragma unroll
-        for (int k = 0; k < NST - 1; ++k)
-            if (k < nsteps) issue(k, k);
-        int cur = 0;  // stage buffer of step k
-        for (int k = 0; k < nsteps; ++k) {
-            if (k + NST - 2 < nsteps)
-                fta_wait_vmcnt<Sh::L * (NST - 2)>();
-            else
-                fta_wait_vmcnt<0>();
-            __syncthreads();  // step k visible to all waves; step k - 1's buffer is free
-            if (k + NST - 1 < nsteps) issue(cur == 0 ? NST - 1 : cur - 1, k + NST - 1);
-            const int u = k * CS + slot;
-            const uint32_t mk = (u < U) ? __builtin_amdgcn_readfirstlane(sMask[tt][sList[u]]) : 0u;
-            if (mk) {
-                const uint16_t* qb = reinterpret_cast<const uint16_t*>(&sStage[cur][0]) + slot * TILE * 8;
-                const uint16_t* ob = qb + CS * TILE * 8;
-                const float* ld = reinterpret_cast<const float*>(&sStage[cur][Sh::LD_OFF]);
-                // Phased so that LDS latency overlaps MFMA work without exceeding the
-                // 256 VGPRs: (1) operand rows, (2) S and dP MFMAs, (3) transposed
-                // operands and lse / delta (while those MFMAs run), (4) softmax,
-                // (5) dV and dK MFMAs.  sched_barrier keeps the phases in order.
-                uint4 qa[KS], oa[KS];
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const int off = SW::off(lane & 31, 2 * ks + hf);
-                    qa[ks] = *reinterpret_cast<const uint4*>(qb + off);
-                    oa[ks] = *reinterpret_cast<const uint4*>(ob + off);
-                }
-                f32x16 s, dpv;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    s[i] = 0.f;
-                    dpv[i] = 0.f;
-                }
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    s = E::mma(qa[ks], kf[ks], s);
-                    dpv = E::mma(oa[ks], vf[ks], dpv);
-                }
-                __builtin_amdgcn_sched_group_barrier(0x100, 2 * KS, 0);  // all operand-row reads
-                __builtin_amdgcn_sched_group_barrier(0x008, 2 * KS, 0);  // then the S / dP MFMAs
-                __builtin_amdgcn_sched_barrier(0);
-                uint4 to[2][DT32], tq[2][DT32];
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                    for (int dt = 0; dt < DT32; ++dt) {
-                        to[ks][dt] = fta_tr_frag_sw<QSEG>(ob, ks * 16, dt * 32, lane);
-                        tq[ks][dt] = fta_tr_frag_sw<QSEG>(qb, ks * 16, dt * 32, lane);
+                    for (int i = 0; i < LQ; ++i) {
+                        const int blk = i * NW + wave;
+                        const int ten = (blk * 64) / (CS * TILE);
+                        const int sl = ((blk * 64) / TILE) % CS;
+                        const int64_t t0 = 32 * cs[sl] - a.q_pad;
+                        const char* base = reinterpret_cast<const char*>(ten == 1 ? dp + t0 * a.d_sn : qp + t0 * a.q_sn);
+                        fta_dma16_at(base + roff[i], sbase + blk * 1024);
                     }
-                float lr[16], dr[16];
+                } else {  // a chunk at a sequence edge: clamp its rows (masked off) into [0, N)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int r = c_row(i, lane);
-                    lr[i] = ld[slot * 32 + r];
-                    dr[i] = ld[(CS + slot) * 32 + r];
+                    for (int i = 0; i < LQ; ++i) {
+                        const int blk = i * NW + wave;
+                        const int ten = (blk * 64) / (CS * TILE);
+                        const int sl = ((blk * 64) / TILE) % CS;
+                        const int r2 = (blk * 64 + lane) % TILE;
+                        const int row = r2 / QSEG;
+                        int j = SW::slot(row, r2 - row * QSEG);
+                        if (j * 8 >= a.Dreal) j = 0;
+                        const int t = min(max(32 * cs[sl] - a.q_pad + row, 0), a.N - 1);
+                        fta_dma16_at((ten == 1 ? dp + (int64_t)t * a.d_sn : qp + (int64_t)t * a.q_sn) + j * 8,
+                                     sbase + blk * 1024);
+                    }
                 }
-                __builtin_amdgcn_sched_barrier(0);
-                uint4 pf[2], dsf[2];
+                int c = cs[0];
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    float pv[8], dv8[8];
+                for (int sl = 1; sl < CS; ++sl) c = (l_sl == sl) ? cs[sl] : c;
+                const int t = min(max(32 * c - a.q_pad + l_row, 0), a.N - 1);
+                fta_dma4_at(l_base + t, sbase + Sh::LD_OFF + wave * 256);
+            };
+
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int i = 8 * ks + e;
+            for (int k = 0; k < NST - 1; ++k)
+                if (k < nsteps) issue(k, k);
+            int cur = 0;  // stage buffer of step k
+            for (int k = 0; k < nsteps; ++k) {
+                if (k + NST - 2 < nsteps)
+                    fta_wait_vmcnt<Sh::L * (NST - 2)>();
+                else
+                    fta_wait_vmcnt<0>();
+                __syncthreads();  // step k visible to all waves; step k - 1's buffer is free
+                if (k + NST - 1 < nsteps) issue(cur == 0 ? NST - 1 : cur - 1, k + NST - 1);
+                const int u = k * CS + slot;
+                const uint32_t mk = (u < U) ? __builtin_amdgcn_readfirstlane(sMask[tt][sList[u]]) : 0u;
+                if (mk) {
+                    const uint16_t* qb = reinterpret_cast<const uint16_t*>(&sStage[cur][0]) + slot * TILE * 8;
+                    const uint16_t* ob = qb + CS * TILE * 8;
+                    const float* ld = reinterpret_cast<const float*>(&sStage[cur][Sh::LD_OFF]);
+                    // Phased so that LDS latency overlaps MFMA work without exceeding the
+                    // 256 VGPRs: (1) operand rows, (2) S and dP MFMAs, (3) transposed
+                    // operands and lse / delta (while those MFMAs run), (4) softmax,
+                    // (5) dV and dK MFMAs.  sched_barrier keeps the phases in order.
+                    uint4 qa[KS], oa[KS];
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        const int off = SW::off(lane & 31, 2 * ks + hf);
+                        qa[ks] = *reinterpret_cast<const uint4*>(qb + off);
+                        oa[ks] = *reinterpret_cast<const uint4*>(ob + off);
+                    }
+                    f32x16 s, dpv;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        s[i] = 0.f;
+                        dpv[i] = 0.f;
+                    }
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        s = E::mma(qa[ks], kf[ks], s);
+                        dpv = E::mma(oa[ks], vf[ks], dpv);
+                    }
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2 * KS, 0);  // all operand-row reads
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2 * KS, 0);  // then the S / dP MFMAs
+                    __builtin_amdgcn_sched_barrier(0);
+                    uint4 to[2][DT32], tq[2][DT32];
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                        for (int dt = 0; dt < DT32; ++dt) {
+                            to[ks][dt] = fta_tr_frag_sw<QSEG>(ob, ks * 16, dt * 32, lane);
+                            tq[ks][dt] = fta_tr_frag_sw<QSEG>(qb, ks * 16, dt * 32, lane);
+                        }
+                    float lr[16], dr[16];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
                         const int r = c_row(i, lane);
-                        // a selected row with a valid key has a finite lse
-                        const bool ok = kok && ((mk >> r) & 1u);
-                        const float p = ok ? fta_exp2(fmaf(s[i], a.c, -lr[i] * 1.4426950408889634f)) : 0.f;
-                        pv[e] = p;
-                        dv8[e] = p * (dpv[i] - dr[i]);
+                        lr[i] = ld[slot * 32 + r];
+                        dr[i] = ld[(CS + slot) * 32 + r];
                     }
-                    pf[ks] = make_uint4(E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
-                                        E::pack2(pv[6], pv[7]));
-                    dsf[ks] = make_uint4(E::pack2(dv8[0], dv8[1]), E::pack2(dv8[2], dv8[3]),
-                                         E::pack2(dv8[4], dv8[5]), E::pack2(dv8[6], dv8[7]));
-                }
+                    __builtin_amdgcn_sched_barrier(0);
+                    uint4 pf[2], dsf[2];
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
+                    for (int ks = 0; ks < 2; ++ks) {
+                        float pv[8], dv8[8];
 #pragma unroll
-                    for (int dt = 0; dt < DT32; ++dt) {
-                        dva[dt] = E::mma(pf[ks], to[ks][dt], dva[dt]);
-                        dka[dt] = E::mma(dsf[ks], tq[ks][dt], dka[dt]);
+                        for (int e = 0; e < 8; ++e) {
+                            const int i = 8 * ks + e;
+                            const int r = c_row(i, lane);
+                            // a selected row with a valid key has a finite lse
+                            const bool ok = kok && ((mk >> r) & 1u);
+                            const float p = ok ? fta_exp2(fmaf(s[i], a.c, -lr[i] * 1.4426950408889634f)) : 0.f;
+                            pv[e] = p;
+                            dv8[e] = p * (dpv[i] - dr[i]);
+                        }
+                        pf[ks] = make_uint4(E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
+                                            E::pack2(pv[6], pv[7]));
+                        dsf[ks] = make_uint4(E::pack2(dv8[0], dv8[1]), E::pack2(dv8[2], dv8[3]),
+                                             E::pack2(dv8[4], dv8[5]), E::pack2(dv8[6], dv8[7]));
+                    }
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                        for (int dt = 0; dt < DT32; ++dt) {
+                            dva[dt] = E::mma(pf[ks], to[ks][dt], dva[dt]);
+                            dka[dt] = E::mma(dsf[ks], tq[ks][dt], dka[dt]);
+                        }
                     }
                 }
+                cur = (cur == NST - 1) ? 0 : cur + 1;
             }
-            cur = (cur == NST - 1) ? 0 : cur + 1;
+            __syncthreads();  // all waves done with the stage buffers, sMask and sList
         }
-        __syncthreads();  // all waves done with the stage buffers, sMask and sList
     }
 
     if (CS > 1) {
@@ -1358,8 +1373,8 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
 
     if (!tile_live || slot != 0) return;
     // C layout: lane column = d (dt * 32 + lane & 31), rows = keys c_row(i, lane)
-    uint16_t* kout = a.out0 + b * a.o0_sb + h * a.o0_sh;
-    uint16_t* vout = a.out1 + b * a.o1_sb + h * a.o1_sh;
+    uint16_t* kout = a.out0 + b * a.o0_sb + hk * a.o0_sh;
+    uint16_t* vout = a.out1 + b * a.o1_sb + hk * a.o1_sh;
 #pragma unroll
     for (int dt = 0; dt < DT32; ++dt) {
         const int d = dt * 32 + (lane & 31);
@@ -1407,7 +1422,7 @@ struct DkvSplitShape {
                   "two WGs per CU");
 };
 
-template <int DT, int D>
+template <int DT, int D, bool GQA = false>
 __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a) {
     using E = Elem<DT>;
     using Sh = DkvSplitShape<D>;
@@ -1424,9 +1439,9 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
     __shared__ int s_tmp[8];
 
     const int wgi = fta_xcd_remap(blockIdx.x, a.total);
-    const int bh = wgi / a.wg_per_bh;
-    const int wk = wgi - bh * a.wg_per_bh;  // KV block
-    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    const int bhk = wgi / a.wg_per_bh;  // (b, K/V head)
+    const int wk = wgi - bhk * a.wg_per_bh;  // KV block
+    const int b = bhk / a.Hk, hk = bhk - (bhk / a.Hk) * a.Hk;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hf = lane >> 5;
@@ -1437,15 +1452,16 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
     const int tk = wk * a.kvb - a.kv_pad + krel;
     const bool kok = krel < a.kvb && tk >= 0 && tk < a.N;
 
-    const uint16_t* qp = a.q + b * a.q_sb + h * a.q_sh;
-    const uint16_t* dp = a.dout + b * a.d_sb + h * a.d_sh;
-    const float* lsep = a.lse_in + (int64_t)bh * a.N;
-    const float* dlp = a.delta_in + (int64_t)bh * a.N;
+    // query-side operands of the query head being walked (set per head below)
+    const uint16_t* qp = nullptr;
+    const uint16_t* dp = nullptr;
+    const float* lsep = nullptr;
+    const float* dlp = nullptr;
 
     // K (hv = 0) or V (hv = 1) rows of this tile, full D
     uint4 kv[KS];
     {
-        const uint16_t* src = hv ? a.v + b * a.v_sb + h * a.v_sh : a.k + b * a.k_sb + h * a.k_sh;
+        const uint16_t* src = hv ? a.v + b * a.v_sb + hk * a.v_sh : a.k + b * a.k_sb + hk * a.k_sh;
         const int64_t sn = hv ? a.v_sn : a.k_sn;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -1453,7 +1469,9 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
             kv[ks] = (kok && d < a.Dreal) ? *reinterpret_cast<const uint4*>(src + (int64_t)tk * sn + d) : fta_zero4();
         }
     }
-    const bool bits_lds = fta_stage_kv_bits<TT>(a, bh, wk, Tb, sBits);  // completes the loads above too
+    // the first query head's membership rows (the staging waits for the K/V loads too)
+    bool bits_lds = fta_stage_kv_bits<TT>(a, b * a.H + hk * a.G, wk, Tb, sBits);
+    // complete the register loads: the DMAs below are invisible to the compiler
     fta_wait_vmcnt<0>();
 
     // Per-lane DMA sources (as in fta_sparse_dkv_kernel with one chunk slot):
@@ -1473,7 +1491,7 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
     // lse / delta: wave 0's 256 bytes hold [lse 32][delta 32] (other waves load a duplicate)
     const int lv = wave * 64 + lane;
     const bool l_isd = lv >= 32 && lv < 64;
-    const float* l_base = l_isd ? dlp : lsep;
+    const float* l_base = nullptr;
     const int l_row = lv & 31;
     const uint32_t lds0 = fta_lds_addr(&sStage[0][0]);
 
@@ -1486,117 +1504,133 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
             dva[dt][i] = 0.f;
         }
 
-    for (int seg0 = 0; seg0 < a.NC; seg0 += kSegC) {
-        const int segn = min(kSegC, a.NC - seg0);
-        const int U = fta_build_kv_masks<TT>(a, bh, wk, Tb, seg0, segn, bits_lds, sBits, sMask, sList, s_tmp);
-        if (U == 0) continue;
-
-        // gather chunk list entry k into stage buffer st
-        auto issue = [&](int st, int k) {
-            const uint32_t sbase = lds0 + st * Sh::STAGE_B;
-            const int c = __builtin_amdgcn_readfirstlane(seg0 + sList[k]);
-            const int t0 = 32 * c - a.q_pad;
-            if (t0 >= 0 && t0 + 31 < a.N) {
-#pragma unroll
-                for (int i = 0; i < LQ; ++i) {
-                    const int blk = i * NW + wave;
-                    const int ten = (blk * 64) / TILE;
-                    const char* base =
-                        reinterpret_cast<const char*>(ten == 1 ? dp + (int64_t)t0 * a.d_sn : qp + (int64_t)t0 * a.q_sn);
-                    fta_dma16_at(base + roff[i], sbase + blk * 1024);
-                }
-            } else {  // a chunk at a sequence edge: clamp its rows (masked off) into [0, N)
-#pragma unroll
-                for (int i = 0; i < LQ; ++i) {
-                    const int blk = i * NW + wave;
-                    const int ten = (blk * 64) / TILE;
-                    const int r2 = (blk * 64 + lane) % TILE;
-                    const int row = r2 / QSEG;
-                    int j = SW::slot(row, r2 - row * QSEG);
-                    if (j * 8 >= a.Dreal) j = 0;
-                    const int t = min(max(t0 + row, 0), a.N - 1);
-                    fta_dma16_at((ten == 1 ? dp + (int64_t)t * a.d_sn : qp + (int64_t)t * a.q_sn) + j * 8,
-                                 sbase + blk * 1024);
-                }
-            }
-            const int t = min(max(t0 + l_row, 0), a.N - 1);
-            fta_dma4_at(l_base + t, sbase + Sh::LD_OFF + wave * 256);
-        };
-
-#pragma unroll
-        for (int k = 0; k < NST - 1; ++k)
-            if (k < U) issue(k, k);
-        int cur = 0;
-        for (int k = 0; k < U; ++k) {
-            if (k + NST - 2 < U)
-                fta_wait_vmcnt<Sh::L * (NST - 2)>();
-            else
-                fta_wait_vmcnt<0>();
-            __syncthreads();  // step k visible; step k - 1's buffer and the exchange area are free
-            if (k + NST - 1 < U) issue(cur == 0 ? NST - 1 : cur - 1, k + NST - 1);
-            const uint32_t mk = __builtin_amdgcn_readfirstlane(sMask[tt][sList[k]]);
-            const uint16_t* qb = reinterpret_cast<const uint16_t*>(&sStage[cur][0]);
-            const uint16_t* ob = qb + TILE * 8;
-            const float* ld = reinterpret_cast<const float*>(&sStage[cur][Sh::LD_OFF]);
-            f32x16 own;  // P (hv = 0) or dP (hv = 1)
-            if (mk) {
-                const uint16_t* ab = hv ? ob : qb;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) own[i] = 0.f;
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks)
-                    own = E::mma(*reinterpret_cast<const uint4*>(ab + SW::off(lane & 31, 2 * ks + hf)), kv[ks], own);
-                if (hv == 0) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int r = c_row(i, lane);
-                        // a selected row with a valid key has a finite lse
-                        const bool ok = kok && ((mk >> r) & 1u);
-                        const float ex = fta_exp2(fmaf(own[i], a.c, -ld[r] * 1.4426950408889634f));
-                        own[i] = ok ? ex : 0.f;
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < 16; ++i) sX[tt][hv][i][lane] = own[i];
-            }
-            __syncthreads();  // both halves of every tile exchanged
-            if (mk) {
-                uint4 pf[2], dsf[2];
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    float pv[8], dv8[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int i = 8 * ks + e;
-                        const float other = sX[tt][hv ^ 1][i][lane];
-                        const float p = hv ? other : own[i];
-                        const float dpv = hv ? own[i] : other;
-                        pv[e] = p;
-                        dv8[e] = p * (dpv - ld[32 + c_row(i, lane)]);
-                    }
-                    pf[ks] = make_uint4(E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
-                                        E::pack2(pv[6], pv[7]));
-                    dsf[ks] = make_uint4(E::pack2(dv8[0], dv8[1]), E::pack2(dv8[2], dv8[3]),
-                                         E::pack2(dv8[4], dv8[5]), E::pack2(dv8[6], dv8[7]));
-                }
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-                    for (int dt = 0; dt < DH; ++dt) {
-                        const int d0 = (hv * DH + dt) * 32;
-                        dva[dt] = E::mma(pf[ks], fta_tr_frag_sw<QSEG>(ob, ks * 16, d0, lane), dva[dt]);
-                        dka[dt] = E::mma(dsf[ks], fta_tr_frag_sw<QSEG>(qb, ks * 16, d0, lane), dka[dt]);
-                    }
-                }
-            }
-            cur = (cur == NST - 1) ? 0 : cur + 1;
+    // the query heads that share this K/V head (one without GQA): their
+    // membership, Q, dO, lse and delta; dK / dV accumulate over all of them
+    const int ngq = GQA ? a.G : 1;  // a constant 1 without GQA: no head loop in that code
+    for (int gq = 0; gq < ngq; ++gq) {
+        const int h = hk * a.G + gq;
+        const int bh = b * a.H + h;
+        qp = a.q + b * a.q_sb + h * a.q_sh;
+        dp = a.dout + b * a.d_sb + h * a.d_sh;
+        lsep = a.lse_in + (int64_t)bh * a.N;
+        dlp = a.delta_in + (int64_t)bh * a.N;
+        l_base = l_isd ? dlp : lsep;
+        if (gq > 0) {
+            __syncthreads();  // the previous head's membership rows are no longer read
+            bits_lds = fta_stage_kv_bits<TT>(a, bh, wk, Tb, sBits);
         }
-        __syncthreads();  // all waves done with the stage buffers, sMask and sList
+        for (int seg0 = 0; seg0 < a.NC; seg0 += kSegC) {
+            const int segn = min(kSegC, a.NC - seg0);
+            const int U = fta_build_kv_masks<TT>(a, bh, wk, Tb, seg0, segn, bits_lds, sBits, sMask, sList, s_tmp);
+            if (U == 0) continue;
+
+            // gather chunk list entry k into stage buffer st
+            auto issue = [&](int st, int k) {
+                const uint32_t sbase = lds0 + st * Sh::STAGE_B;
+                const int c = __builtin_amdgcn_readfirstlane(seg0 + sList[k]);
+                const int t0 = 32 * c - a.q_pad;
+                if (t0 >= 0 && t0 + 31 < a.N) {
+#pragma unroll
+                    for (int i = 0; i < LQ; ++i) {
+                        const int blk = i * NW + wave;
+                        const int ten = (blk * 64) / TILE;
+                        const char* base =
+                            reinterpret_cast<const char*>(ten == 1 ? dp + (int64_t)t0 * a.d_sn : qp + (int64_t)t0 * a.q_sn);
+                        fta_dma16_at(base + roff[i], sbase + blk * 1024);
+                    }
+                } else {  // a chunk at a sequence edge: clamp its rows (masked off) into [0, N)
+#pragma unroll
+                    for (int i = 0; i < LQ; ++i) {
+                        const int blk = i * NW + wave;
+                        const int ten = (blk * 64) / TILE;
+                        const int r2 = (blk * 64 + lane) % TILE;
+                        const int row = r2 / QSEG;
+                        int j = SW::slot(row, r2 - row * QSEG);
+                        if (j * 8 >= a.Dreal) j = 0;
+                        const int t = min(max(t0 + row, 0), a.N - 1);
+                        fta_dma16_at((ten == 1 ? dp + (int64_t)t * a.d_sn : qp + (int64_t)t * a.q_sn) + j * 8,
+                                     sbase + blk * 1024);
+                    }
+                }
+                const int t = min(max(t0 + l_row, 0), a.N - 1);
+                fta_dma4_at(l_base + t, sbase + Sh::LD_OFF + wave * 256);
+            };
+
+#pragma unroll
+            for (int k = 0; k < NST - 1; ++k)
+                if (k < U) issue(k, k);
+            int cur = 0;
+            for (int k = 0; k < U; ++k) {
+                if (k + NST - 2 < U)
+                    fta_wait_vmcnt<Sh::L * (NST - 2)>();
+                else
+                    fta_wait_vmcnt<0>();
+                __syncthreads();  // step k visible; step k - 1's buffer and the exchange area are free
+                if (k + NST - 1 < U) issue(cur == 0 ? NST - 1 : cur - 1, k + NST - 1);
+                const uint32_t mk = __builtin_amdgcn_readfirstlane(sMask[tt][sList[k]]);
+                const uint16_t* qb = reinterpret_cast<const uint16_t*>(&sStage[cur][0]);
+                const uint16_t* ob = qb + TILE * 8;
+                const float* ld = reinterpret_cast<const float*>(&sStage[cur][Sh::LD_OFF]);
+                f32x16 own;  // P (hv = 0) or dP (hv = 1)
+                if (mk) {
+                    const uint16_t* ab = hv ? ob : qb;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) own[i] = 0.f;
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks)
+                        own = E::mma(*reinterpret_cast<const uint4*>(ab + SW::off(lane & 31, 2 * ks + hf)), kv[ks], own);
+                    if (hv == 0) {
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            const int r = c_row(i, lane);
+                            // a selected row with a valid key has a finite lse
+                            const bool ok = kok && ((mk >> r) & 1u);
+                            const float ex = fta_exp2(fmaf(own[i], a.c, -ld[r] * 1.4426950408889634f));
+                            own[i] = ok ? ex : 0.f;
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) sX[tt][hv][i][lane] = own[i];
+                }
+                __syncthreads();  // both halves of every tile exchanged
+                if (mk) {
+                    uint4 pf[2], dsf[2];
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        float pv[8], dv8[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const int i = 8 * ks + e;
+                            const float other = sX[tt][hv ^ 1][i][lane];
+                            const float p = hv ? other : own[i];
+                            const float dpv = hv ? own[i] : other;
+                            pv[e] = p;
+                            dv8[e] = p * (dpv - ld[32 + c_row(i, lane)]);
+                        }
+                        pf[ks] = make_uint4(E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
+                                            E::pack2(pv[6], pv[7]));
+                        dsf[ks] = make_uint4(E::pack2(dv8[0], dv8[1]), E::pack2(dv8[2], dv8[3]),
+                                             E::pack2(dv8[4], dv8[5]), E::pack2(dv8[6], dv8[7]));
+                    }
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                        for (int dt = 0; dt < DH; ++dt) {
+                            const int d0 = (hv * DH + dt) * 32;
+                            dva[dt] = E::mma(pf[ks], fta_tr_frag_sw<QSEG>(ob, ks * 16, d0, lane), dva[dt]);
+                            dka[dt] = E::mma(dsf[ks], fta_tr_frag_sw<QSEG>(qb, ks * 16, d0, lane), dka[dt]);
+                        }
+                    }
+                }
+                cur = (cur == NST - 1) ? 0 : cur + 1;
+            }
+            __syncthreads();  // all waves done with the stage buffers, sMask and sList
+        }
     }
 
     // C layout: lane column = d, rows = keys c_row(i, lane)
-    uint16_t* kout = a.out0 + b * a.o0_sb + h * a.o0_sh;
-    uint16_t* vout = a.out1 + b * a.o1_sb + h * a.o1_sh;
+    uint16_t* kout = a.out0 + b * a.o0_sb + hk * a.o0_sh;
+    uint16_t* vout = a.out1 + b * a.o1_sb + hk * a.o1_sh;
 #pragma unroll
     for (int dt = 0; dt < DH; ++dt) {
         const int d = (hv * DH + dt) * 32 + (lane & 31);
@@ -1648,6 +1682,8 @@ int geometry(int B, int H, int N, int D, int g, int kvb, int qph, int qpt, int k
 
 void fill_common(AttnArgs& a, int H, int N, int D, int g, int kvb, int qph, int kvph, float scale, const Geo& G) {
     a.H = H;
+    a.Hk = H;  // no GQA unless the caller sets Hk / G
+    a.G = 1;
     a.N = N;
     a.Dreal = D;
     a.g = g;
@@ -1733,6 +1769,7 @@ int launch_dq_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
 template <int DT>
 int launch_dkv_dt(AttnArgs& a, int Dk, int Tb, int B, int H, int ntiles, hipStream_t st) {
     int TT = 0;
+    const bool gqa = a.G > 1;
     auto go = [&](auto kern, int tt, int nw) {
         TT = tt;
         a.wg_per_bh = (ntiles + tt - 1) / tt;
@@ -1740,36 +1777,42 @@ int launch_dkv_dt(AttnArgs& a, int Dk, int Tb, int B, int H, int ntiles, hipStre
         hipLaunchKernelGGL(kern, dim3(a.total), dim3(nw * 64), 0, st, a);
     };
     switch (Dk) {
+#define FTA_DKV_GO(DK, TTX, CSX)                                                             \
+    (gqa ? go(fta_sparse_dkv_kernel<DT, DK, TTX, CSX, true>, TTX, TTX * CSX)                 \
+         : go(fta_sparse_dkv_kernel<DT, DK, TTX, CSX, false>, TTX, TTX * CSX))
 #define FTA_DKV(DK, NW, TT1, CS1, TT2, CS2)                                                  \
     case DK:                                                                                 \
         if (Tb == 1)                                                                         \
-            go(fta_sparse_dkv_kernel<DT, DK, TT1, CS1>, TT1, TT1 * CS1);                     \
+            FTA_DKV_GO(DK, TT1, CS1);                                                        \
         else if (Tb == 2)                                                                    \
-            go(fta_sparse_dkv_kernel<DT, DK, TT2, CS2>, TT2, TT2 * CS2);                     \
+            FTA_DKV_GO(DK, TT2, CS2);                                                        \
         else                                                                                 \
-            go(fta_sparse_dkv_kernel<DT, DK, NW, 1>, NW, NW);                                \
+            FTA_DKV_GO(DK, NW, 1);                                                           \
         break;
         FTA_DKV(32, 8, 1, 4, 2, 4)
         case 64:
             if (Tb == 2)
-                go(fta_sparse_dkv_split_kernel<DT, 64>, 2, 4);
+                gqa ? go(fta_sparse_dkv_split_kernel<DT, 64, true>, 2, 4)
+                    : go(fta_sparse_dkv_split_kernel<DT, 64, false>, 2, 4);
             else if (Tb == 1)
-                go(fta_sparse_dkv_kernel<DT, 64, 1, 4>, 1, 4);
+                FTA_DKV_GO(64, 1, 4);
             else
-                go(fta_sparse_dkv_kernel<DT, 64, 8, 1>, 8, 8);
+                FTA_DKV_GO(64, 8, 1);
             break;
         FTA_DKV(96, 4, 1, 4, 2, 2)
         case 128:
             if (Tb == 2)
-                go(fta_sparse_dkv_split_kernel<DT, 128>, 2, 4);
+                gqa ? go(fta_sparse_dkv_split_kernel<DT, 128, true>, 2, 4)
+                    : go(fta_sparse_dkv_split_kernel<DT, 128, false>, 2, 4);
             else if (Tb == 1)
-                go(fta_sparse_dkv_kernel<DT, 128, 1, 4>, 1, 4);
+                FTA_DKV_GO(128, 1, 4);
             else
-                go(fta_sparse_dkv_kernel<DT, 128, 4, 1>, 4, 4);
+                FTA_DKV_GO(128, 4, 1);
             break;
         FTA_DKV(160, 4, 2, 2, 2, 2)
         FTA_DKV(256, 4, 4, 1, 4, 1)
 #undef FTA_DKV
+#undef FTA_DKV_GO
         default:
             return fta::arg_error("sparse_attn_bwd: unsupported head dim");
     }
@@ -1796,13 +1839,14 @@ size_t fta_sparse_attn_fwd_workspace_size(int B, int H, int N, int D, int q_bloc
     return 0;  // the forward needs no scratch
 }
 
-int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
-                        const void* v, const int64_t* v_strides, int dtype, int B, int H, int N, int D,
-                        const int32_t* merged_indices, int QM, int W, int q_block_size, int kv_block_size,
-                        int q_pad_head, int q_pad_tail, int kv_pad_head, int kv_pad_tail, float scale, void* o,
-                        const int64_t* o_strides, float* lse, void* workspace, size_t workspace_bytes,
-                        void* stream) {
+int fta_sparse_attn_fwd_gqa(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                            const void* v, const int64_t* v_strides, int dtype, int B, int H, int Hk, int N, int D,
+                            const int32_t* merged_indices, int QM, int W, int q_block_size, int kv_block_size,
+                            int q_pad_head, int q_pad_tail, int kv_pad_head, int kv_pad_tail, float scale,
+                            void* o, const int64_t* o_strides, float* lse, void* workspace, size_t workspace_bytes,
+                            void* stream) {
     FTA_TRY_BEGIN
+    if (Hk <= 0 || H % Hk != 0) return fta::arg_error("sparse_attn: num_heads must be a multiple of num_kv_heads");
     Geo G;
     int rc = geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
                       &G);
@@ -1832,6 +1876,8 @@ int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k, 
     a.o0_sn = o_strides[2];
     a.lse = lse;
     fill_common(a, H, N, D, q_block_size, kv_block_size, q_pad_head, kv_pad_head, scale, G);
+    a.Hk = Hk;
+    a.G = H / Hk;
     const int T = (G.Dk <= 160) ? 8 : 4;  // query tiles per workgroup
     a.wg_per_bh = (G.Npq + 32 * T - 1) / (32 * T);
     a.total = a.wg_per_bh * B * H;
@@ -1852,14 +1898,16 @@ size_t fta_sparse_attn_bwd_workspace_size(int B, int H, int N, int D, int q_bloc
     return sel_bytes(B, H, G);  // membership bitmap KV block -> q-blocks
 }
 
-int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
-                        const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
-                        int dtype, int B, int H, int N, int D, const int32_t* merged_indices, int QM, int W,
-                        int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head,
-                        int kv_pad_tail, float scale, const float* lse, const float* delta, void* dq,
-                        const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
-                        const int64_t* dv_strides, void* workspace, size_t workspace_bytes, void* stream) {
+int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                            const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
+                            int dtype, int B, int H, int Hk, int N, int D, const int32_t* merged_indices, int QM,
+                            int W, int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail,
+                            int kv_pad_head, int kv_pad_tail, float scale, const float* lse, const float* delta,
+                            void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                            const int64_t* dv_strides, void* workspace, size_t workspace_bytes, void* stream) {
     FTA_TRY_BEGIN
+    if (Hk <= 0 || H % Hk != 0)
+        return fta::arg_error("sparse_attn_bwd: num_heads must be a multiple of num_kv_heads");
     Geo G;
     int rc = geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
                       &G);
@@ -1894,6 +1942,8 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, 
     a.lse_in = lse;
     a.delta_in = delta;
     fill_common(a, H, N, D, q_block_size, kv_block_size, q_pad_head, kv_pad_head, scale, G);
+    a.Hk = Hk;
+    a.G = H / Hk;
 
     // dQ
     a.out0 = (uint16_t*)dq;
@@ -1922,9 +1972,34 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, 
     a.o1_sn = dv_strides[2];
     const int Tb = (kv_block_size + 31) / 32;
     const int ntiles = G.Mkv * Tb;
-    if (dtype == FTA_DTYPE_BF16) return launch_dkv_dt<FTA_DTYPE_BF16>(a, G.Dk, Tb, B, H, ntiles, st);
-    return launch_dkv_dt<FTA_DTYPE_F16>(a, G.Dk, Tb, B, H, ntiles, st);
+    // one dK/dV WG set per K/V head; each walks the G query heads that share it
+    if (dtype == FTA_DTYPE_BF16) return launch_dkv_dt<FTA_DTYPE_BF16>(a, G.Dk, Tb, B, Hk, ntiles, st);
+    return launch_dkv_dt<FTA_DTYPE_F16>(a, G.Dk, Tb, B, Hk, ntiles, st);
     FTA_TRY_END
+}
+
+int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                        const void* v, const int64_t* v_strides, int dtype, int B, int H, int N, int D,
+                        const int32_t* merged_indices, int QM, int W, int q_block_size, int kv_block_size,
+                        int q_pad_head, int q_pad_tail, int kv_pad_head, int kv_pad_tail, float scale, void* o,
+                        const int64_t* o_strides, float* lse, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+    return fta_sparse_attn_fwd_gqa(q, q_strides, k, k_strides, v, v_strides, dtype, B, H, H, N, D, merged_indices,
+                                   QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head,
+                                   kv_pad_tail, scale, o, o_strides, lse, workspace, workspace_bytes, stream);
+}
+
+int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                        const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
+                        int dtype, int B, int H, int N, int D, const int32_t* merged_indices, int QM, int W,
+                        int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head,
+                        int kv_pad_tail, float scale, const float* lse, const float* delta, void* dq,
+                        const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                        const int64_t* dv_strides, void* workspace, size_t workspace_bytes, void* stream) {
+    return fta_sparse_attn_bwd_gqa(q, q_strides, k, k_strides, v, v_strides, dout, do_strides, dtype, B, H, H, N, D,
+                                   merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail,
+                                   kv_pad_head, kv_pad_tail, scale, lse, delta, dq, dq_strides, dk, dk_strides, dv,
+                                   dv_strides, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -171,10 +171,13 @@ def flash_topk_attn(
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Sparse attention over merged KV block indices
     (reference: flash_topk_attn_v2/__init__.py:136-169).  ``counts`` and
-    ``S_MAX`` are accepted and ignored, as in the reference."""
+    ``S_MAX`` are accepted and ignored, as in the reference.
+
+    ``num_kv_heads`` < ``num_heads`` runs grouped-query attention (k, v with
+    ``num_kv_heads`` heads, ``num_heads`` a multiple of it).  This extends the
+    reference, which raises NotImplementedError for it (:153-156).
+    """
     del counts, S_MAX
-    if num_kv_heads is not None and num_kv_heads != num_heads:
-        raise NotImplementedError("GQA (num_kv_heads != num_heads) is not supported")
 
     return flash_sparse_attn(
         q,
@@ -187,6 +190,7 @@ def flash_topk_attn(
         scale=scale,
         q_padding=q_padding,
         kv_padding=kv_padding,
+        num_kv_heads=num_kv_heads,
     )
 
 

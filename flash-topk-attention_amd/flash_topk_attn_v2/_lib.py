@@ -48,10 +48,15 @@ _SIGNATURES = {
     "fta_sparse_attn_fwd_workspace_size": (_sz, [_i] * 10),
     "fta_sparse_attn_fwd": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _p, _i, _i, _i, _i, _i, _i,
                                  _i, _i, _f, _p, _i64p, _p, _p, _sz, _p]),
+    "fta_sparse_attn_fwd_gqa": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _i, _p, _i, _i, _i, _i,
+                                     _i, _i, _i, _i, _f, _p, _i64p, _p, _p, _sz, _p]),
     "fta_preprocess_delta": (_i, [_p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _p, _p]),
     "fta_sparse_attn_bwd_workspace_size": (_sz, [_i] * 10),
     "fta_sparse_attn_bwd": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _p, _i, _i, _i,
                                  _i, _i, _i, _i, _i, _f, _p, _p, _p, _i64p, _p, _i64p, _p, _i64p, _p, _sz, _p]),
+    "fta_sparse_attn_bwd_gqa": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _i, _p, _i,
+                                     _i, _i, _i, _i, _i, _i, _i, _f, _p, _p, _p, _i64p, _p, _i64p, _p, _i64p, _p,
+                                     _sz, _p]),
 }
 
 

@@ -18,22 +18,22 @@ from . import _lib
 from .sparse_attn_bwd import preprocess_delta, sparse_attn_bwd
 
 
-def _sparse_attn_fwd(q, k, v, merged, H, g, kvb, scale, q_padding, kv_padding):
+def _sparse_attn_fwd(q, k, v, merged, H, g, kvb, scale, q_padding, kv_padding, Hk):
     B, N, C = q.shape
     D = C // H
     dev = q.device
     qq, qs = _lib.token_view(q, "bnc", H)
-    kk, ks = _lib.token_view(k, "bnc", H)
-    vv, vs = _lib.token_view(v, "bnc", H)
+    kk, ks = _lib.token_view(k, "bnc", Hk)
+    vv, vs = _lib.token_view(v, "bnc", Hk)
     o = torch.empty(B, N, C, device=dev, dtype=q.dtype)
     lse = torch.empty(B, H, N, device=dev, dtype=torch.float32)
     QM, W = merged.shape[2], merged.shape[3]
     L = _lib.lib()
     geo = (B, H, N, D, g, kvb, q_padding[0], q_padding[1], kv_padding[0], kv_padding[1])
     ws = _lib.workspace(L.fta_sparse_attn_fwd_workspace_size(*geo), dev)
-    rc = L.fta_sparse_attn_fwd(
+    rc = L.fta_sparse_attn_fwd_gqa(
         _lib.ptr(qq), _lib.i64arr(qs), _lib.ptr(kk), _lib.i64arr(ks), _lib.ptr(vv), _lib.i64arr(vs),
-        _lib.dtype_code(q.dtype), B, H, N, D, _lib.ptr(merged), QM, W, g, kvb,
+        _lib.dtype_code(q.dtype), B, H, Hk, N, D, _lib.ptr(merged), QM, W, g, kvb,
         q_padding[0], q_padding[1], kv_padding[0], kv_padding[1], float(scale),
         _lib.ptr(o), _lib.i64arr([N * C, D, C]), _lib.ptr(lse), _lib.ptr(ws), ws.numel(),
         _lib.stream_ptr(dev),
@@ -47,9 +47,11 @@ class FlashSparseAttnFunc(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, merged_indices, num_heads, q_block_size, kv_block_size,
-                softmax_scale, q_padding, kv_padding):
+                softmax_scale, q_padding, kv_padding, num_kv_heads=None):
+        Hk = num_heads if num_kv_heads is None else num_kv_heads
         o, lse = _sparse_attn_fwd(q, k, v, merged_indices, num_heads, q_block_size, kv_block_size,
-                                  softmax_scale, q_padding, kv_padding)
+                                  softmax_scale, q_padding, kv_padding, Hk)
+        ctx.num_kv_heads = Hk
         ctx.save_for_backward(q, k, v, o, merged_indices, lse)
         ctx.num_heads = num_heads
         ctx.q_block_size = q_block_size
@@ -66,9 +68,9 @@ class FlashSparseAttnFunc(torch.autograd.Function):
         delta = preprocess_delta(o, grad_output, ctx.num_heads)
         dq, dk, dv = sparse_attn_bwd(
             q, k, v, o, grad_output, lse, merged, ctx.num_heads, ctx.q_block_size, ctx.kv_block_size,
-            ctx.softmax_scale, ctx.q_padding, ctx.kv_padding, delta=delta,
+            ctx.softmax_scale, ctx.q_padding, ctx.kv_padding, delta=delta, num_kv_heads=ctx.num_kv_heads,
         )
-        return dq, dk, dv, None, None, None, None, None, None, None
+        return dq, dk, dv, None, None, None, None, None, None, None, None
 
 
 def flash_sparse_attn(
@@ -82,6 +84,7 @@ def flash_sparse_attn(
     scale: Optional[float] = None,
     q_padding: Tuple[int, int] = (0, 0),
     kv_padding: Tuple[int, int] = (0, 0),
+    num_kv_heads: Optional[int] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Block-sparse attention forward (differentiable in q, k, v).
 
@@ -94,6 +97,10 @@ def flash_sparse_attn(
         kv_block_size: KV block size (any positive integer).
         scale: Softmax scale, default ``1 / sqrt(D)``.
         q_padding, kv_padding: virtual ``(pad_head, pad_tail)``.
+        num_kv_heads: K/V heads for grouped-query attention (``k``, ``v`` are
+            ``[B, N, num_kv_heads * D]``; query head ``h`` uses K/V head
+            ``h // (num_heads // num_kv_heads)``).  Default: ``num_heads``.
+            An extension: the reference has no GQA.
 
     Returns:
         ``(output [B, N, C] same dtype as q, lse [B, H, N] float32 natural log)``.
@@ -117,6 +124,11 @@ def flash_sparse_attn(
 
     if C != H * D:
         raise ValueError(f"C ({C}) must be divisible by num_heads ({H})")
+    Hk = H if num_kv_heads is None else int(num_kv_heads)
+    if Hk <= 0 or H % Hk != 0:
+        raise ValueError(f"num_heads ({H}) must be a positive multiple of num_kv_heads ({Hk})")
+    if tuple(k.shape) != (B, N, Hk * D) or tuple(v.shape) != (B, N, Hk * D):
+        raise ValueError(f"k and v must be [B, N, num_kv_heads * D] = {[B, N, Hk * D]}")
     if q_block_size <= 0 or q_block_size > 64:
         raise ValueError(f"q_block_size must be in (0, 64], got {q_block_size}")
     if kv_block_size <= 0:
@@ -169,7 +181,7 @@ def flash_sparse_attn(
     merged = merged_indices.contiguous()
     output, lse = FlashSparseAttnFunc.apply(
         q, k, v, merged, H, q_block_size, kv_block_size, float(scale),
-        (q_pad_head, q_pad_tail), (kv_pad_head, kv_pad_tail),
+        (q_pad_head, q_pad_tail), (kv_pad_head, kv_pad_tail), Hk,
     )
     if orig_dtype == torch.float32:
         output = output.float()

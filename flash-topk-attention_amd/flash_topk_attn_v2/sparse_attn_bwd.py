@@ -79,40 +79,44 @@ def flash_sort_by_count(
 
 def sparse_attn_bwd(
     q, k, v, o, do, lse, merged_indices, num_heads, q_block_size, kv_block_size, scale,
-    q_padding=(0, 0), kv_padding=(0, 0), delta=None,
+    q_padding=(0, 0), kv_padding=(0, 0), delta=None, num_kv_heads=None,
 ):
-    """dQ, dK, dV ``[B, N, C]`` (dtype of q) for block-sparse attention.
+    """dQ ``[B, N, C]``, dK, dV ``[B, N, Hk * D]`` (dtype of q) for block-sparse
+    attention; ``Hk = num_kv_heads`` (default ``num_heads``), and each K/V head's
+    gradient sums over the query heads that share it.
 
-    ``q, k, v, o, do`` are ``[B, N, C]`` bf16/fp16; ``lse`` is the forward's
-    natural-log ``[B, H, N]``.
+    ``q, o, do`` are ``[B, N, C]``, ``k, v`` ``[B, N, Hk * D]`` bf16/fp16; ``lse``
+    is the forward's natural-log ``[B, H, N]``.
     """
     B, N, C = q.shape
     H = num_heads
     D = C // H
+    Hk = H if num_kv_heads is None else num_kv_heads
     dev = q.device
     if delta is None:
         delta = preprocess_delta(o, do, H)
     if do.dtype != q.dtype:
         do = do.to(q.dtype)
     qq, qs = _lib.token_view(q, "bnc", H)
-    kk, ks = _lib.token_view(k, "bnc", H)
-    vv, vs = _lib.token_view(v, "bnc", H)
+    kk, ks = _lib.token_view(k, "bnc", Hk)
+    vv, vs = _lib.token_view(v, "bnc", Hk)
     dd, dos = _lib.token_view(do, "bnc", H)
     merged = merged_indices.to(torch.int32).contiguous()
     QM, W = merged.shape[2], merged.shape[3]
     dq = torch.empty(B, N, C, device=dev, dtype=q.dtype)
-    dk = torch.empty(B, N, C, device=dev, dtype=q.dtype)
-    dv = torch.empty(B, N, C, device=dev, dtype=q.dtype)
+    dk = torch.empty(B, N, Hk * D, device=dev, dtype=q.dtype)
+    dv = torch.empty(B, N, Hk * D, device=dev, dtype=q.dtype)
     gs = [N * C, D, C]
+    gk = [N * Hk * D, D, Hk * D]
     L = _lib.lib()
     geo = (B, H, N, D, q_block_size, kv_block_size, q_padding[0], q_padding[1], kv_padding[0], kv_padding[1])
     ws = _lib.workspace(L.fta_sparse_attn_bwd_workspace_size(*geo), dev)
-    rc = L.fta_sparse_attn_bwd(
+    rc = L.fta_sparse_attn_bwd_gqa(
         _lib.ptr(qq), _lib.i64arr(qs), _lib.ptr(kk), _lib.i64arr(ks), _lib.ptr(vv), _lib.i64arr(vs),
-        _lib.ptr(dd), _lib.i64arr(dos), _lib.dtype_code(q.dtype), B, H, N, D, _lib.ptr(merged), QM, W,
+        _lib.ptr(dd), _lib.i64arr(dos), _lib.dtype_code(q.dtype), B, H, Hk, N, D, _lib.ptr(merged), QM, W,
         q_block_size, kv_block_size, q_padding[0], q_padding[1], kv_padding[0], kv_padding[1], float(scale),
         _lib.ptr(lse.contiguous()), _lib.ptr(delta.contiguous()), _lib.ptr(dq), _lib.i64arr(gs), _lib.ptr(dk),
-        _lib.i64arr(gs), _lib.ptr(dv), _lib.i64arr(gs), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev),
+        _lib.i64arr(gk), _lib.ptr(dv), _lib.i64arr(gk), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev),
     )
     _lib.check(rc, "sparse_attn_bwd")
     return dq, dk, dv

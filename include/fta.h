@@ -193,6 +193,21 @@ int fta_preprocess_delta(const void* o, const int64_t* o_strides, const void* do
                          const int64_t* do_strides, int dtype, int B, int H, int N, int D,
                          float* delta, void* stream);
 
+/*
+ * Grouped-query forward: k and v hold Hk heads ([B][N][Hk][D] strided), query
+ * head h reads K/V head h / (H / Hk); H must be a multiple of Hk.  The other
+ * arguments and outputs are those of fta_sparse_attn_fwd (which equals this
+ * call with Hk = H).  The reference rejects num_kv_heads != num_heads
+ * (flash_topk_attn_v2/__init__.py:153-156); this extends flash_topk_attn there.
+ */
+int fta_sparse_attn_fwd_gqa(const void* q, const int64_t* q_strides, const void* k,
+                            const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                            int dtype, int B, int H, int Hk, int N, int D,
+                            const int32_t* merged_indices, int QM, int W, int q_block_size,
+                            int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head,
+                            int kv_pad_tail, float scale, void* o, const int64_t* o_strides,
+                            float* lse, void* workspace, size_t workspace_bytes, void* stream);
+
 size_t fta_sparse_attn_bwd_workspace_size(int B, int H, int N, int D, int q_block_size,
                                           int kv_block_size, int q_pad_head, int q_pad_tail,
                                           int kv_pad_head, int kv_pad_tail);
@@ -217,6 +232,22 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k,
                         const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
                         const int64_t* dv_strides, void* workspace, size_t workspace_bytes,
                         void* stream);
+
+/*
+ * Grouped-query backward: dk and dv have Hk heads; each is the sum over the
+ * H / Hk query heads that share the K/V head (accumulated in fp32 inside one
+ * workgroup, no atomics).  Otherwise as fta_sparse_attn_bwd (= Hk = H).
+ * Extends the reference the same way as fta_sparse_attn_fwd_gqa.
+ */
+int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void* k,
+                            const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                            const void* dout, const int64_t* do_strides, int dtype, int B, int H,
+                            int Hk, int N, int D, const int32_t* merged_indices, int QM, int W,
+                            int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail,
+                            int kv_pad_head, int kv_pad_tail, float scale, const float* lse,
+                            const float* delta, void* dq, const int64_t* dq_strides, void* dk,
+                            const int64_t* dk_strides, void* dv, const int64_t* dv_strides,
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -56,9 +56,25 @@ def test_api_validation_matches_reference_errors():
         fta.build_qblock_topk_indices(torch.zeros(2, 2, dtype=torch.int32), 4)
     with pytest.raises(ValueError, match="q_pad_head=4 must be < q_block_size=4"):
         fta.build_qblock_topk_indices(torch.zeros(1, 1, 8, 2, dtype=torch.int32), 4, (4, 0))
-    with pytest.raises(NotImplementedError, match="GQA"):
-        fta.flash_topk_attn(q, q, q, None, None, 2, 4, 4, num_kv_heads=1)
+    # GQA is supported (an extension of the reference), so no NotImplementedError;
+    # CPU tensors are rejected as for any other call
+    with pytest.raises(ValueError, match="requires CUDA"):
+        fta.flash_topk_attn(q, q, q, torch.zeros(1, 2, 3, 1, dtype=torch.int32), None, 2, 4, 4, num_kv_heads=1)
     with pytest.raises(ValueError, match="requires CUDA"):
         fta.flash_sparse_attn(q, q, q, torch.zeros(1, 1, 1, 1, dtype=torch.int32), 1, 4, 4)
     with pytest.raises(ValueError, match="requires CUDA"):
         fta.flash_block_score(q, q, 1, 5)
+
+
+def test_gqa_head_count_checked_before_any_gpu_work():
+    """fta_sparse_attn_{fwd,bwd}_gqa reject H not a multiple of Hk up front."""
+    from flash_topk_attn_v2 import _lib
+
+    L = _lib.lib()
+    st = _lib.i64arr([0, 0, 0])
+    rc = L.fta_sparse_attn_fwd_gqa(None, st, None, st, None, st, 0, 1, 6, 4, 64, 64, None, 2, 1, 32, 64,
+                                   0, 0, 0, 0, 0.125, None, st, None, None, 0, None)
+    assert rc == 1 and b"multiple of num_kv_heads" in L.fta_last_error()
+    rc = L.fta_sparse_attn_bwd_gqa(None, st, None, st, None, st, None, st, 0, 1, 6, 0, 64, 64, None, 2, 1, 32, 64,
+                                   0, 0, 0, 0, 0.125, None, None, None, st, None, st, None, st, None, 0, None)
+    assert rc == 1 and b"multiple of num_kv_heads" in L.fta_last_error()

@@ -228,6 +228,49 @@ def test_sparse_attn_fwd_bwd_vs_oracle(case):
                           min_frac=0.9995, hard_atol=1e-2 * max(1.0, np.abs(ref).max() / 4))
 
 
+GQA_CASES = [
+    # B, N, H, Hk, D, g, b, qpad, kvpad, W, dtype
+    (1, 1000, 4, 2, 128, 32, 64, (0, 24), (0, 24), 8, torch.bfloat16),   # split dK/dV kernel
+    (2, 600, 6, 2, 64, 16, 64, (4, 4), (12, 28), 6, torch.float16),
+    (1, 700, 4, 1, 96, 32, 96, (0, 4), (5, 63), 5, torch.bfloat16),      # generic dK/dV, 3 tiles per block
+    (1, 512, 4, 2, 32, 32, 32, (0, 0), (0, 0), 6, torch.bfloat16),       # one tile per block
+]
+
+
+@pytest.mark.parametrize("case", GQA_CASES, ids=lambda c: f"H{c[2]}Hk{c[3]}D{c[4]}b{c[6]}")
+def test_gqa_matches_repeated_kv(case):
+    """Grouped-query attention (an extension: the reference raises for it) equals
+    the multi-head path with each K/V head repeated for its query heads: o, lse
+    and dQ bit for bit, dK / dV as the sum of the repeated heads' gradients."""
+    B, N, H, Hk, D, g, b, qpad, kvpad, W, dt = case
+    say(f"[gqa] {case}")
+    G = H // Hk
+    QM = (qpad[0] + N + qpad[1]) // g
+    M = (kvpad[0] + N + kvpad[1]) // b
+    merged = torch.from_numpy(_random_merged(B, H, QM, W, M, 31)).cuda()
+    q = rand((B, N, H * D), 1, dt, "cuda").requires_grad_(True)
+    k = rand((B, N, Hk * D), 2, dt, "cuda").requires_grad_(True)
+    v = rand((B, N, Hk * D), 3, dt, "cuda").requires_grad_(True)
+    do = rand((B, N, H * D), 4, dt, "cuda")
+    o, lse = fta.flash_topk_attn(q, k, v, merged, None, H, g, b, None, Hk, kvpad, qpad)
+    o.backward(do)
+
+    def rep(x):
+        return x.detach().view(B, N, Hk, D).repeat_interleave(G, dim=2).reshape(B, N, H * D).requires_grad_(True)
+
+    q2 = q.detach().clone().requires_grad_(True)
+    k2, v2 = rep(k), rep(v)
+    o2, lse2 = fta.flash_topk_attn(q2, k2, v2, merged, None, H, g, b, None, None, kvpad, qpad)
+    o2.backward(do)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o2) and torch.equal(lse, lse2), "GQA forward != repeated-K/V forward"
+    assert torch.equal(q.grad, q2.grad), "GQA dQ != repeated-K/V dQ"
+    for name, got, ref in (("dk", k.grad, k2.grad), ("dv", v.grad, v2.grad)):
+        r = ref.float().view(B, N, Hk, G, D).sum(3).reshape(B, N, Hk * D).cpu().numpy()
+        s2 = max(1.0, np.abs(r).max() / 4)
+        assert_close_frac(np32(got), r, atol=2e-3 * s2, rtol=1e-2, name=name, min_frac=0.9995, hard_atol=1e-2 * s2)
+
+
 def test_reverse_indices_and_sort_by_count():
     say("[reverse]")
     B, H, QM, W, M = 2, 3, 70, 9, 40
