@@ -83,6 +83,49 @@ def cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, rows):
                       f"(score+select+merge+fwd+bwd), float64 BLAS"}
 
 
+# V1 fused scoring rows of the reference's BENCHMARK.md (other hardware; D not
+# stated there, 128 here): (B, N, H, b, topk, published "Scoring (ms)", its
+# "FA2 (ms)" forward-only lower bound, line)
+V1_ROWS = [(1, 32768, 4, 64, 64, 112.299, 18.524, 136), (1, 8192, 8, 128, 16, 3.759, 2.284, 108)]
+
+
+def bench_v1(dev, stream):
+    """V1 flash_topk_score (dense o + top-k block scores) forward, and forward
+    + backward through o, at two rows of the reference's V1 benchmark."""
+    import torch
+
+    import flash_topk_attn as v1
+
+    D = 128
+    res = []
+    for B, N, H, b, topk, ref_ms, fa2_ms, line in V1_ROWS:
+        gen = torch.Generator(device="cpu").manual_seed(9)
+        q, k, v, do = (torch.randn(B, N, H * D, generator=gen).to(torch.bfloat16).to(dev) for _ in range(4))
+        fw, fb = [], []
+        for it in range(4):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+            e[0].record(stream)
+            with torch.no_grad():
+                v1.flash_topk_score(q, k, v, H, b, topk)
+            e[1].record(stream)
+            ql, kl, vl = (t.detach().requires_grad_(True) for t in (q, k, v))
+            o, _, _ = v1.flash_topk_score(ql, kl, vl, H, b, topk)
+            o.backward(do)
+            e[2].record(stream)
+            torch.cuda.synchronize()
+            if it:
+                fw.append(e[0].elapsed_time(e[1]))
+                fb.append(e[1].elapsed_time(e[2]))
+        fms, fbms = sorted(fw)[1], sorted(fb)[1]
+        f_fwd = 2.0 * B * H * N * N * D + 4.0 * B * H * N * N * D  # scoring QK^T + dense attention
+        res.append({"config": f"B{B} N{N} H{H} D{D} b{b} topk{topk} bf16", "fwd_ms": round(fms, 3),
+                    "fwd_tflops": round(f_fwd / fms / 1e9, 1), "fwd_bwd_ms": round(fbms, 3),
+                    "reference_published_ms_other_hw": ref_ms,
+                    "reference_fa2_ms_other_hw": fa2_ms, "reference_source": f"BENCHMARK.md:{line}"})
+        del q, k, v, do, ql, kl, vl, o
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -90,6 +133,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-iid", action="store_true")
+    ap.add_argument("--no-v1", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=8192)
     ap.add_argument("--only", choices=["score", "topk", "merge", "fwd", "bwd", "copy"], default=None,
                     help="profiling aid: run one stage of the C3 step --steps times and exit")
@@ -264,6 +308,9 @@ def main():
                          "fwd_tflops": round(4 * D * Pi / fms / 1e9, 2),
                          "bwd_tflops_10DP": round(10 * D * Pi / bms / 1e9, 2),
                          "mean_count": Pi / (g * b * B * H * (N // g))}
+
+    if not args.no_v1:
+        out["v1_score"] = bench_v1(dev, stream)
 
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, args.cpu_rows)

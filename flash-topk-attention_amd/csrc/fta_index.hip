@@ -37,6 +37,7 @@ __device__ __forceinline__ int fta_block_scan256(int v, int* s_tmp, int* total) 
 //   positive entries sorted by (score desc, id asc), first W kept.
 // ----------------------------------------------------------------------------
 constexpr int kMergeChunk = 1024;  // staged (id, score) entries per step
+constexpr int kUnionMax = 8192;    // largest union row (ids held in LDS: 32 KB)
 
 __global__ __launch_bounds__(256) void fta_qblock_merge_kernel(const int32_t* __restrict__ idx,
                                                                const float* __restrict__ scr, int g, int K,
@@ -285,6 +286,74 @@ __global__ __launch_bounds__(256) void fta_delta_kernel(const uint16_t* __restri
     if (valid && sub == 0) delta[((int64_t)b * H + h) * N + n] = acc;
 }
 
+
+// ----------------------------------------------------------------------------
+// q-block union (reference V1: flash_topk_attn/attention.py:23-138).  One
+// workgroup per (b, h, q-block): the g*K ids of the block's query rows (rows
+// outside [0, N) under the virtual q padding contribute -1) are sorted
+// ascending in LDS (bitonic, P = next pow2 of g*K, -1 mapped past every id),
+// then the first copy of each non-negative id is compacted to the front of
+// the P-wide output row; the rest of the row is -1 and counts = #unique ids.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fta_qblock_union_kernel(const int32_t* __restrict__ idx, int N, int K,
+                                                               int g, int q_pad_head, int QM, int P,
+                                                               int32_t* __restrict__ merged,
+                                                               int32_t* __restrict__ counts) {
+    extern __shared__ int s_key[];
+    __shared__ int s_tmp[8];
+    const int tid = threadIdx.x;
+    const int64_t slice = blockIdx.x;
+    const int64_t bh = slice / QM;
+    const int qm = (int)(slice - bh * QM);
+    const int n = g * K;
+    const int row0 = qm * g - q_pad_head;
+    const int32_t* src = idx + bh * (int64_t)N * K;
+    for (int i = tid; i < P; i += 256) {
+        int v = 0x7fffffff;
+        if (i < n) {
+            const int r = row0 + i / K;
+            if (r >= 0 && r < N) {
+                const int id = src[(int64_t)r * K + (i - (i / K) * K)];
+                if (id >= 0) v = id;
+            }
+        }
+        s_key[i] = v;
+    }
+    __syncthreads();
+    // bitonic sort, ascending; each step compares P/2 disjoint pairs
+    for (int k = 2; k <= P; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int t = tid; t < (P >> 1); t += 256) {
+                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+                const int a = s_key[i], b = s_key[i + j];
+                const bool up = (i & k) == 0;
+                if ((a > b) == up) {
+                    s_key[i] = b;
+                    s_key[i + j] = a;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    // thread t owns the contiguous run [t*per, (t+1)*per)
+    const int per = (P + 255) / 256;
+    const int lo = min(tid * per, P), hi = min(lo + per, P);
+    int mine = 0;
+    for (int i = lo; i < hi; ++i) {
+        const int v = s_key[i];
+        mine += (v != 0x7fffffff && (i == 0 || v != s_key[i - 1])) ? 1 : 0;
+    }
+    int total = 0;
+    int pos = fta_block_scan256(mine, s_tmp, &total);
+    int32_t* out = merged + slice * (int64_t)P;
+    for (int i = lo; i < hi; ++i) {
+        const int v = s_key[i];
+        if (v != 0x7fffffff && (i == 0 || v != s_key[i - 1])) out[pos++] = v;
+    }
+    for (int i = total + tid; i < P; i += 256) out[i] = -1;
+    if (tid == 0) counts[slice] = total;
+}
+
 namespace fta {
 int launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t st) {
     if (n <= 0) return FTA_OK;
@@ -337,6 +406,32 @@ int fta_qblock_merge_maxid(const int32_t* topk_indices, const float* topk_scores
                        topk_indices, topk_scores, q_block_size, k_per_query, 0, max_index, qblock_topk,
                        merged_indices, merged_scores, counts);
     return fta::check_launch("fta_qblock_merge_kernel");
+    FTA_TRY_END
+}
+
+int fta_qblock_union(const int32_t* topk_indices, int BH, int N, int K, int q_block_size, int q_pad_head,
+                     int q_pad_tail, int s_max, int32_t* merged_indices, int32_t* counts, void* stream) {
+    FTA_TRY_BEGIN
+    if (BH < 0 || N < 0 || K < 0) return fta::arg_error("qblock_union: negative dims");
+    if (q_block_size <= 0) return fta::arg_error("qblock_union: q_block_size must be positive");
+    if (q_pad_head < 0 || q_pad_tail < 0 || q_pad_head >= q_block_size || q_pad_tail >= q_block_size)
+        return fta::arg_error("qblock_union: q padding must each be in [0, q_block_size)");
+    const int64_t np = (int64_t)q_pad_head + N + q_pad_tail;
+    if (np % q_block_size != 0) return fta::arg_error("qblock_union: q_pad_head + N + q_pad_tail not divisible");
+    const int64_t n = (int64_t)q_block_size * K;
+    if (s_max <= 0 || (s_max & (s_max - 1)) != 0 || s_max < n)
+        return fta::arg_error("qblock_union: s_max must be a power of two >= q_block_size * K");
+    if (s_max > kUnionMax) return fta::unsupported("qblock_union: q_block_size * K exceeds 8192");
+    const int QM = (int)(np / q_block_size);
+    const int64_t slices = (int64_t)BH * QM;
+    if (slices > 0x7fffffff) return fta::arg_error("qblock_union: too many q-blocks");
+    if (slices == 0) return FTA_OK;
+    if (!topk_indices && n > 0 && N > 0) return fta::arg_error("qblock_union: topk_indices is NULL");
+    if (!merged_indices || !counts) return fta::arg_error("qblock_union: null output");
+    hipLaunchKernelGGL(fta_qblock_union_kernel, dim3((unsigned)slices), dim3(256), (size_t)s_max * sizeof(int),
+                       (hipStream_t)stream, topk_indices, N, K, q_block_size, q_pad_head, QM, s_max,
+                       merged_indices, counts);
+    return fta::check_launch("fta_qblock_union_kernel");
     FTA_TRY_END
 }
 

@@ -853,6 +853,45 @@ __device__ __forceinline__ int fta_valid_count(int m, int M, int bsz, int pad_he
     return vc;
 }
 
+// Merge a lane's parked candidates into its sorted register list (insertion
+// network, top down: slot p takes slot p-1's entry when the candidate beats
+// it, the candidate when it beats only slot p), then tighten (tv, ti) to the
+// m_out-th entry.  A function rather than a lambda so that it is always
+// inlined: the register lists must never be addressed through memory.
+template <int KB, int CAP>
+__device__ __forceinline__ void fta_topk_flush(float (&lv)[KB], int (&li)[KB], int& cnt, const float (&cv)[CAP][64],
+                                               const int (&ci)[CAP][64], int lane, int m_out, float& tv, int& ti) {
+    int mc = cnt;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) mc = max(mc, __shfl_xor(mc, off, 64));
+    for (int j = 0; j < mc; ++j) {
+        const bool ok = j < cnt;
+        const float v = ok ? cv[j][lane] : -FTA_INF;
+        const int id = ok ? ci[j][lane] : 0x7fffffff;
+        bool bhi = fta_better(v, id, lv[KB - 1], li[KB - 1]);
+#pragma unroll
+        for (int p = KB - 1; p > 0; --p) {
+            const bool blo = fta_better(v, id, lv[p - 1], li[p - 1]);
+            const float nv = blo ? lv[p - 1] : (bhi ? v : lv[p]);
+            const int ni = blo ? li[p - 1] : (bhi ? id : li[p]);
+            lv[p] = nv;
+            li[p] = ni;
+            bhi = blo;
+        }
+        if (bhi) {
+            lv[0] = v;
+            li[0] = id;
+        }
+    }
+    cnt = 0;
+#pragma unroll
+    for (int p = 0; p < KB; ++p)
+        if (p == m_out - 1 && li[p] != 0x7fffffff) {
+            tv = lv[p];
+            ti = li[p];
+        }
+}
+
 template <int KB, int MODE>
 __global__ __launch_bounds__(256) void fta_topk_select_kernel(
     const float* __restrict__ in, int64_t stride_row, int64_t stride_m, const float* __restrict__ row_lse,
@@ -899,7 +938,7 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
     // 2^x >= thr_norm, with a 2^-12 margin far above exp2 / log2 rounding, so
     // the test stays conservative and exp2 runs only for candidates.
     float thr_log = -FTA_INF;
-    auto set_thr = [&]() {
+    auto set_thr = [&] __attribute__((always_inline)) () {
         const float t = tv * (float)bsz;
         thr_norm = t - fabsf(t) * 9.5367431640625e-07f;
         thr_log = (thr_norm > 0.f) ? fta_log2(thr_norm) - 2.44140625e-04f : -FTA_INF;
@@ -913,49 +952,17 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
     }
     set_thr();
 
-    auto flush = [&]() {
-        int mc = cnt;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) mc = max(mc, __shfl_xor(mc, off, 64));
-        for (int j = 0; j < mc; ++j) {
-            const bool ok = j < cnt;
-            const float v = ok ? cand_v[wave][j][lane] : -FTA_INF;
-            const int id = ok ? cand_i[wave][j][lane] : 0x7fffffff;
-            bool bt[KB];
-#pragma unroll
-            for (int p = 0; p < KB; ++p) bt[p] = fta_better(v, id, lv[p], li[p]);
-#pragma unroll
-            for (int p = KB - 1; p > 0; --p) {
-                const float nv = bt[p - 1] ? lv[p - 1] : (bt[p] ? v : lv[p]);
-                const int ni = bt[p - 1] ? li[p - 1] : (bt[p] ? id : li[p]);
-                lv[p] = nv;
-                li[p] = ni;
-            }
-            if (bt[0]) {
-                lv[0] = v;
-                li[0] = id;
-            }
-        }
-        cnt = 0;
-#pragma unroll
-        for (int p = 0; p < KB; ++p)
-            if (p == m_out - 1 && li[p] != 0x7fffffff) {
-                tv = lv[p];
-                ti = li[p];
-            }
-        set_thr();
-    };
 
     // Unconditional loads (an inactive lane reads row 0), clamped past M, two
     // batches in flight: batch k + 1 loads while batch k is tested.
-    auto load_batch = [&](int m1, float (&xs)[LDB]) {
+    auto load_batch = [&] __attribute__((always_inline)) (int m1, float (&xs)[LDB]) {
 #pragma unroll
         for (int u = 0; u < LDB; ++u) {
             const int m = min(m1 + u, M - 1);
             xs[u] = (MODE == 0) ? src[m * stride_m] : src[(int64_t)m * N];
         }
     };
-    auto test_batch = [&](int m1, const float (&xs)[LDB]) {
+    auto test_batch = [&] __attribute__((always_inline)) (int m1, const float (&xs)[LDB]) {
         // Skip the batch when no lane can find a candidate in it: the largest
         // value of each lane's batch is below its pre-filter bound, and the
         // batch holds no partial (always tested) edge block.  Exact: the
@@ -994,7 +1001,10 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
                     }
                 }
             }
-            if (__ballot(cnt > CAP - UNR) != 0ull) flush();
+            if (__ballot(cnt > CAP - UNR) != 0ull) {
+                fta_topk_flush<KB, CAP>(lv, li, cnt, cand_v[wave], cand_i[wave], lane, m_out, tv, ti);
+                set_thr();
+            }
         }
     };
     float xa[LDB], xb[LDB];
@@ -1006,7 +1016,7 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
         load_batch(m1 + 2 * LDB, xa);
         test_batch(m1 + LDB, xb);
     }
-    flush();
+    fta_topk_flush<KB, CAP>(lv, li, cnt, cand_v[wave], cand_i[wave], lane, m_out, tv, ti);
 
     if (!active) return;
     float cs = 0.f;

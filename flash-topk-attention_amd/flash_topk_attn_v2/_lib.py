@@ -42,6 +42,7 @@ _SIGNATURES = {
                             _sz, _p]),
     "fta_qblock_merge": (_i, [_p, _p, _i64, _i, _i, _i, _i, _p, _p, _p, _p]),
     "fta_qblock_merge_maxid": (_i, [_p, _p, _i64, _i, _i, _p, _i, _p, _p, _p, _p]),
+    "fta_qblock_union": (_i, [_p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p]),
     "fta_build_reverse_indices_workspace_size": (_sz, [_i, _i, _i, _i]),
     "fta_build_reverse_indices": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p, _sz, _p]),
     "fta_sort_by_count": (_i, [_p, _i64, _p, _p, _p]),

@@ -136,6 +136,19 @@ int fta_qblock_merge_maxid(const int32_t* topk_indices, const float* topk_scores
                            int q_block_size, int k_per_query, const int32_t* max_index, int qblock_topk,
                            int32_t* merged_indices, float* merged_scores, int32_t* counts, void* stream);
 
+/*
+ * V1 q-block union: for each (b*h, q-block) the ascending unique non-negative
+ * ids of the block's q_block_size * K top-k entries (query rows outside
+ * [0, N) under the virtual q padding contribute nothing), written as a valid
+ * prefix of merged_indices[bh][qm][0 .. s_max) followed by -1, and counts
+ * [bh][qm] = the number of ids.  topk_indices is [BH, N, K] int32 contiguous;
+ * s_max must be a power of two >= q_block_size * K and <= 8192.  Replaces
+ * _build_qblock_indices_kernel behind V1 build_qblock_topk_indices
+ * (flash_topk_attn/attention.py:23-138).
+ */
+int fta_qblock_union(const int32_t* topk_indices, int BH, int N, int K, int q_block_size, int q_pad_head,
+                     int q_pad_tail, int s_max, int32_t* merged_indices, int32_t* counts, void* stream);
+
 size_t fta_build_reverse_indices_workspace_size(int B, int H, int QM, int M);
 
 /*

@@ -22,6 +22,15 @@ relative to the reference repository root, ``v2/`` = ``flash_topk_attn_v2/``):
 * ``sort_by_count``        v2/sparse_attn_bwd.py:79-108
 * ``sparse_attn_bwd``      v2/sparse_attn_bwd.py:111-294
 
+V1 compatibility layer (``v1/`` = ``flash_topk_attn/``):
+
+* ``v1_qblock_union``      v1/attention.py:23-138 (sort, dedup, -1 fill)
+* ``v1_topk_score``        v1/scoring.py:1360-1469 (naive: softmax block sums,
+                           / valid count under padding, descending top-k; dense o)
+* ``v1_sparse_attn``       v1/attention.py:423-568, 571-647 (ids limited to
+                           ``counts``, one merged row shared by all heads when
+                           ``merged.shape[1] == 1``)
+
 Orders that the reference leaves implementation-defined are fixed here, and
 the HIP kernels follow the same rules:
 
@@ -417,3 +426,99 @@ __all__ = [
     "sort_by_count",
     "sparse_attn_bwd",
 ]
+
+
+# --------------------------------------------------------------------------
+# V1 compatibility layer: v1/attention.py, v1/scoring.py
+# --------------------------------------------------------------------------
+
+
+def _next_pow2(x: int) -> int:
+    return 1 if x <= 0 else 1 << (x - 1).bit_length()
+
+
+def v1_qblock_union(
+    topk_indices: np.ndarray, q_block_size: int, q_padding: Tuple[int, int] = (0, 0)
+) -> Tuple[np.ndarray, np.ndarray, int]:
+    """v1/attention.py:23-138: per q-block, the ascending unique non-negative
+    ids of its rows' top-k entries (rows padded with -1), -1 filled to
+    ``S_MAX = next_pow2(q_block_size * K)``; counts = number of ids."""
+    B, H, N, K = topk_indices.shape
+    ph, pt = q_padding
+    idx = np.pad(np.asarray(topk_indices).astype(np.int64), ((0, 0), (0, 0), (ph, pt), (0, 0)), constant_values=-1)
+    QM = (ph + N + pt) // q_block_size
+    S = _next_pow2(q_block_size * K)
+    merged = np.full((B, H, QM, S), -1, dtype=np.int32)
+    counts = np.zeros((B, H, QM), dtype=np.int32)
+    for b in range(B):
+        for h in range(H):
+            for qm in range(QM):
+                ids = idx[b, h, qm * q_block_size:(qm + 1) * q_block_size].reshape(-1)
+                u = np.unique(ids[ids >= 0])
+                merged[b, h, qm, :len(u)] = u
+                counts[b, h, qm] = len(u)
+    return merged, counts, S
+
+
+def v1_topk_score(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: Optional[np.ndarray],
+    num_heads: Optional[int],
+    score_block_size: int,
+    topk: int,
+    padding: Tuple[int, int] = (0, 0),
+) -> Tuple[Optional[np.ndarray], np.ndarray, np.ndarray]:
+    """v1/scoring.py:1360-1469.  Block scores are the softmax mass per block
+    (float64), divided by the block's valid token count when padding is used
+    (the count rule of ``valid_counts``); the top ``min(topk, M)`` are returned
+    in descending order, ties to the lower index.  With ``v``, also the dense
+    attention output ``o`` ([B, N, C] float64; q/k/v 3D only)."""
+    bs = block_score(q, k, num_heads, score_block_size, padding)
+    M = bs.shape[-1]
+    if padding != (0, 0):
+        bs = bs / valid_counts(M, score_block_size, padding).astype(np.float64)
+    kk = min(topk, M)
+    order = np.argsort(-bs, axis=-1, kind="stable")[..., :kk]
+    scores = np.take_along_axis(bs, order, axis=-1)
+    o = None
+    if v is not None:
+        B, N, C = q.shape
+        H = num_heads
+        Dh = C // H
+        q4, k4, v4 = _to_bhnd(q, H), _to_bhnd(k, H), _to_bhnd(v, H)
+        s = np.einsum("bhqd,bhkd->bhqk", q4 * Dh ** -0.5, k4)
+        p = np.exp(s - _logsumexp(s)[..., None])
+        o = _from_bhnd(np.einsum("bhqk,bhkd->bhqd", p, v4))
+    return o, order.astype(np.int32), scores
+
+
+def v1_sparse_attn(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    merged_indices: np.ndarray,
+    counts: np.ndarray,
+    num_heads: int,
+    q_block_size: int,
+    kv_block_size: int,
+    scale: Optional[float] = None,
+    kv_padding: Tuple[int, int] = (0, 0),
+    q_padding: Tuple[int, int] = (0, 0),
+    S_MAX: Optional[int] = None,
+) -> Tuple[np.ndarray, np.ndarray]:
+    """v1/attention.py:423-647: softmax over the union of the first
+    ``min(count, S_MAX)`` ids of each q-block (heads share row 0 when
+    ``merged.shape[1] == 1``); o = 0, lse = -inf for empty q-blocks."""
+    B, N, C = q.shape
+    H = num_heads
+    merged = np.asarray(merged_indices).astype(np.int64)
+    if S_MAX is None:
+        S_MAX = merged.shape[-1]
+    W = min(S_MAX, merged.shape[-1])
+    merged = merged[..., :W]
+    cnt = np.minimum(np.asarray(counts).astype(np.int64), W)
+    merged = np.where(np.arange(W) < cnt[..., None], merged, -1)
+    if merged.shape[1] == 1:
+        merged = np.broadcast_to(merged, (B, H) + merged.shape[2:])
+    return sparse_attn(q, k, v, merged, H, q_block_size, kv_block_size, scale, q_padding, kv_padding)

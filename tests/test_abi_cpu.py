@@ -78,3 +78,34 @@ def test_gqa_head_count_checked_before_any_gpu_work():
     rc = L.fta_sparse_attn_bwd_gqa(None, st, None, st, None, st, None, st, 0, 1, 6, 0, 64, 64, None, 2, 1, 32, 64,
                                    0, 0, 0, 0, 0.125, None, None, None, st, None, st, None, st, None, 0, None)
     assert rc == 1 and b"multiple of num_kv_heads" in L.fta_last_error()
+
+
+def test_v1_api_validation_without_gpu():
+    import flash_topk_attn as v1
+
+    q = torch.zeros(1, 100, 64)
+    with pytest.raises(ValueError, match="unsupported backend"):
+        v1.flash_topk_score(q, q, q, 1, backend="cuda")
+    with pytest.raises(ValueError, match="v is required"):
+        v1.flash_topk_score(q, q, None, 1)
+    with pytest.raises(ValueError, match="num_heads is required"):
+        v1.flash_topk_score(q, q, q)
+    with pytest.raises(ValueError, match="must each be <"):
+        v1.flash_topk_score(q, q, None, 1, 64, 1, (64, 0), score_only=True)
+    with pytest.raises(ValueError, match="must be divisible"):
+        v1.flash_topk_score(q, q, None, 1, 64, 1, (0, 0), score_only=True)
+    with pytest.raises(ValueError, match=r"topk \(3\) > num_blocks \(2\)"):
+        v1.flash_topk_score(q, q, None, 1, 64, 3, (0, 28), score_only=True)
+    with pytest.raises(ValueError, match=r"num_heads \(3\) != q.shape\[1\] \(2\)"):
+        v1.flash_topk_score(torch.zeros(1, 2, 8, 16), torch.zeros(1, 2, 8, 16), None, 3, score_only=True)
+    ids = torch.zeros(1, 1, 100, 4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="q_pad_head=32 must be < q_block_size=32"):
+        v1.build_qblock_topk_indices(ids, 32, (32, 0))
+    with pytest.raises(AssertionError, match="must be divisible"):
+        v1.build_qblock_topk_indices(ids, 32, (0, 0))
+    with pytest.raises(NotImplementedError, match="union limit"):
+        v1.build_qblock_topk_indices(torch.zeros(1, 1, 128, 256, dtype=torch.int32), 64)
+    with pytest.raises(ValueError, match="requires CUDA"):
+        v1.build_qblock_topk_indices(ids, 20, (0, 0))
+    with pytest.raises(ValueError, match="requires CUDA"):
+        v1.flash_topk_attn(q, q, q, ids, ids[..., 0], 1, 32, 64)

@@ -82,6 +82,30 @@ def test_topk_select_bit_exact_and_fused(case, thr, topk):
     np.testing.assert_array_equal(fa.cpu().numpy(), ra)
 
 
+WIDE_K_CASES = [
+    # B, N, H, D, b, padding, dtype, layout, thr, topk: register lists of 32 and 64 entries
+    (1, 2048, 2, 64, 32, (0, 0), torch.bfloat16, "bnc", 1.0, 32),
+    (1, 4096, 2, 64, 32, (0, 0), torch.float16, "bnc", 0.95, 48),
+    (1, 4072, 1, 128, 64, (24, 0), torch.bfloat16, "bnc", 2.0, 64),
+]
+
+
+@pytest.mark.parametrize("case", WIDE_K_CASES, ids=lambda c: f"N{c[1]}b{c[4]}k{c[9]}t{c[8]}")
+def test_topk_select_wide_k_bit_exact(case):
+    B, N, H, D, b, pad, dt, layout, thr, topk = case
+    say(f"[topk wide] {case}")
+    q, k = _qk(case[:8], 21)
+    scores = fta.flash_block_score(q, k, H, b, pad)
+    idx, raw, avg = fta.flash_topk_select(scores, thr, topk, b, pad)
+    fi, fr, fa = fta.flash_topk_score(q, k, H, b, topk, pad, thr)
+    torch.cuda.synchronize()
+    ri, rr, ra = O.topk_select(scores.cpu().numpy(), thr, topk, b, pad)
+    for got in ((idx, raw, avg), (fi, fr, fa)):
+        np.testing.assert_array_equal(got[0].cpu().numpy(), ri)
+        np.testing.assert_array_equal(got[1].cpu().numpy(), rr)
+        np.testing.assert_array_equal(got[2].cpu().numpy(), ra)
+
+
 @pytest.mark.parametrize("case", SCORE_CASES[:4], ids=lambda c: f"N{c[1]}D{c[3]}b{c[4]}")
 def test_topk_score_vs_float64_oracle(case):
     B, N, H, D, b, pad, dt, layout = case

@@ -293,3 +293,79 @@ def test_reverse_indices_brute_force():
     flat = cnt.ravel().tolist()
     assert sid.tolist() == sorted(range(len(flat)), key=lambda i: (-flat[i], i))
     assert sc.tolist() == [flat[i] for i in sid]
+
+
+# ---------------------------------------------------------------- V1 layer
+
+
+def test_v1_union_brute_force():
+    r = _rng(20)
+    B, H, N, K, g, qpad = 2, 2, 37, 5, 8, (1, 2)
+    ids = r.integers(-1, 12, (B, H, N, K))
+    merged, counts, S = O.v1_qblock_union(ids, g, qpad)
+    assert S == 64  # next_pow2(8 * 5)
+    QM = (1 + N + 2) // g
+    for b in range(B):
+        for h in range(H):
+            for qm in range(QM):
+                want = set()
+                for j in range(g):
+                    n = qm * g + j - qpad[0]
+                    if 0 <= n < N:
+                        want |= {int(x) for x in ids[b, h, n] if x >= 0}
+                row = merged[b, h, qm]
+                assert counts[b, h, qm] == len(want)
+                assert list(row[:len(want)]) == sorted(want)
+                assert np.all(row[len(want):] == -1)
+
+
+def test_v1_topk_score_is_sorted_block_mass_and_dense_o():
+    r = _rng(21)
+    B, N, H, D, b = 1, 24, 2, 8, 8
+    q, k, v = (r.standard_normal((B, N, H * D)) for _ in range(3))
+    o, idx, sc = O.v1_topk_score(q, k, v, H, b, 3)
+    brute = _brute_block_score(q, k, H, b, (0, 0))
+    # topk = M: every block, in descending mass, and the masses sum to 1
+    np.testing.assert_allclose(sc.sum(-1), 1.0, rtol=1e-12)
+    for bb in range(B):
+        for h in range(H):
+            for n in range(N):
+                order = sorted(range(3), key=lambda m: (-brute[bb, h, n, m], m))
+                assert list(idx[bb, h, n]) == order
+                np.testing.assert_allclose(sc[bb, h, n], brute[bb, h, n, order], rtol=1e-10)
+    th = [torch.from_numpy(x).view(B, N, H, D).transpose(1, 2) for x in (q, k, v)]
+    ref = torch.nn.functional.scaled_dot_product_attention(*th).transpose(1, 2).reshape(B, N, H * D)
+    np.testing.assert_allclose(o, ref.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_v1_topk_score_padding_divides_by_valid_count():
+    r = _rng(22)
+    B, N, H, D, b, pad = 1, 13, 1, 4, 8, (3, 0)
+    q, k = (r.standard_normal((B, N, H * D)) for _ in range(2))
+    _, idx, sc = O.v1_topk_score(q, k, None, H, b, 2, pad)
+    brute = _brute_block_score(q, k, H, b, pad)
+    per_tok = brute / np.array([5.0, 8.0])  # block 0 holds 8 - 3 real tokens
+    for n in range(N):
+        order = sorted(range(2), key=lambda m: (-per_tok[0, 0, n, m], m))
+        assert list(idx[0, 0, n]) == order
+        np.testing.assert_allclose(sc[0, 0, n], per_tok[0, 0, n, order], rtol=1e-10)
+
+
+def test_v1_sparse_attn_counts_and_shared_heads():
+    r = _rng(23)
+    B, N, H, D, g, b = 1, 16, 2, 4, 8, 4
+    q, k, v = (r.standard_normal((B, N, H * D)) for _ in range(3))
+    merged = np.array([[[[0, 2, 3, -1], [1, 3, 0, 2]]]], dtype=np.int32)  # H_BI = 1
+    counts = np.array([[[2, 4]]], dtype=np.int32)
+    o, lse = O.v1_sparse_attn(q, k, v, merged, counts, H, g, b, S_MAX=3)
+    # q-block 0 uses blocks {0, 2}; q-block 1 uses the first 3 ids {1, 3, 0}; both heads alike
+    q4, k4, v4 = (x.reshape(B, N, H, D).transpose(0, 2, 1, 3) for x in (q, k, v))
+    for h in range(H):
+        for qm, blocks in ((0, [0, 2]), (1, [1, 3, 0])):
+            toks = [t for m in blocks for t in range(m * b, m * b + b)]
+            s = q4[0, h, qm * g:(qm + 1) * g] @ k4[0, h, toks].T / math.sqrt(D)
+            p = np.exp(s - s.max(-1, keepdims=True))
+            ref_lse = np.log(p.sum(-1)) + s.max(-1)
+            ref_o = (p / p.sum(-1, keepdims=True)) @ v4[0, h, toks]
+            np.testing.assert_allclose(lse[0, h, qm * g:(qm + 1) * g], ref_lse, rtol=1e-12)
+            np.testing.assert_allclose(o.reshape(B, N, H, D)[0, qm * g:(qm + 1) * g, h], ref_o, rtol=1e-10)
