@@ -35,8 +35,9 @@ def flash_topk_score(
 
     Returns ``(topk_indices int32, topk_raw_scores f32, topk_avg_scores f32)``,
     each ``[B, H, N, min(topk, M)]`` (``M`` when ``topk == 0``).  Scoring and
-    selection run fused: the ``[B, H, N, M]`` score tensor is never
-    materialised.
+    selection run in one C call: the normalised ``[B, H, N, M]`` scores are
+    never formed; the selector reads the scorer's per-block log2-sums from a
+    workspace.
     """
     input_4d = q.ndim == 4
     if input_4d:
