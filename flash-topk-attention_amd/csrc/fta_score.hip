@@ -853,21 +853,37 @@ __device__ __forceinline__ int fta_valid_count(int m, int M, int bsz, int pad_he
     return vc;
 }
 
-// Merge a lane's parked candidates into its sorted register list (insertion
-// network, top down: slot p takes slot p-1's entry when the candidate beats
-// it, the candidate when it beats only slot p), then tighten (tv, ti) to the
-// m_out-th entry.  A function rather than a lambda so that it is always
-// inlined: the register lists must never be addressed through memory.
-template <int KB, int CAP>
+// Merge a lane's parked candidates into its sorted register list, then
+// tighten (tv, ti) to the m_out-th entry.  Candidates are parked by a cheap
+// pre-filter only (the loaded value x and block m); the exact tests run here,
+// for candidates alone: the pre-filter bound (pre) and raw >= thr_norm, both
+// waived for partial edge blocks, then avg = raw / valid_count must beat the
+// current m_out-th entry.  Bounds only tighten, so testing against the bounds
+// at flush time rather than at parking time drops only blocks that could not
+// be in the final list.  Insertion network, top down: slot p takes slot p-1's
+// entry when the candidate beats it, the candidate when it beats only slot p.
+// A function rather than a lambda so that it is always inlined: the register
+// lists must never be addressed through memory.
+template <int KB, int CAP, int MODE>
 __device__ __forceinline__ void fta_topk_flush(float (&lv)[KB], int (&li)[KB], int& cnt, const float (&cv)[CAP][64],
-                                               const int (&ci)[CAP][64], int lane, int m_out, float& tv, int& ti) {
+                                               const int (&ci)[CAP][64], int lane, bool active, float rl, float pre,
+                                               float thr_norm, int M, int bsz, int pad_head, int pad_tail,
+                                               int m_out, float& tv, int& ti) {
     int mc = cnt;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) mc = max(mc, __shfl_xor(mc, off, 64));
     for (int j = 0; j < mc; ++j) {
-        const bool ok = j < cnt;
-        const float v = ok ? cv[j][lane] : -FTA_INF;
-        const int id = ok ? ci[j][lane] : 0x7fffffff;
+        const float xs = cv[j][lane];
+        const int m = ci[j][lane];
+        const bool edge = (m == 0 && pad_head > 0) || (m == M - 1 && pad_tail > 0);
+        const float x = (MODE == 0) ? xs : xs - rl;
+        const float raw = (MODE == 0) ? x : fta_exp2(x);
+        const int vc = fta_valid_count(m, M, bsz, pad_head, pad_tail);
+        const float avg = raw / (float)vc;
+        const bool ok = active && j < cnt && (edge || (x >= pre && raw >= thr_norm)) &&
+                        fta_better(avg, m, tv, ti);
+        const float v = ok ? avg : -FTA_INF;
+        const int id = ok ? m : 0x7fffffff;
         bool bhi = fta_better(v, id, lv[KB - 1], li[KB - 1]);
 #pragma unroll
         for (int p = KB - 1; p > 0; --p) {
@@ -962,19 +978,30 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
             xs[u] = (MODE == 0) ? src[m * stride_m] : src[(int64_t)m * N];
         }
     };
+    // Scan: every block of a sub-batch is parked at slot cnt of the lane's list
+    // and cnt advances when the pre-filter passes (x >= pre, or a partial edge
+    // block), with no branch per block: the lanes of a wave find candidates at
+    // unrelated blocks, so a per-block branch would run for almost every block.
+    auto flush = [&] __attribute__((always_inline)) () {
+        fta_topk_flush<KB, CAP, MODE>(lv, li, cnt, cand_v[wave], cand_i[wave], lane, active, rl,
+                                      (MODE == 0) ? thr_norm : thr_log, thr_norm, M, bsz, pad_head, pad_tail,
+                                      m_out, tv, ti);
+        set_thr();
+    };
     auto test_batch = [&] __attribute__((always_inline)) (int m1, const float (&xs)[LDB]) {
-        // Skip the batch when no lane can find a candidate in it: the largest
-        // value of each lane's batch is below its pre-filter bound, and the
-        // batch holds no partial (always tested) edge block.  Exact: the
-        // per-block tests below would reject every block of such a batch.
+        const bool edges = (m1 == 0 && pad_head > 0) || (m1 + LDB >= M && pad_tail > 0);
+        // the lane's pre-filter bound; +inf parks nothing for lanes past the last row
+        const float pre = active ? ((MODE == 0) ? thr_norm : thr_log) : FTA_INF;
+        const float pre_edge = active ? -FTA_INF : FTA_INF;  // edge blocks: parked unconditionally
+        // Skip the batch when no lane can park a block of it: the largest value
+        // of each lane's batch is below its bound and the batch holds no edge
+        // block.  Exact: the scan below would park nothing.
         {
             float bm = xs[0];
 #pragma unroll
             for (int u = 1; u < LDB; ++u) bm = fmaxf(bm, xs[u]);
             const float bx = (MODE == 0) ? bm : bm - rl;
-            const bool may = active && ((MODE == 0) ? (bx >= thr_norm) : (bx >= thr_log));
-            const bool edges = (m1 == 0 && pad_head > 0) || (m1 + LDB >= M && pad_tail > 0);
-            if (!edges && __ballot(may) == 0ull) return;
+            if (!edges && __ballot(bx >= pre) == 0ull) return;
         }
 #pragma unroll
         for (int sb = 0; sb < LDB; sb += UNR) {
@@ -982,29 +1009,16 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
 #pragma unroll
             for (int u = 0; u < UNR; ++u) {
                 const int m = m1 + sb + u;
-                const bool edge = (m == 0 && pad_head > 0) || (m == M - 1 && pad_tail > 0);
                 const float x = (MODE == 0) ? xs[sb + u] : xs[sb + u] - rl;
-                const bool pass = (MODE == 0) ? (x >= thr_norm) : (x >= thr_log);
-                if (active && m < M && (pass || edge)) {
-                    const float raw = (MODE == 0) ? x : fta_exp2(x);
-                    if (raw >= thr_norm || edge) {
-                        const int vc = fta_valid_count(m, M, bsz, pad_head, pad_tail);
-                        // x / 2^j == x * 2^-j exactly (same exact value, same rounding)
-                        const float avg = ((vc & (vc - 1)) == 0)
-                                              ? raw * __builtin_amdgcn_ldexpf(1.f, -__builtin_ctz(vc))
-                                              : raw / (float)vc;
-                        if (fta_better(avg, m, tv, ti)) {
-                            cand_v[wave][cnt][lane] = avg;
-                            cand_i[wave][cnt][lane] = m;
-                            ++cnt;
-                        }
-                    }
-                }
+                // per-block bound, selected by wave-uniform conditions (no branch)
+                const bool em = edges && ((m == 0 && pad_head > 0) || (m == M - 1 && pad_tail > 0));
+                const float pm = (m >= M) ? FTA_INF : (em ? pre_edge : pre);
+                const bool pass = x >= pm;
+                cand_v[wave][cnt][lane] = xs[sb + u];
+                cand_i[wave][cnt][lane] = m;
+                cnt += pass ? 1 : 0;
             }
-            if (__ballot(cnt > CAP - UNR) != 0ull) {
-                fta_topk_flush<KB, CAP>(lv, li, cnt, cand_v[wave], cand_i[wave], lane, m_out, tv, ti);
-                set_thr();
-            }
+            if (__ballot(cnt > CAP - UNR) != 0ull) flush();
         }
     };
     float xa[LDB], xb[LDB];
@@ -1016,7 +1030,7 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
         load_batch(m1 + 2 * LDB, xa);
         test_batch(m1 + LDB, xb);
     }
-    fta_topk_flush<KB, CAP>(lv, li, cnt, cand_v[wave], cand_i[wave], lane, m_out, tv, ti);
+    flush();
 
     if (!active) return;
     float cs = 0.f;
