@@ -882,6 +882,7 @@ __device__ __forceinline__ void fta_topk_flush(float (&lv)[KB], int (&li)[KB], i
         const float avg = raw / (float)vc;
         const bool ok = active && j < cnt && (edge || (x >= pre && raw >= thr_norm)) &&
                         fta_better(avg, m, tv, ti);
+        if (__ballot(ok) == 0ull) continue;  // no lane inserts: skip the network
         const float v = ok ? avg : -FTA_INF;
         const int id = ok ? m : 0x7fffffff;
         bool bhi = fta_better(v, id, lv[KB - 1], li[KB - 1]);
@@ -897,6 +898,10 @@ __device__ __forceinline__ void fta_topk_flush(float (&lv)[KB], int (&li)[KB], i
         if (bhi) {
             lv[0] = v;
             li[0] = id;
+        }
+        if (m_out == KB && li[KB - 1] != 0x7fffffff) {  // a full list bounds the rest of the flush
+            tv = lv[KB - 1];
+            ti = li[KB - 1];
         }
     }
     cnt = 0;
@@ -917,7 +922,7 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
     constexpr int LDB = 32;             // blocks loaded per batch
     constexpr int UNR = 8;              // blocks tested between candidate-list checks
     constexpr int CAP = 16 + UNR;       // a sub-batch starts with at most CAP - UNR parked candidates
-    __shared__ float cand_v[4][CAP][64];
+    __shared__ __align__(16) float cand_v[4][CAP][64];
     __shared__ int cand_i[4][CAP][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int row = blockIdx.x * 256 + tid;
@@ -1032,7 +1037,10 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
     }
     flush();
 
-    if (!active) return;
+    // the wave's rows are consecutive: rows wrow0 .. wrow0 + nrows - 1
+    const int64_t wrow0 = (int64_t)blockIdx.x * 256 + wave * 64;
+    const int nrows = (int)min((int64_t)64, (int64_t)rows - wrow0);
+    if (nrows <= 0) return;
     float cs = 0.f;
     int cut = m_out;
     bool found = false;
@@ -1047,15 +1055,50 @@ __global__ __launch_bounds__(256) void fta_topk_select_kernel(
             }
         }
     }
+    float rawv[KB];
+#pragma unroll
+    for (int p = 0; p < KB; ++p) {
+        const bool keep = p < cut;
+        rawv[p] = keep ? __fmul_rn(lv[p], (float)fta_valid_count(li[p], M, bsz, pad_head, pad_tail)) : 0.f;
+        lv[p] = keep ? lv[p] : 0.f;
+        li[p] = keep ? li[p] : -1;
+    }
+    const bool aligned = ((reinterpret_cast<uintptr_t>(out_idx) | reinterpret_cast<uintptr_t>(out_raw) |
+                           reinterpret_cast<uintptr_t>(out_avg)) & 15) == 0;
+    if (m_out <= CAP && aligned) {
+        // Stage each output's 64 x m_out block (contiguous in HBM) in this wave's
+        // candidate buffer, then write it with 16-byte stores over consecutive
+        // addresses instead of one 4-byte store per (lane, slot).
+        float* st = &cand_v[wave][0][0];
+        const int total = nrows * m_out, n4 = total >> 2;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            float* out = (k == 0) ? reinterpret_cast<float*>(out_idx) : (k == 1) ? out_raw : out_avg;
+            out += wrow0 * m_out;
+#pragma unroll
+            for (int p = 0; p < KB; ++p)
+                if (p < m_out)
+                    st[lane * m_out + p] = (k == 0) ? __builtin_bit_cast(float, li[p]) : (k == 1) ? rawv[p] : lv[p];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (int c = lane; c < n4; c += 64)
+                reinterpret_cast<float4*>(out)[c] = reinterpret_cast<const float4*>(st)[c];
+            for (int e = (n4 << 2) + lane; e < total; e += 64) out[e] = st[e];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        return;
+    }
+    if (!active) return;
     const int64_t o = (int64_t)row * m_out;
 #pragma unroll
     for (int p = 0; p < KB; ++p) {
         if (p < m_out) {
-            const bool keep = p < cut;
-            out_idx[o + p] = keep ? li[p] : -1;
-            out_avg[o + p] = keep ? lv[p] : 0.f;
-            out_raw[o + p] =
-                keep ? __fmul_rn(lv[p], (float)fta_valid_count(li[p], M, bsz, pad_head, pad_tail)) : 0.f;
+            out_idx[o + p] = li[p];
+            out_avg[o + p] = lv[p];
+            out_raw[o + p] = rawv[p];
         }
     }
 }
