@@ -149,6 +149,124 @@ __global__ __launch_bounds__(256) void fta_qblock_merge_kernel(const int32_t* __
 }
 
 // ----------------------------------------------------------------------------
+// q-block merge, one wave per slice (used when g*K <= 4096).  Same results as
+// fta_qblock_merge_kernel without an M-sized histogram:
+//   1. the slice's valid entries (0 <= id < block count) are compacted and
+//      sorted ascending by (id << 16 | position) in LDS (bitonic), so each
+//      id's entries form one run in position order;
+//   2. the first lane of a run sums it sequentially in that order (the same
+//      fp32 additions, in the same order, as the histogram kernel);
+//   3. positive sums are compacted and sorted by (score desc, id asc).
+// No workgroup barrier: up to four waves, each on its own slice and LDS region.
+// ----------------------------------------------------------------------------
+constexpr int kMergeWaveMax = 4096;  // largest g*K of the one-wave path
+
+__device__ __forceinline__ void fta_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ __launch_bounds__(256) void fta_qblock_merge_wave_kernel(
+    const int32_t* __restrict__ idx, const float* __restrict__ scr, int64_t num_slices, int g, int K, int NP,
+    int Mt_arg, const int32_t* __restrict__ max_id, int W, int32_t* __restrict__ out_idx,
+    float* __restrict__ out_scr, int32_t* __restrict__ counts) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wpb = blockDim.x >> 6;
+    const int64_t slice = (int64_t)blockIdx.x * wpb + wave;
+    if (slice >= num_slices) return;
+    const int Mt = max_id ? min(max(*max_id + 1, 1), 4096) : Mt_arg;
+    unsigned char* base = smem + (size_t)wave * NP * 16;
+    unsigned long long* out = reinterpret_cast<unsigned long long*>(base);  // [NP]
+    uint32_t* key = reinterpret_cast<uint32_t*>(base + (size_t)NP * 8);      // [NP]
+    float* sc = reinterpret_cast<float*>(base + (size_t)NP * 12);            // [NP], by position
+    const int n = g * K;
+    const int32_t* ip = idx + slice * (int64_t)n;
+    const float* sp = scr + slice * (int64_t)n;
+    // valid entries are compacted (ballot) so that only next_pow2(#valid) keys are sorted
+    int NV = 0;
+    for (int r0 = 0; r0 < n; r0 += 64) {
+        const int i = r0 + lane;
+        bool valid = false;
+        uint32_t kv = 0xffffffffu;
+        if (i < n) {
+            const int id = ip[i];
+            sc[i] = sp[i];
+            valid = id >= 0 && id < Mt;
+            kv = ((uint32_t)id << 16) | (uint32_t)i;
+        }
+        const unsigned long long vm = __ballot(valid);
+        if (valid) key[NV + __popcll(vm & ((1ull << lane) - 1ull))] = kv;
+        NV += __popcll(vm);
+    }
+    int NS = 1;
+    while (NS < NV) NS <<= 1;
+    for (int i = NV + lane; i < NS; i += 64) key[i] = 0xffffffffu;
+    fta_wave_sync();
+    for (int k = 2; k <= NS; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int t = lane; t < (NS >> 1); t += 64) {
+                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+                const uint32_t a = key[i], b = key[i + j];
+                if ((a > b) == ((i & k) == 0)) {
+                    key[i] = b;
+                    key[i + j] = a;
+                }
+            }
+            fta_wave_sync();
+        }
+    }
+    int P = 0;
+    for (int r0 = 0; r0 < NV; r0 += 64) {
+        const int i = r0 + lane;
+        const uint32_t kv = (i < NV) ? key[i] : 0xffffffffu;
+        const uint32_t id = kv >> 16;
+        const bool head = kv != 0xffffffffu && (i == 0 || (key[i - 1] >> 16) != id);
+        float sum = 0.f;
+        if (head)
+            for (int j = i; j < NV && (key[j] >> 16) == id; ++j) sum = __fadd_rn(sum, sc[key[j] & 0xffffu]);
+        const bool pos = head && sum > 0.f;
+        const unsigned long long mask = __ballot(pos);
+        const int off = __popcll(mask & ((1ull << lane) - 1ull));
+        if (pos)
+            out[P + off] = ((unsigned long long)__builtin_bit_cast(uint32_t, sum) << 32) |
+                           (unsigned long long)(0xffffffffu - id);
+        P += __popcll(mask);
+    }
+    int S = 1;
+    while (S < P) S <<= 1;
+    for (int i = P + lane; i < S; i += 64) out[i] = 0ull;
+    fta_wave_sync();
+    for (int k = 2; k <= S; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int t = lane; t < (S >> 1); t += 64) {
+                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+                const unsigned long long a = out[i], b = out[i + j];
+                if ((a < b) == ((i & k) == 0)) {  // descending
+                    out[i] = b;
+                    out[i + j] = a;
+                }
+            }
+            fta_wave_sync();
+        }
+    }
+    const int keep = P < W ? P : W;
+    int32_t* oi = out_idx + slice * (int64_t)W;
+    float* os = out_scr ? out_scr + slice * (int64_t)W : nullptr;
+    for (int p = lane; p < W; p += 64) {
+        if (p < keep) {
+            const unsigned long long kv = out[p];
+            oi[p] = (int)(0xffffffffu - (uint32_t)(kv & 0xffffffffull));
+            if (os) os[p] = __builtin_bit_cast(float, (uint32_t)(kv >> 32));
+        } else {
+            oi[p] = -1;
+            if (os) os[p] = 0.f;
+        }
+    }
+    if (counts && lane == 0) counts[slice] = keep;
+}
+
+// ----------------------------------------------------------------------------
 // Reverse index (reference: flash_topk_attn_v2/sparse_attn_bwd.py:36-76,
 // csrc/build_reverse_indices_kernel.cu:6-104).
 // Membership bitmap sel[bh][m][qm/32] bit (qm%32) = q-block qm selected KV
@@ -374,6 +492,29 @@ int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint3
 }
 }  // namespace fta
 
+namespace fta {
+// One-wave-per-slice merge when g*K <= 4096 (LDS: 16 B per padded entry per
+// wave), the histogram kernel otherwise.
+int launch_qblock_merge(const int32_t* idx, const float* scr, int64_t num_slices, int g, int K, int Mt,
+                        const int32_t* max_id, int W, int32_t* out_idx, float* out_scr, int32_t* counts,
+                        hipStream_t st) {
+    const int64_t n = (int64_t)g * K;
+    if (n >= 1 && n <= kMergeWaveMax) {
+        int NP = 1;
+        while (NP < n) NP <<= 1;
+        const int wpb = (NP <= 1024) ? 4 : (NP <= 2048) ? 2 : 1;
+        const int64_t blocks = (num_slices + wpb - 1) / wpb;
+        hipLaunchKernelGGL(fta_qblock_merge_wave_kernel, dim3((unsigned)blocks), dim3(64 * wpb),
+                           (size_t)wpb * NP * 16, st, idx, scr, num_slices, g, K, NP, Mt, max_id, W, out_idx,
+                           out_scr, counts);
+        return check_launch("fta_qblock_merge_wave_kernel");
+    }
+    hipLaunchKernelGGL(fta_qblock_merge_kernel, dim3((unsigned)num_slices), dim3(256), 0, st, idx, scr, g, K, Mt,
+                       max_id, W, out_idx, out_scr, counts);
+    return check_launch("fta_qblock_merge_kernel");
+}
+}  // namespace fta
+
 extern "C" {
 
 int fta_qblock_merge(const int32_t* topk_indices, const float* topk_scores, int64_t num_slices, int q_block_size,
@@ -386,10 +527,9 @@ int fta_qblock_merge(const int32_t* topk_indices, const float* topk_scores, int6
     if (num_score_blocks > 4096) return fta::unsupported("num_score_blocks exceeds block sort limit 4096");
     if (qblock_topk <= 0) return fta::arg_error("qblock_topk must be positive");
     if (num_slices == 0) return FTA_OK;
-    hipLaunchKernelGGL(fta_qblock_merge_kernel, dim3((unsigned)num_slices), dim3(256), 0, (hipStream_t)stream,
-                       topk_indices, topk_scores, q_block_size, k_per_query, num_score_blocks, (const int32_t*)nullptr,
-                       qblock_topk, merged_indices, merged_scores, counts);
-    return fta::check_launch("fta_qblock_merge_kernel");
+    return fta::launch_qblock_merge(topk_indices, topk_scores, num_slices, q_block_size, k_per_query,
+                                    num_score_blocks, nullptr, qblock_topk, merged_indices, merged_scores, counts,
+                                    (hipStream_t)stream);
     FTA_TRY_END
 }
 
@@ -402,10 +542,9 @@ int fta_qblock_merge_maxid(const int32_t* topk_indices, const float* topk_scores
     if (max_index == nullptr) return fta::arg_error("qblock_merge: max_index is NULL");
     if (qblock_topk <= 0) return fta::arg_error("qblock_topk must be positive");
     if (num_slices == 0) return FTA_OK;
-    hipLaunchKernelGGL(fta_qblock_merge_kernel, dim3((unsigned)num_slices), dim3(256), 0, (hipStream_t)stream,
-                       topk_indices, topk_scores, q_block_size, k_per_query, 0, max_index, qblock_topk,
-                       merged_indices, merged_scores, counts);
-    return fta::check_launch("fta_qblock_merge_kernel");
+    return fta::launch_qblock_merge(topk_indices, topk_scores, num_slices, q_block_size, k_per_query, 0,
+                                    max_index, qblock_topk, merged_indices, merged_scores, counts,
+                                    (hipStream_t)stream);
     FTA_TRY_END
 }
 

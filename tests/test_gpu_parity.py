@@ -125,7 +125,8 @@ def test_topk_score_vs_float64_oracle(case):
 
 @pytest.mark.parametrize("g,K,Mt,W,pad", [(32, 16, 128, None, (0, 0)), (1, 16, 128, None, (0, 0)),
                                           (16, 8, 157, 128, (3, 13)), (32, 16, 512, 256, (0, 0)),
-                                          (4, 64, 4096, 300, (1, 3))])
+                                          (4, 64, 4096, 300, (1, 3)),
+                                          (64, 80, 700, 512, (5, 9))])  # g*K > 4096: histogram kernel
 @pytest.mark.parametrize("with_scores", [False, True])
 def test_merge_bit_exact(g, K, Mt, W, pad, with_scores):
     say(f"[merge] g={g} K={K} Mt={Mt} W={W} pad={pad} scores={with_scores}")
