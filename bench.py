@@ -55,31 +55,39 @@ def make_inputs(B, N, H, D, peaked, seed, dev):
     return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
 
 
-def cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, rows):
-    """Numpy oracle (oracle/fta_oracle.py) on head 0, first `rows` queries."""
+def cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, rows, heads):
+    """Numpy oracle (oracle/fta_oracle.py) on heads 0 .. heads-1, first `rows` queries of each."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import fta_oracle as O
 
     N = q.shape[1]
-    f = lambda t: t[:, :, :D].float().cpu().numpy()  # head 0
-    qn, kn, vn, dn = f(q), f(k), f(v), f(do)
-    t0 = time.perf_counter()
-    sc = O.block_score(qn, kn, 1, b, rows=np.arange(rows))
-    idx, raw, avg = O.topk_select(sc.astype(np.float32), thr, topk, b)
-    merged, counts, _ = O.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
-    qbl = [(0, 0, qm) for qm in range(rows // g)]
-    full = np.full((1, 1, N // g, W), -1, dtype=np.int32)
-    full[:, :, : rows // g] = merged
-    O.sparse_attn(qn, kn, vn, full, 1, g, b, None, qblocks=qbl)
-    O.sparse_attn_bwd(qn, kn, vn, dn, full, 1, g, b, None, qblocks=qbl)
-    secs = time.perf_counter() - t0
-    P = g * b * int(counts.sum())
-    flops = 2.0 * rows * N * D + 14.0 * D * P
-    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": os.cpu_count(), "kind": "port",
+    secs, flops = 0.0, 0.0
+    for h in range(heads):
+        f = lambda t: t[:, :, h * D:(h + 1) * D].float().cpu().numpy()
+        qn, kn, vn, dn = f(q), f(k), f(v), f(do)
+        t0 = time.perf_counter()
+        sc = O.block_score(qn, kn, 1, b, rows=np.arange(rows))
+        idx, raw, avg = O.topk_select(sc.astype(np.float32), thr, topk, b)
+        merged, counts, _ = O.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
+        qbl = [(0, 0, qm) for qm in range(rows // g)]
+        full = np.full((1, 1, N // g, W), -1, dtype=np.int32)
+        full[:, :, : rows // g] = merged
+        O.sparse_attn(qn, kn, vn, full, 1, g, b, None, qblocks=qbl)
+        O.sparse_attn_bwd(qn, kn, vn, dn, full, 1, g, b, None, qblocks=qbl)
+        secs += time.perf_counter() - t0
+        P = g * b * int(counts.sum())
+        flops += 2.0 * rows * N * D + 14.0 * D * P
+    try:  # threads of numpy's BLAS pool (the only multi-threaded part of the oracle)
+        import threadpoolctl
+
+        cores = max(int(i.get("num_threads", 1)) for i in threadpoolctl.threadpool_info()) or 1
+    except Exception:
+        cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "seconds": secs,
-            "sample": f"numpy oracle, 1 head x {rows} queries of the C3 workload "
+            "sample": f"numpy oracle, {heads} head(s) x {rows} queries of the C3 workload "
                       f"(score+select+merge+fwd+bwd), float64 BLAS"}
 
 
@@ -134,7 +142,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-iid", action="store_true")
     ap.add_argument("--no-v1", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=8192)
+    ap.add_argument("--cpu-rows", type=int, default=32768)
+    ap.add_argument("--cpu-heads", type=int, default=2)
     ap.add_argument("--only", choices=["score", "topk", "merge", "fwd", "bwd", "copy"], default=None,
                     help="profiling aid: run one stage of the C3 step --steps times and exit")
     ap.add_argument("--iid", action="store_true",
@@ -313,7 +322,7 @@ def main():
         out["v1_score"] = bench_v1(dev, stream)
 
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, args.cpu_rows)
+        out["cpu_baseline"] = cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, args.cpu_rows, args.cpu_heads)
 
     print(json.dumps(out), flush=True)
 
