@@ -144,7 +144,7 @@ def main():
     ap.add_argument("--no-v1", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=32768)
     ap.add_argument("--cpu-heads", type=int, default=2)
-    ap.add_argument("--only", choices=["score", "topk", "merge", "fwd", "bwd", "copy"], default=None,
+    ap.add_argument("--only", choices=["score", "topk", "merge", "fwd", "bwd", "copy", "v1"], default=None,
                     help="profiling aid: run one stage of the C3 step --steps times and exit")
     ap.add_argument("--iid", action="store_true",
                     help="with --only: the C3-iid variant (iid q/k/v, threshold 1.0, qblock_topk 512)")
@@ -160,6 +160,12 @@ def main():
     from flash_topk_attn_v2 import _lib
 
     dev = torch.device("cuda:0")
+    if args.only == "v1":  # the V1 benchmark rows alone (profiling aid)
+        for _ in range(args.steps):
+            bench_v1(dev, torch.cuda.current_stream(dev))
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "v1", "steps": args.steps}), flush=True)
+        return
     B, N, H, D, b, topk, thr, g, W = 1, 32768, 32, 128, 64, 16, 0.9, 32, 256
     q, k, v = make_inputs(B, N, H, D, True, 2, dev)
     gd = torch.Generator(device=dev).manual_seed(7)
