@@ -694,10 +694,15 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
 
         float e0[2], e1[2];
         const int kb = m * 64 - pad_head;
-        if (kb >= 0 && kb + 64 <= N && m + 1 < M) {
-            // interior block: no masking, so both stages are branch-free regions
-            // stage A: MFMAs of half 1 of block m, exps of half 0
+        if (m + 1 < M) {
+            // Every block but the last runs the same two stages; a block at a
+            // sequence edge first masks its scores in place (uniform branches),
+            // so the loop-carried accumulators have one definition and keep
+            // their registers.  Masked scores are -inf: their exps are 0.
+            const bool edge = kb < 0 || kb + 64 > N;
+            if (edge) edge_mask(m, 0, h0);
             stage(m, 1, h1, h0, e0);      // MFMAs of half 1 of block m, exps of half 0
+            if (edge) edge_mask(m, 1, h1);
             stage(m + 1, 0, h0, h1, e1);  // MFMAs of half 0 of block m + 1, exps of half 1
         } else {
             edge_mask(m, 0, h0);
