@@ -919,14 +919,16 @@ __device__ __forceinline__ void fta_topk_flush(float (&lv)[KB], int (&li)[KB], i
 }
 
 template <int KB, int MODE>
-__global__ __launch_bounds__(256) void fta_topk_select_kernel(
+// Lists of <= 16 entries fit 4 waves per SIMD (<= 128 VGPRs), which keeps more
+// of the scan's loads in flight; longer lists need the full register file.
+__global__ __launch_bounds__(256, (KB <= 16) ? 4 : 1) void fta_topk_select_kernel(
     const float* __restrict__ in, int64_t stride_row, int64_t stride_m, const float* __restrict__ row_lse,
     int N, int rows, int M, int m_out, int bsz, int pad_head, int pad_tail, float threshold,
     int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg,
     const int32_t* __restrict__ tau_idx) {
-    constexpr int LDB = 32;             // blocks loaded per batch
+    constexpr int LDB = 24;             // blocks loaded per batch
     constexpr int UNR = 8;              // blocks tested between candidate-list checks
-    constexpr int CAP = 16 + UNR;       // a sub-batch starts with at most CAP - UNR parked candidates
+    constexpr int CAP = 12 + UNR;       // a sub-batch starts with at most CAP - UNR parked candidates
     __shared__ __align__(16) float cand_v[4][CAP][64];
     __shared__ int cand_i[4][CAP][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
