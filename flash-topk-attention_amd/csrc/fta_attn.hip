@@ -49,6 +49,7 @@ struct AttnArgs {
     int64_t o1_sb, o1_sh, o1_sn;
     float* lse;             // forward output, natural log, [BH][N]
     const float* lse_in;    // backward input
+    const float* lse2_in;   // lse_in * log2(e), [BH][N] (workspace; dK/dV split kernel)
     const float* delta_in;  // backward input
     int H, N, Dreal, g, kvb, q_pad, kv_pad, Mkv, NC;
     int Hk, G;  // K/V heads and query heads per K/V head (G = H / Hk; 1 without GQA)
@@ -1512,7 +1513,7 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
         const int bh = b * a.H + h;
         qp = a.q + b * a.q_sb + h * a.q_sh;
         dp = a.dout + b * a.d_sb + h * a.d_sh;
-        lsep = a.lse_in + (int64_t)bh * a.N;
+        lsep = a.lse2_in + (int64_t)bh * a.N;  // log2 units: no per-element scaling
         dlp = a.delta_in + (int64_t)bh * a.N;
         l_base = l_isd ? dlp : lsep;
         if (gq > 0) {
@@ -1580,13 +1581,19 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
                     for (int ks = 0; ks < KS; ++ks)
                         own = E::mma(*reinterpret_cast<const uint4*>(ab + SW::off(lane & 31, 2 * ks + hf)), kv[ks], own);
                     if (hv == 0) {
+                        if (mk == 0xffffffffu && __ballot(!kok) == 0ull) {
+                            // every row of the chunk selected, every key valid: no mask
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            const int r = c_row(i, lane);
-                            // a selected row with a valid key has a finite lse
-                            const bool ok = kok && ((mk >> r) & 1u);
-                            const float ex = fta_exp2(fmaf(own[i], a.c, -ld[r] * 1.4426950408889634f));
-                            own[i] = ok ? ex : 0.f;
+                            for (int i = 0; i < 16; ++i) own[i] = fta_exp2(fmaf(own[i], a.c, -ld[c_row(i, lane)]));
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 16; ++i) {
+                                const int r = c_row(i, lane);
+                                // a selected row with a valid key has a finite lse
+                                const bool ok = kok && ((mk >> r) & 1u);
+                                const float ex = fta_exp2(fmaf(own[i], a.c, -ld[r]));
+                                own[i] = ok ? ex : 0.f;
+                            }
                         }
                     }
 #pragma unroll
@@ -1646,6 +1653,14 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
             }
         }
     }
+}
+
+
+// lse2 = lse * log2(e) (the same fp32 product the kernels formed per element)
+__global__ __launch_bounds__(256) void fta_lse2_kernel(const float* __restrict__ lse, float* __restrict__ lse2,
+                                                       int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) lse2[i] = lse[i] * 1.4426950408889634f;
 }
 
 // ----------------------------------------------------------------------------
@@ -1824,6 +1839,11 @@ size_t sel_bytes(int B, int H, const Geo& G) {
     return fta::align_up((size_t)B * H * G.Mkv * ((G.QM + 31) / 32) * sizeof(uint32_t));
 }
 
+// the backward workspace: membership bitmap, then lse in log2 units
+size_t bwd_bytes(int B, int H, int N, const Geo& G) {
+    return sel_bytes(B, H, G) + fta::align_up((size_t)B * H * N * sizeof(float));
+}
+
 }  // namespace
 
 extern "C" {
@@ -1895,7 +1915,7 @@ size_t fta_sparse_attn_bwd_workspace_size(int B, int H, int N, int D, int q_bloc
     if (geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
                  &G) != FTA_OK)
         return 0;
-    return sel_bytes(B, H, G);  // membership bitmap KV block -> q-blocks
+    return bwd_bytes(B, H, N, G);  // membership bitmap KV block -> q-blocks, lse in log2 units
 }
 
 int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -1914,10 +1934,14 @@ int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void*
     if (rc != FTA_OK) return rc;
     if (W <= 0) return fta::arg_error("sparse_attn_bwd: qblock_topk must be positive");
     if (G.Mkv > 0x3fffffff / 32) return fta::unsupported("sparse_attn_bwd: too many KV blocks");
-    if (workspace_bytes < sel_bytes(B, H, G)) return fta::arg_error("sparse_attn_bwd: workspace too small");
+    if (workspace_bytes < bwd_bytes(B, H, N, G)) return fta::arg_error("sparse_attn_bwd: workspace too small");
     hipStream_t st = (hipStream_t)stream;
     uint32_t* sel = (uint32_t*)workspace;
     if ((rc = fta::launch_sel_bitmap(merged_indices, B * H, QM, W, G.Mkv, sel, st)) != FTA_OK) return rc;
+    float* lse2 = (float*)((char*)workspace + sel_bytes(B, H, G));
+    const int64_t nl = (int64_t)B * H * N;
+    hipLaunchKernelGGL(fta_lse2_kernel, dim3((unsigned)((nl + 255) / 256)), dim3(256), 0, st, lse, lse2, nl);
+    if ((rc = fta::check_launch("fta_lse2_kernel")) != FTA_OK) return rc;
 
     AttnArgs a = {};
     a.q = (const uint16_t*)q;
@@ -1940,6 +1964,7 @@ int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void*
     a.sel = sel;
     a.W = W;
     a.lse_in = lse;
+    a.lse2_in = lse2;
     a.delta_in = delta;
     fill_common(a, H, N, D, q_block_size, kv_block_size, q_pad_head, kv_pad_head, scale, G);
     a.Hk = Hk;
