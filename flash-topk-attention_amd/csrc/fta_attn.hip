@@ -920,12 +920,23 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
                         dpv[sb] = E::mma(*reinterpret_cast<const uint4*>(vbase + off), df[ks], dpv[sb]);
                     }
                 }
-                // valid keys [klo, khi) relative to kb; a lane whose query column
-                // is not selected gets the empty range (branch-free masking)
+                // A lane whose query column is not selected uses an infinite lse:
+                // all its exps are exactly 0.  Keys outside [klo, khi) (chunks at
+                // a sequence end, or past a short block) get -inf scores in place
+                // under a wave-uniform branch; every other chunk is unmasked.
                 const bool colok = rowlive && ((mk >> (lane & 31)) & 1u);
-                const int klo = colok ? max(0, -kb) : 64;
-                const int khi = colok ? min(min(rem, 64), a.N - kb) : 0;
-                const unsigned kw = (unsigned)max(khi - klo, 0);  // a chunk past N has khi < klo
+                const float lse_c = colok ? lse2 : FTA_INF;
+                const int klo = max(0, -kb), khi = min(min(rem, 64), a.N - kb);
+                if (klo > 0 || khi < 64) {
+                    const unsigned kw = (unsigned)max(khi - klo, 0);  // a chunk past N has khi < klo
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            const int rel = sb * 32 + c_row(i, lane);
+                            s[sb][i] = ((unsigned)(rel - klo) < kw) ? s[sb][i] : -FTA_INF;
+                        }
+                }
                 uint4 dsf[4];
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
@@ -933,10 +944,7 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int sb = ks >> 1, i = 8 * (ks & 1) + e;
-                        const int rel = sb * 32 + c_row(i, lane);
-                        const bool ok = (unsigned)(rel - klo) < kw;
-                        const float ex = fta_exp2(fmaf(s[sb][i], a.c, -lse2));
-                        const float p = ok ? ex : 0.f;
+                        const float p = fta_exp2(fmaf(s[sb][i], a.c, -lse_c));
                         dsv[e] = p * (dpv[sb][i] - dl);
                     }
                     dsf[ks] = make_uint4(E::pack2(dsv[0], dsv[1]), E::pack2(dsv[2], dsv[3]),
