@@ -506,25 +506,29 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
                     s[0] = E::mma(a0, qf[ks], s[0]);
                     s[1] = E::mma(a1, qf[ks], s[1]);
                 }
-                // valid keys of the chunk: [klo, khi) relative to kb (wave-uniform)
+                // valid keys of the chunk: [klo, khi) relative to kb (wave-uniform).
+                // Keys outside it get -inf scores in place (chunks at a sequence end
+                // or past a short block only).  A lane whose query column is not
+                // selected keeps its scores but takes no part: its chunk maximum is
+                // -inf and its exps use an infinite offset (exactly 0).
                 const int klo = max(0, -kb), khi = min(min(rem, 64), a.N - kb);
-                if (klo > 0 || khi < 64 || mk != 0xffffffffu) {
-                    // branch-free: one compare pair per element, the column bit per lane
-                    const bool colok = (mk >> (lane & 31)) & 1u;
-                    const int lo = colok ? klo : 64, hi = colok ? max(khi, klo) : 64;  // empty if past N
+                if (klo > 0 || khi < 64) {
+                    const unsigned kw = (unsigned)max(khi - klo, 0);  // a chunk past N has khi < klo
 #pragma unroll
                     for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
                         for (int i = 0; i < 16; ++i) {
                             const int rel = sb * 32 + c_row(i, lane);
-                            s[sb][i] = ((unsigned)(rel - lo) < (unsigned)(hi - lo)) ? s[sb][i] : -FTA_INF;
+                            s[sb][i] = ((unsigned)(rel - klo) < kw) ? s[sb][i] : -FTA_INF;
                         }
                 }
+                const bool colok = (mk >> (lane & 31)) & 1u;
                 float mx = s[0][0];
 #pragma unroll
                 for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
                     for (int i = (sb == 0); i < 16; ++i) mx = fmaxf(mx, s[sb][i]);
+                mx = colok ? mx : -FTA_INF;
                 mx = fmaxf(mx, fta_xor32(mx));
                 const float mn = fmaxf(m_run, mx);
                 const bool grow = (mn - m_run) * a.c > 8.f;
@@ -537,7 +541,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
                     l_run *= alpha;
                     if (grow) m_run = mn;
                 }
-                const float mc = (m_run == -FTA_INF) ? 0.f : m_run * a.c;
+                const float mc = !colok ? FTA_INF : (m_run == -FTA_INF) ? 0.f : m_run * a.c;
                 float ls = 0.f;
                 uint4 pf[4];
 #pragma unroll
