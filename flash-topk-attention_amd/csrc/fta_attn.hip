@@ -376,6 +376,27 @@ struct FwdPipeShape {
     static_assert(NST * STAGE_B + NW * kSeg * 4 + kSeg * 4 <= 150 * 1024, "LDS budget");
 };
 
+// Empty asm with every fragment as a read-write VGPR operand: all loads into
+// `f` complete before it, and none can be moved below it.
+typedef unsigned int fta_u32x4v __attribute__((ext_vector_type(4)));
+template <int KS>
+__device__ __forceinline__ void fta_pin_frags(uint4 (&f)[2][KS]) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int k = 0; k < KS; k += 4) {
+            fta_u32x4v x0 = __builtin_bit_cast(fta_u32x4v, f[h][k]);
+            fta_u32x4v x1 = __builtin_bit_cast(fta_u32x4v, f[h][(k + 1) % KS]);
+            fta_u32x4v x2 = __builtin_bit_cast(fta_u32x4v, f[h][(k + 2) % KS]);
+            fta_u32x4v x3 = __builtin_bit_cast(fta_u32x4v, f[h][(k + 3) % KS]);
+            asm volatile("" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
+            f[h][k] = __builtin_bit_cast(uint4, x0);
+            if (k + 1 < KS) f[h][k + 1] = __builtin_bit_cast(uint4, x1);
+            if (k + 2 < KS) f[h][k + 2] = __builtin_bit_cast(uint4, x2);
+            if (k + 3 < KS) f[h][k + 3] = __builtin_bit_cast(uint4, x3);
+        }
+}
+
 template <int DT, int D, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArgs a) {
     using E = Elem<DT>;
@@ -499,12 +520,21 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
                 for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
                     for (int i = 0; i < 16; ++i) s[sb][i] = 0.f;
+                // all K fragments of the chunk first, then the MFMAs: one LDS
+                // latency per chunk instead of one per MFMA
+                uint4 ka[2][KS];
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
-                    const uint4 a0 = *reinterpret_cast<const uint4*>(kbase + SW::off(lane & 31, 2 * ks + hf));
-                    const uint4 a1 = *reinterpret_cast<const uint4*>(kbase + SW::off(32 + (lane & 31), 2 * ks + hf));
-                    s[0] = E::mma(a0, qf[ks], s[0]);
-                    s[1] = E::mma(a1, qf[ks], s[1]);
+                    ka[0][ks] = *reinterpret_cast<const uint4*>(kbase + SW::off(lane & 31, 2 * ks + hf));
+                    ka[1][ks] = *reinterpret_cast<const uint4*>(kbase + SW::off(32 + (lane & 31), 2 * ks + hf));
+                }
+                // the empty asm takes every fragment as an operand, so the loads
+                // cannot sink to their MFMAs (which exposes one LDS latency per MFMA)
+                fta_pin_frags<KS>(ka);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    s[0] = E::mma(ka[0][ks], qf[ks], s[0]);
+                    s[1] = E::mma(ka[1][ks], qf[ks], s[1]);
                 }
                 // valid keys of the chunk: [klo, khi) relative to kb (wave-uniform).
                 // Keys outside it get -inf scores in place (chunks at a sequence end
