@@ -273,19 +273,33 @@ __global__ __launch_bounds__(256) void fta_qblock_merge_wave_kernel(
 // block m.  Bit-OR is order independent, so the lists derived from it (q-block
 // ids ascending) are deterministic.
 // ----------------------------------------------------------------------------
-__global__ void fta_fill_u32_kernel(uint32_t* __restrict__ p, int64_t n, uint32_t v) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-        p[i] = v;
-}
 
-__global__ void fta_sel_bitmap_kernel(const int32_t* __restrict__ merged, int QM, int W, int M, int QW,
-                                      uint32_t* __restrict__ sel) {
-    const int64_t slice = blockIdx.x;  // bh * QM + qm
-    const int64_t bh = slice / QM;
-    const int qm = (int)(slice - bh * QM);
-    for (int s = threadIdx.x; s < W; s += blockDim.x) {
-        const int m = merged[slice * W + s];
-        if (m >= 0 && m < M) atomicOr(&sel[(bh * M + m) * QW + (qm >> 5)], 1u << (qm & 31));
+// Membership bitmap sel[bh][m][qw]: bit (qm & 31) of word qw = qm / 32 is set
+// when q-block qm's merged list holds KV block m.  One workgroup per (bh, qw)
+// builds that word column for every m in LDS (atomicOr there), a chunk of
+// kSelChunk blocks at a time, and writes every word: no global atomics and no
+// separate clearing pass.
+constexpr int kSelChunk = 8192;
+
+__global__ __launch_bounds__(256) void fta_sel_bitmap_kernel(const int32_t* __restrict__ merged, int QM, int W,
+                                                             int M, int QW, uint32_t* __restrict__ sel) {
+    __shared__ uint32_t bits[kSelChunk];
+    const int64_t bh = blockIdx.x / QW;
+    const int qw = (int)(blockIdx.x - bh * QW);
+    const int q0 = qw * 32, nq = min(32, QM - q0);
+    const int32_t* mp = merged + (bh * QM + q0) * (int64_t)W;
+    for (int m0 = 0; m0 < M; m0 += kSelChunk) {
+        const int mn = min(kSelChunk, M - m0);
+        for (int i = threadIdx.x; i < mn; i += 256) bits[i] = 0u;
+        __syncthreads();
+        for (int qq = 0; qq < nq; ++qq)
+            for (int e = threadIdx.x; e < W; e += 256) {
+                const int m = mp[(int64_t)qq * W + e] - m0;
+                if (m >= 0 && m < mn) atomicOr(&bits[m], 1u << qq);
+            }
+        __syncthreads();
+        for (int i = threadIdx.x; i < mn; i += 256) sel[(bh * M + m0 + i) * QW + qw] = bits[i];
+        __syncthreads();
     }
 }
 
@@ -473,21 +487,12 @@ __global__ __launch_bounds__(256) void fta_qblock_union_kernel(const int32_t* __
 }
 
 namespace fta {
-int launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t st) {
-    if (n <= 0) return FTA_OK;
-    int64_t blocks = (n + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(fta_fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, st, p, n, v);
-    return check_launch("fta_fill_u32_kernel");
-}
 
 int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint32_t* sel, hipStream_t st) {
     const int QW = (QM + 31) / 32;
-    int rc = launch_fill_u32(sel, (int64_t)BH * M * QW, 0u, st);
-    if (rc != FTA_OK) return rc;
-    if ((int64_t)BH * QM > 0)
-        hipLaunchKernelGGL(fta_sel_bitmap_kernel, dim3((unsigned)((int64_t)BH * QM)), dim3(128), 0, st, merged, QM,
-                           W, M, QW, sel);
+    if ((int64_t)BH * QW == 0 || M <= 0) return FTA_OK;
+    hipLaunchKernelGGL(fta_sel_bitmap_kernel, dim3((unsigned)((int64_t)BH * QW)), dim3(256), 0, st, merged, QM, W,
+                       M, QW, sel);
     return check_launch("fta_sel_bitmap_kernel");
 }
 }  // namespace fta

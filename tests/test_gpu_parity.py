@@ -166,6 +166,7 @@ def test_merge_device_max_edge_cases():
 
 ATTN_CASES = [
     # B, N, H, D, g, b, qpad, kvpad, W, dtype
+    (1, 131100, 1, 32, 32, 16, (0, 4), (0, 4), 16, torch.bfloat16),  # 8194 KV blocks: two bitmap chunks
     (1, 1024, 2, 64, 32, 64, (0, 0), (0, 0), 12, torch.float16),
     (1, 1024, 2, 128, 32, 64, (0, 0), (0, 0), 20, torch.bfloat16),
     (2, 1000, 2, 64, 16, 64, (4, 4), (12, 12), 10, torch.bfloat16),
