@@ -167,6 +167,93 @@ __device__ __forceinline__ void fta_wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Bitonic sort of arr[0, n) (n a power of two <= 64 * E) held in registers: lane
+// l holds elements l*E .. l*E+E-1 (past n: `pad`, which sorts last).  Strides
+// below E swap within a lane, larger ones exchange with lane l ^ (stride / E).
+// Ascending, or descending with DESC.  The result is written back to arr.
+template <typename K>
+__device__ __forceinline__ K fta_shfl_xor_k(K v, int d) {
+    if constexpr (sizeof(K) == 8) {
+        const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+        return ((K)(uint32_t)__shfl_xor((int)hi, d, 64) << 32) | (K)(uint32_t)__shfl_xor((int)lo, d, 64);
+    } else {
+        return (K)__shfl_xor((int)v, d, 64);
+    }
+}
+
+template <int E, typename K, bool DESC>
+__device__ __forceinline__ void fta_wave_sort_regs(K* arr, int n, K pad, int lane) {
+    constexpr int NN = 64 * E;
+    K v[E];
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+        const int i = lane * E + r;
+        v[r] = (i < n) ? arr[i] : pad;
+    }
+#pragma unroll
+    for (int k = 2; k <= NN; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            if (j < E) {
+#pragma unroll
+                for (int r = 0; r < E; ++r) {
+                    if ((r & j) == 0) {
+                        const bool up = (((lane * E + r) & k) == 0) != DESC;
+                        const K a = v[r], b = v[r | j];
+                        const bool sw = up ? (a > b) : (a < b);
+                        v[r] = sw ? b : a;
+                        v[r | j] = sw ? a : b;
+                    }
+                }
+            } else {
+                const int d = j / E;
+                const bool lower = (lane & d) == 0;
+#pragma unroll
+                for (int r = 0; r < E; ++r) {
+                    const K p = fta_shfl_xor_k(v[r], d);
+                    const bool up = (((lane * E + r) & k) == 0) != DESC;
+                    v[r] = (lower == up) ? (v[r] < p ? v[r] : p) : (v[r] > p ? v[r] : p);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+        const int i = lane * E + r;
+        if (i < n) arr[i] = v[r];
+    }
+}
+
+// Sort arr[0, n) (n a power of two) across one wave: in registers up to 512
+// elements, else bitonic in LDS.
+template <typename K, bool DESC>
+__device__ __forceinline__ void fta_wave_sort(K* arr, int n, K pad, int lane) {
+    if (n <= 64) {
+        fta_wave_sort_regs<1, K, DESC>(arr, n, pad, lane);
+    } else if (n <= 128) {
+        fta_wave_sort_regs<2, K, DESC>(arr, n, pad, lane);
+    } else if (n <= 256) {
+        fta_wave_sort_regs<4, K, DESC>(arr, n, pad, lane);
+    } else if (n <= 512) {
+        fta_wave_sort_regs<8, K, DESC>(arr, n, pad, lane);
+    } else {
+        for (int k = 2; k <= n; k <<= 1) {
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                for (int t = lane; t < (n >> 1); t += 64) {
+                    const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+                    const K a = arr[i], b = arr[i + j];
+                    if ((DESC ? (a < b) : (a > b)) == ((i & k) == 0)) {
+                        arr[i] = b;
+                        arr[i + j] = a;
+                    }
+                }
+                fta_wave_sync();
+            }
+        }
+    }
+    fta_wave_sync();
+}
+
 __global__ __launch_bounds__(256) void fta_qblock_merge_wave_kernel(
     const int32_t* __restrict__ idx, const float* __restrict__ scr, int64_t num_slices, int g, int K, int NP,
     int Mt_arg, const int32_t* __restrict__ max_id, int W, int32_t* __restrict__ out_idx,
@@ -203,19 +290,7 @@ __global__ __launch_bounds__(256) void fta_qblock_merge_wave_kernel(
     while (NS < NV) NS <<= 1;
     for (int i = NV + lane; i < NS; i += 64) key[i] = 0xffffffffu;
     fta_wave_sync();
-    for (int k = 2; k <= NS; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int t = lane; t < (NS >> 1); t += 64) {
-                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
-                const uint32_t a = key[i], b = key[i + j];
-                if ((a > b) == ((i & k) == 0)) {
-                    key[i] = b;
-                    key[i + j] = a;
-                }
-            }
-            fta_wave_sync();
-        }
-    }
+    fta_wave_sort<uint32_t, false>(key, NS, 0xffffffffu, lane);
     int P = 0;
     for (int r0 = 0; r0 < NV; r0 += 64) {
         const int i = r0 + lane;
@@ -237,19 +312,7 @@ __global__ __launch_bounds__(256) void fta_qblock_merge_wave_kernel(
     while (S < P) S <<= 1;
     for (int i = P + lane; i < S; i += 64) out[i] = 0ull;
     fta_wave_sync();
-    for (int k = 2; k <= S; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int t = lane; t < (S >> 1); t += 64) {
-                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
-                const unsigned long long a = out[i], b = out[i + j];
-                if ((a < b) == ((i & k) == 0)) {  // descending
-                    out[i] = b;
-                    out[i + j] = a;
-                }
-            }
-            fta_wave_sync();
-        }
-    }
+    fta_wave_sort<unsigned long long, true>(out, S, 0ull, lane);  // descending
     const int keep = P < W ? P : W;
     int32_t* oi = out_idx + slice * (int64_t)W;
     float* os = out_scr ? out_scr + slice * (int64_t)W : nullptr;
