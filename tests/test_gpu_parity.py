@@ -207,6 +207,25 @@ def _random_merged(B, H, QM, W, M, seed, empty_frac=0.1):
     return merged
 
 
+def _drawn_attn_case(seed):
+    """A seeded random geometry: head dim, q / KV block sizes, virtual paddings
+    at both ends, list width and dtype (the oracle finishes in seconds)."""
+    r = np.random.default_rng(1000 + seed)
+    D = int(r.choice([32, 64, 96, 128]))
+    g = int(r.choice([1, 8, 16, 24, 32, 48, 64]))
+    b = int(r.choice([16, 32, 48, 64, 96, 128]))
+    N = int(r.integers(200, 1500))
+    H = int(r.integers(1, 4))
+    qph = int(r.integers(0, g))
+    kph = int(r.integers(0, b))
+    W = int(r.integers(1, 24))
+    dt = [torch.bfloat16, torch.float16][int(r.integers(0, 2))]
+    return (1, N, H, D, g, b, (qph, (-(qph + N)) % g), (kph, (-(kph + N)) % b), W, dt)
+
+
+ATTN_CASES += [_drawn_attn_case(s) for s in range(8)]
+
+
 def _attn_inputs(case, seed):
     B, N, H, D, g, b, qpad, kvpad, W, dt = case
     QM = (qpad[0] + N + qpad[1]) // g
