@@ -106,6 +106,43 @@ def test_topk_select_wide_k_bit_exact(case):
         np.testing.assert_array_equal(got[2].cpu().numpy(), ra)
 
 
+def _drawn_score_case(seed):
+    """A seeded random scoring geometry with a threshold and top-k."""
+    r = np.random.default_rng(2000 + seed)
+    D = int(r.choice([32, 40, 64, 96, 128, 160]))
+    b = int(r.choice([16, 32, 48, 64, 96, 128]))
+    N = int(r.integers(100, 1300))
+    H = int(r.integers(1, 4))
+    ph = int(r.integers(0, b))
+    pt = (-(ph + N)) % b
+    dt = [torch.bfloat16, torch.float16][int(r.integers(0, 2))]
+    layout = ["bnc", "bhnd"][int(r.integers(0, 2))]
+    M = (ph + N + pt) // b
+    topk = int(r.integers(0, min(M, 64) + 1))
+    thr = float(r.choice([0.5, 0.9, 1.0]))
+    return (1, N, H, D, b, (ph, pt), dt, layout), thr, topk
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_drawn_scoring_geometries(seed):
+    case, thr, topk = _drawn_score_case(seed)
+    B, N, H, D, b, pad, dt, layout = case
+    say(f"[score drawn] {case} thr={thr} topk={topk}")
+    q, k = _qk(case, 50 + seed)
+    scores = fta.flash_block_score(q, k, H, b, pad)
+    idx, raw, avg = fta.flash_topk_select(scores, thr, topk, b, pad)
+    fi, fr, fa = fta.flash_topk_score(q, k, H, b, topk, pad, thr)
+    torch.cuda.synchronize()
+    qn, kn = _oracle_inputs(q, k)
+    ref = O.block_score(qn, kn, H, b, pad)
+    np.testing.assert_allclose(scores.cpu().numpy(), ref, rtol=2e-4, atol=2e-7)
+    ri, rr, ra = O.topk_select(scores.cpu().numpy(), thr, topk, b, pad)
+    for got in ((idx, raw, avg), (fi, fr, fa)):
+        np.testing.assert_array_equal(got[0].cpu().numpy(), ri)
+        np.testing.assert_array_equal(got[1].cpu().numpy(), rr)
+        np.testing.assert_array_equal(got[2].cpu().numpy(), ra)
+
+
 @pytest.mark.parametrize("case", SCORE_CASES[:4], ids=lambda c: f"N{c[1]}D{c[3]}b{c[4]}")
 def test_topk_score_vs_float64_oracle(case):
     B, N, H, D, b, pad, dt, layout = case
