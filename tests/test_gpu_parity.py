@@ -87,6 +87,7 @@ WIDE_K_CASES = [
     (1, 2048, 2, 64, 32, (0, 0), torch.bfloat16, "bnc", 1.0, 32),
     (1, 4096, 2, 64, 32, (0, 0), torch.float16, "bnc", 0.95, 48),
     (1, 4072, 1, 128, 64, (24, 0), torch.bfloat16, "bnc", 2.0, 64),
+    (1, 4096, 1, 64, 32, (0, 0), torch.bfloat16, "bnc", 0.95, 100),  # m_out > 64: sort selector
 ]
 
 
