@@ -99,7 +99,8 @@ V1_ROWS = [(1, 32768, 4, 64, 64, 112.299, 18.524, 136), (1, 8192, 8, 128, 16, 3.
 
 def bench_v1(dev, stream):
     """V1 flash_topk_score (dense o + top-k block scores) forward, and forward
-    + backward through o, at two rows of the reference's V1 benchmark."""
+    + backward through o, at two rows of the reference's V1 benchmark, and the
+    exact q-block union of the forward's top-k indices."""
     import torch
 
     import flash_topk_attn as v1
@@ -114,7 +115,7 @@ def bench_v1(dev, stream):
             e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
             e[0].record(stream)
             with torch.no_grad():
-                v1.flash_topk_score(q, k, v, H, b, topk)
+                _, idx, _ = v1.flash_topk_score(q, k, v, H, b, topk)
             e[1].record(stream)
             ql, kl, vl = (t.detach().requires_grad_(True) for t in (q, k, v))
             o, _, _ = v1.flash_topk_score(ql, kl, vl, H, b, topk)
@@ -125,12 +126,23 @@ def bench_v1(dev, stream):
                 fw.append(e[0].elapsed_time(e[1]))
                 fb.append(e[1].elapsed_time(e[2]))
         fms, fbms = sorted(fw)[1], sorted(fb)[1]
+        # exact q-block union of those indices (q_block_size 32)
+        ut = []
+        for it in range(4):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            e[0].record(stream)
+            v1.build_qblock_topk_indices(idx, 32)
+            e[1].record(stream)
+            torch.cuda.synchronize()
+            if it:
+                ut.append(e[0].elapsed_time(e[1]))
         f_fwd = 2.0 * B * H * N * N * D + 4.0 * B * H * N * N * D  # scoring QK^T + dense attention
         res.append({"config": f"B{B} N{N} H{H} D{D} b{b} topk{topk} bf16", "fwd_ms": round(fms, 3),
                     "fwd_tflops": round(f_fwd / fms / 1e9, 1), "fwd_bwd_ms": round(fbms, 3),
+                    "union_g32_ms": round(sorted(ut)[1], 3),
                     "reference_published_ms_other_hw": ref_ms,
                     "reference_fa2_ms_other_hw": fa2_ms, "reference_source": f"BENCHMARK.md:{line}"})
-        del q, k, v, do, ql, kl, vl, o
+        del q, k, v, do, ql, kl, vl, o, idx
     return res
 
 

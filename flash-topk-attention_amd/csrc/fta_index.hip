@@ -484,69 +484,52 @@ __global__ __launch_bounds__(256) void fta_delta_kernel(const uint16_t* __restri
 
 // ----------------------------------------------------------------------------
 // q-block union (reference V1: flash_topk_attn/attention.py:23-138).  One
-// workgroup per (b, h, q-block): the g*K ids of the block's query rows (rows
+// wave per (b, h, q-block): the g*K ids of the block's query rows (rows
 // outside [0, N) under the virtual q padding contribute -1) are sorted
-// ascending in LDS (bitonic, P = next pow2 of g*K, -1 mapped past every id),
-// then the first copy of each non-negative id is compacted to the front of
+// ascending (bitonic in registers up to 512 ids, else in the wave's LDS slab;
+// P = next pow2 of g*K, -1 mapped past every id), then the first copy of each non-negative id is compacted to the front of
 // the P-wide output row; the rest of the row is -1 and counts = #unique ids.
 // ----------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void fta_qblock_union_kernel(const int32_t* __restrict__ idx, int N, int K,
                                                                int g, int q_pad_head, int QM, int P,
-                                                               int32_t* __restrict__ merged,
+                                                               int64_t slices, int32_t* __restrict__ merged,
                                                                int32_t* __restrict__ counts) {
-    extern __shared__ int s_key[];
-    __shared__ int s_tmp[8];
-    const int tid = threadIdx.x;
-    const int64_t slice = blockIdx.x;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wpb = blockDim.x >> 6;
+    const int64_t slice = (int64_t)blockIdx.x * wpb + wave;
+    if (slice >= slices) return;
+    uint32_t* key = reinterpret_cast<uint32_t*>(smem) + (size_t)wave * P;
     const int64_t bh = slice / QM;
     const int qm = (int)(slice - bh * QM);
     const int n = g * K;
     const int row0 = qm * g - q_pad_head;
     const int32_t* src = idx + bh * (int64_t)N * K;
-    for (int i = tid; i < P; i += 256) {
-        int v = 0x7fffffff;
+    for (int i = lane; i < P; i += 64) {
+        uint32_t v = 0x7fffffffu;  // sorts after every id
         if (i < n) {
             const int r = row0 + i / K;
             if (r >= 0 && r < N) {
                 const int id = src[(int64_t)r * K + (i - (i / K) * K)];
-                if (id >= 0) v = id;
+                if (id >= 0) v = (uint32_t)id;
             }
         }
-        s_key[i] = v;
+        key[i] = v;
     }
-    __syncthreads();
-    // bitonic sort, ascending; each step compares P/2 disjoint pairs
-    for (int k = 2; k <= P; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int t = tid; t < (P >> 1); t += 256) {
-                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
-                const int a = s_key[i], b = s_key[i + j];
-                const bool up = (i & k) == 0;
-                if ((a > b) == up) {
-                    s_key[i] = b;
-                    s_key[i + j] = a;
-                }
-            }
-            __syncthreads();
-        }
-    }
-    // thread t owns the contiguous run [t*per, (t+1)*per)
-    const int per = (P + 255) / 256;
-    const int lo = min(tid * per, P), hi = min(lo + per, P);
-    int mine = 0;
-    for (int i = lo; i < hi; ++i) {
-        const int v = s_key[i];
-        mine += (v != 0x7fffffff && (i == 0 || v != s_key[i - 1])) ? 1 : 0;
-    }
-    int total = 0;
-    int pos = fta_block_scan256(mine, s_tmp, &total);
+    fta_wave_sync();
+    fta_wave_sort<uint32_t, false>(key, P, 0x7fffffffu, lane);
+    // the first copy of each id, compacted in ascending order
     int32_t* out = merged + slice * (int64_t)P;
-    for (int i = lo; i < hi; ++i) {
-        const int v = s_key[i];
-        if (v != 0x7fffffff && (i == 0 || v != s_key[i - 1])) out[pos++] = v;
+    int total = 0;
+    for (int r0 = 0; r0 < P; r0 += 64) {
+        const int i = r0 + lane;
+        const uint32_t v = (i < P) ? key[i] : 0x7fffffffu;
+        const bool fresh = v != 0x7fffffffu && (i == 0 || v != key[i - 1]);
+        const unsigned long long mask = __ballot(fresh);
+        if (fresh) out[total + __popcll(mask & ((1ull << lane) - 1ull))] = (int32_t)v;
+        total += __popcll(mask);
     }
-    for (int i = total + tid; i < P; i += 256) out[i] = -1;
-    if (tid == 0) counts[slice] = total;
+    for (int i = total + lane; i < P; i += 64) out[i] = -1;
+    if (lane == 0) counts[slice] = total;
 }
 
 namespace fta {
@@ -635,9 +618,11 @@ int fta_qblock_union(const int32_t* topk_indices, int BH, int N, int K, int q_bl
     if (slices == 0) return FTA_OK;
     if (!topk_indices && n > 0 && N > 0) return fta::arg_error("qblock_union: topk_indices is NULL");
     if (!merged_indices || !counts) return fta::arg_error("qblock_union: null output");
-    hipLaunchKernelGGL(fta_qblock_union_kernel, dim3((unsigned)slices), dim3(256), (size_t)s_max * sizeof(int),
-                       (hipStream_t)stream, topk_indices, N, K, q_block_size, q_pad_head, QM, s_max,
-                       merged_indices, counts);
+    // one wave per slice (LDS: s_max ids per wave, at most 32 KB per workgroup)
+    const int wpb = (s_max <= 2048) ? 4 : (s_max <= 4096) ? 2 : 1;
+    hipLaunchKernelGGL(fta_qblock_union_kernel, dim3((unsigned)((slices + wpb - 1) / wpb)), dim3(64 * wpb),
+                       (size_t)wpb * s_max * sizeof(int), (hipStream_t)stream, topk_indices, N, K, q_block_size,
+                       q_pad_head, QM, s_max, slices, merged_indices, counts);
     return fta::check_launch("fta_qblock_union_kernel");
     FTA_TRY_END
 }
