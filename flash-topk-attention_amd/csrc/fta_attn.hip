@@ -23,6 +23,8 @@
 #include "fta_common.h"
 #include "fta_host.h"
 
+#include <mutex>
+
 namespace fta {
 int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint32_t* sel, hipStream_t st);
 }  // namespace fta
@@ -2070,3 +2072,68 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k, 
 }
 
 }  // extern "C"
+
+// ----------------------------------------------------------------------------
+// Allocation-free backward.  Its workspace is this file-scope device array
+// (each GPU that loads the library holds its own copy until the process ends).
+// Host code never passes `scratch` itself to a kernel or a copy: the name is a
+// host-side stand-in; the array's device address comes from
+// hipGetSymbolAddress, taken once per device on the first call there.
+// ----------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[FTA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_address(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        fta::set_error(std::string("sparse_attn_bwd_noalloc: hipGetDevice: ") + hipGetErrorString(e));
+        return FTA_ERR_HIP;
+    }
+    if (dev < 0 || dev >= kMaxDevices) return fta::unsupported("sparse_attn_bwd_noalloc: device index >= 64");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            fta::set_error(std::string("sparse_attn_bwd_noalloc: hipGetSymbolAddress(scratch): ") +
+                           hipGetErrorString(e));
+            return FTA_ERR_HIP;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return FTA_OK;
+}
+}  // namespace
+
+extern "C" int fta_sparse_attn_bwd_noalloc(
+    const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+    const int64_t* v_strides, const void* dout, const int64_t* do_strides, int dtype, int B, int H, int Hk, int N,
+    int D, const int32_t* merged_indices, int QM, int W, int q_block_size, int kv_block_size, int q_pad_head,
+    int q_pad_tail, int kv_pad_head, int kv_pad_tail, float scale, const float* lse, const float* delta, void* dq,
+    const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv, const int64_t* dv_strides,
+    void* stream) {
+    FTA_TRY_BEGIN
+    const size_t need = fta_sparse_attn_bwd_workspace_size(B, H, N, D, q_block_size, kv_block_size, q_pad_head,
+                                                           q_pad_tail, kv_pad_head, kv_pad_tail);
+    if (need > (size_t)FTA_NOALLOC_SCRATCH_BYTES)
+        return fta::unsupported(
+            "sparse_attn_bwd_noalloc: the problem needs more scratch than FTA_NOALLOC_SCRATCH_BYTES "
+            "(membership bitmap + log2 lse); use fta_sparse_attn_bwd_gqa with a caller workspace");
+    void* ws = nullptr;
+    const int rc = scratch_address(&ws);
+    if (rc != FTA_OK) return rc;
+    // every scratch byte the kernels read is written earlier in the same call
+    // (the bitmap is built whole, the log2 lse is converted in full), so no
+    // clearing is needed; calls that overlap on one GPU race on the array
+    return fta_sparse_attn_bwd_gqa(q, q_strides, k, k_strides, v, v_strides, dout, do_strides, dtype, B, H, Hk, N,
+                                   D, merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail,
+                                   kv_pad_head, kv_pad_tail, scale, lse, delta, dq, dq_strides, dk, dk_strides, dv,
+                                   dv_strides, ws, (size_t)FTA_NOALLOC_SCRATCH_BYTES, stream);
+    FTA_TRY_END
+}

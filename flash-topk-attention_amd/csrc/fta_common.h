@@ -211,3 +211,6 @@ __device__ __forceinline__ void fta_wait_vmcnt() {
 #define FTA_ERR_ARG 1
 #define FTA_ERR_UNSUPPORTED 2
 #define FTA_ERR_HIP 3
+
+// Size of the device array behind fta_sparse_attn_bwd_noalloc (include/fta.h).
+#define FTA_NOALLOC_SCRATCH_BYTES (64u << 20)

@@ -58,6 +58,9 @@ _SIGNATURES = {
     "fta_sparse_attn_bwd_gqa": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _i, _p, _i,
                                      _i, _i, _i, _i, _i, _i, _i, _f, _p, _p, _p, _i64p, _p, _i64p, _p, _i64p, _p,
                                      _sz, _p]),
+    "fta_sparse_attn_bwd_noalloc": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _i, _p,
+                                         _i, _i, _i, _i, _i, _i, _i, _i, _f, _p, _p, _p, _i64p, _p, _i64p, _p,
+                                         _i64p, _p]),
 }
 
 

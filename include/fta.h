@@ -262,6 +262,30 @@ int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void*
                             const int64_t* dk_strides, void* dv, const int64_t* dv_strides,
                             void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Allocation-free backward.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving or training loops, harnesses that forbid hipMalloc).  Same arguments
+ * and results as fta_sparse_attn_bwd_gqa without (workspace, workspace_bytes):
+ * the scratch (membership bitmap + lse in log2 units, the size that
+ * fta_sparse_attn_bwd_workspace_size reports) lives in a device array of
+ * FTA_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the
+ * process ends.  A problem needing more returns FTA_ERR_UNSUPPORTED.  The call
+ * allocates nothing (no hipMalloc, no library allocator); it uses the current
+ * device's array, so `stream` must belong to the current device.  Calls that
+ * overlap on one GPU (different streams, or host threads) race on the array.
+ */
+#define FTA_NOALLOC_SCRATCH_BYTES (64u << 20)
+int fta_sparse_attn_bwd_noalloc(const void* q, const int64_t* q_strides, const void* k,
+                                const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                const void* dout, const int64_t* do_strides, int dtype, int B, int H,
+                                int Hk, int N, int D, const int32_t* merged_indices, int QM, int W,
+                                int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail,
+                                int kv_pad_head, int kv_pad_tail, float scale, const float* lse,
+                                const float* delta, void* dq, const int64_t* dq_strides, void* dk,
+                                const int64_t* dk_strides, void* dv, const int64_t* dv_strides,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif
