@@ -42,8 +42,9 @@ def _sparse_attn_fwd(q, k, v, merged, H, g, kvb, scale, q_padding, kv_padding, H
     return o, lse
 
 
-class FlashSparseAttnFunc(torch.autograd.Function):
-    """Autograd function: HIP forward, HIP dQ / dK / dV backward."""
+class _SparseAttnGQAFunc(torch.autograd.Function):
+    """Autograd function behind ``flash_sparse_attn``: HIP forward, HIP dQ / dK /
+    dV backward, virtual paddings passed through, optional grouped K/V heads."""
 
     @staticmethod
     def forward(ctx, q, k, v, merged_indices, num_heads, q_block_size, kv_block_size,
@@ -71,6 +72,75 @@ class FlashSparseAttnFunc(torch.autograd.Function):
             ctx.softmax_scale, ctx.q_padding, ctx.kv_padding, delta=delta, num_kv_heads=ctx.num_kv_heads,
         )
         return dq, dk, dv, None, None, None, None, None, None, None, None
+
+
+class FlashSparseAttnFunc(torch.autograd.Function):
+    """Autograd function with the reference's call contract
+    (flash_topk_attn_v2/sparse_attn.py:130-224):
+
+    ``FlashSparseAttnFunc.apply(q, k, v, merged_indices, counts, num_heads,
+    q_block_size, kv_block_size, qblock_topk, softmax_scale, q_pad_head,
+    kv_pad_head, N_real, num_kv_blocks)`` with q, k, v ``[B, N_phys, C]``
+    (rows past ``N_real`` are physical padding and are not read) returns
+    ``(output [B, N_real, C], softmax_max, softmax_lse)``, each ``[B, H, N_real]``
+    fp32.  The kernels produce the full natural-log lse in one value, so
+    ``softmax_max`` is 0 and ``softmax_lse`` is the lse: their sum is the
+    reference's lse (sparse_attn.py:391).  The virtual tail paddings follow
+    from the shapes, as in the reference's kernels: q tail =
+    QM * q_block_size - q_pad_head - N_real, kv tail = num_kv_blocks *
+    kv_block_size - kv_pad_head - N_real.  ``counts`` and ``qblock_topk`` are
+    implied by ``merged_indices`` (-1 entries are skipped).  Gradients are
+    ``[B, N_phys, C]`` with zero rows past ``N_real``.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, merged_indices, counts, num_heads, q_block_size, kv_block_size, qblock_topk,
+                softmax_scale, q_pad_head, kv_pad_head, N_real, num_kv_blocks):
+        del counts, qblock_topk
+        B, N_phys, C = q.shape
+        N = int(N_real)
+        if N <= 0 or N > N_phys:
+            raise ValueError(f"N_real={N_real} must be in [1, N_phys={N_phys}]")
+        QM = merged_indices.shape[2]
+        q_padding = (int(q_pad_head), QM * q_block_size - int(q_pad_head) - N)
+        kv_padding = (int(kv_pad_head), int(num_kv_blocks) * kv_block_size - int(kv_pad_head) - N)
+        if q_padding[1] < 0 or kv_padding[1] < 0:
+            raise ValueError("merged_indices / num_kv_blocks do not cover N_real with the given head paddings")
+        merged = merged_indices.to(torch.int32).contiguous()
+        qs, ks, vs = q[:, :N], k[:, :N], v[:, :N]
+        o, lse = _sparse_attn_fwd(qs, ks, vs, merged, num_heads, q_block_size, kv_block_size,
+                                  float(softmax_scale), q_padding, kv_padding, num_heads)
+        softmax_max = torch.zeros_like(lse)
+        ctx.save_for_backward(q, k, v, o, merged, lse)
+        ctx.num_heads = num_heads
+        ctx.q_block_size = q_block_size
+        ctx.kv_block_size = kv_block_size
+        ctx.softmax_scale = float(softmax_scale)
+        ctx.q_padding = q_padding
+        ctx.kv_padding = kv_padding
+        ctx.N_real = N
+        ctx.mark_non_differentiable(softmax_max, lse)
+        return o, softmax_max, lse
+
+    @staticmethod
+    def backward(ctx, grad_output, _grad_sm, _grad_sl):
+        q, k, v, o, merged, lse = ctx.saved_tensors
+        N = ctx.N_real
+        B, N_phys, C = q.shape
+        H = ctx.num_heads
+        delta = preprocess_delta(o, grad_output, H)
+        dq, dk, dv = sparse_attn_bwd(
+            q[:, :N], k[:, :N], v[:, :N], o, grad_output, lse, merged, H, ctx.q_block_size, ctx.kv_block_size,
+            ctx.softmax_scale, ctx.q_padding, ctx.kv_padding, delta=delta,
+        )
+        if N_phys > N:
+            grads = []
+            for g in (dq, dk, dv):
+                full = g.new_zeros(B, N_phys, C)
+                full[:, :N] = g
+                grads.append(full)
+            dq, dk, dv = grads
+        return (dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None)
 
 
 def flash_sparse_attn(
@@ -179,7 +249,7 @@ def flash_sparse_attn(
         scale = 1.0 / math.sqrt(D)
 
     merged = merged_indices.contiguous()
-    output, lse = FlashSparseAttnFunc.apply(
+    output, lse = _SparseAttnGQAFunc.apply(
         q, k, v, merged, H, q_block_size, kv_block_size, float(scale),
         (q_pad_head, q_pad_tail), (kv_pad_head, kv_pad_tail), Hk,
     )

@@ -399,3 +399,41 @@ def test_pipeline_config1():
     qt, kt, vt = (x.double().view(B, N, H, D).transpose(1, 2) for x in (q, k, v))
     ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt).transpose(1, 2).reshape(B, N, H * D)
     np.testing.assert_allclose(np32(o), ref.cpu().numpy(), atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("N,Nphys,H,D,g,b,qph,kvph,W", [
+    (1024, 1024, 2, 128, 32, 64, 0, 0, 12),
+    (1000, 1000, 2, 64, 16, 64, 8, 24, 9),
+    (40, 64, 2, 64, 8, 64, 0, 0, 2),  # physical padding to 64 rows, as flash_sparse_attn makes it
+])
+def test_flash_sparse_attn_func_reference_contract(N, Nphys, H, D, g, b, qph, kvph, W):
+    """FlashSparseAttnFunc.apply with the reference's 14 arguments
+    (flash_topk_attn_v2/sparse_attn.py:134-161) equals flash_topk_attn on the
+    same inputs: o bit for bit, softmax_max + softmax_lse == lse, gradients
+    equal on the real rows and zero on the physical padding rows."""
+    say(f"[FlashSparseAttnFunc] N{N} Nphys{Nphys} H{H} D{D} g{g} b{b} pads {qph},{kvph}")
+    from flash_topk_attn_v2 import FlashSparseAttnFunc
+
+    QM = -(-(qph + N) // g)
+    M = -(-(kvph + N) // b)
+    qpad, kvpad = (qph, QM * g - qph - N), (kvph, M * b - kvph - N)
+    merged = torch.from_numpy(_random_merged(1, H, QM, W, M, 7)).cuda()
+    counts = (merged >= 0).sum(-1).int()
+    base = [rand((1, Nphys, H * D), 70 + i, torch.bfloat16, "cuda") for i in range(3)]
+    do = rand((1, N, H * D), 74, torch.bfloat16, "cuda")
+    scale = D ** -0.5
+
+    x1 = [t.clone().requires_grad_(True) for t in base]
+    o1, sm, sl = FlashSparseAttnFunc.apply(x1[0], x1[1], x1[2], merged, counts, H, g, b, W, scale, qph, kvph, N, M)
+    o1.backward(do)
+    x2 = [t[:, :N].clone().requires_grad_(True) for t in base]
+    o2, lse2 = fta.flash_topk_attn(x2[0], x2[1], x2[2], merged, counts, H, g, b, scale, None, kvpad, qpad)
+    o2.backward(do)
+    torch.cuda.synchronize()
+    assert o1.shape == (1, N, H * D) and sm.shape == (1, H, N) and sl.shape == (1, H, N)
+    assert torch.equal(o1, o2)
+    assert torch.equal(sm + sl, lse2)
+    for a, c in zip(x1, x2):
+        assert a.grad.shape == (1, Nphys, H * D)
+        assert torch.equal(a.grad[:, :N], c.grad)
+        assert not a.grad[:, N:].any()

@@ -30,6 +30,12 @@ UNION_CASES = [
     (1, 2, 4096, 16, 512, (0, 0), 64, False),   # g*K = 8192: the largest row
     (1, 2, 64, 0, 16, (0, 0), 1, False),        # K = 0: every q-block empty
     (1, 1, 40, 16, 64, (0, 24), 100000, False),  # ids far beyond any bitmap
+    # LDS bitonic paths with several waves per workgroup; 3 heads x 5 q-blocks = 15
+    # slices, a count that neither 4 nor 2 waves per workgroup divide (tail workgroup)
+    (1, 3, 320, 16, 64, (0, 0), 700, False),    # g*K = 1024
+    (1, 3, 640, 16, 128, (0, 0), 3000, False),  # g*K = 2048
+    (1, 3, 640, 32, 128, (0, 0), 4096, False),  # g*K = 4096
+    (1, 3, 600, 32, 128, (20, 20), 4000, True),  # g*K = 4096 with q padding
 ]
 
 
