@@ -506,19 +506,41 @@ struct ScorePipeShape {
     static_assert(SLOTS % 256 == 0, "whole DMA instructions per wave");
 };
 
-template <int DT, int D>
+// Candidate streams (template NG > 0, top-k lists of at most 16 blocks):
+// instead of the [BH][M][N] per-block values, each wave appends, per block, an
+// entry (value, lane << 16 | m) for every query of the wave for which the block
+// can still be in the top-k, compacted in lane order (cand[wave][...]); the
+// wave's entry count goes to cand_count[wave].  A block is dropped for a query
+// when at least m_out earlier blocks rank strictly above it: each query keeps,
+// in LDS, the two largest ranking keys (block value + log2(b / valid count)) of
+// NG interleaved block groups (m mod NG, NG = 4 for m_out <= 8, else 8); the
+// smallest second largest over the groups bounds 2 NG >= m_out earlier blocks
+// from below.  The bound is refreshed once per NG blocks and lowered by a
+// margin far above fp32 exp2 / log2 rounding, and partial edge blocks always
+// pass, so the final selection over the streams equals the one over all
+// blocks.  tau_key[row] receives the final bound (at least m_out blocks rank
+// at or above it).
+constexpr int kStreamMaxTopk = 16;
+
+__device__ __forceinline__ float fta_stream_margin(float b) { return b - (0x1p-10f + fabsf(b) * 0x1p-18f); }
+
+template <int DT, int D, int NG>
 __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
     int H, int N, int Dreal, int M, int bsz, int pad_head, int pad_tail, float c,
     float* __restrict__ blk_lse, float* __restrict__ row_lse, int qtiles, int total, int kgroups,
-    int32_t* __restrict__ tau_idx) {
+    int32_t* __restrict__ tau_idx, uint2* __restrict__ cand, int* __restrict__ cand_count,
+    float* __restrict__ tau_key) {
+    // NG > 0: candidate streams with NG block groups (STREAM)
+    constexpr bool STREAM = NG > 0;
     using E = Elem<DT>;
     using Sh = ScorePipeShape<D>;
     using SW = FtaSwz<Sh::QSEG>;
     constexpr int KS = D / 16;
     constexpr int QSEG = Sh::QSEG, LQ = Sh::LQ, NBUF = Sh::NBUF;
     __shared__ __align__(1024) unsigned char sK[NBUF][Sh::BUF_B];
+    __shared__ float2 sG[STREAM ? NG : 1][256];
 
     const int wg = fta_xcd_remap(blockIdx.x, total);
     const int bh = wg / qtiles;
@@ -668,6 +690,20 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     const float adj_head = (pad_head > 0) ? fta_log2((float)bsz / (float)(bsz - pad_head)) : 0.f;
     const float adj_tail = (pad_tail > 0) ? fta_log2((float)bsz / (float)(bsz - pad_tail)) : 0.f;
 
+    // candidate-stream state: this wave's key / mask streams, write position,
+    // current filter bound and group slot
+    uint2* cst = nullptr;
+    int spos = 0, gslot = 0;
+    // lanes past N never pass: their bound is +inf
+    const bool lane_ok = qbase + lane < N;
+    float sbnd = lane_ok ? -FTA_INF : FTA_INF;
+    if constexpr (STREAM) {
+        const int64_t sw = (int64_t)wg * 4 + wave;
+        cst = cand + sw * 64 * M;
+#pragma unroll
+        for (int j = 0; j < NG; ++j) sG[j][tid] = make_float2(-FTA_INF, -FTA_INF);
+    }
+
 #pragma unroll
     for (int j = 0; j < NBUF - 1; ++j)
         if (j < M) issue(j);
@@ -774,8 +810,33 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
                 }
         }
         const int qi = qbase + lane;
-        if (qi < N) blk_lse[((int64_t)bh * M + m) * N + qi] = mine;
-        if (kgroups > 0) {
+        if constexpr (STREAM) {
+            // wave-uniform adjustment and edge flag (partial edge blocks always pass)
+            const float adj = ((m == 0) ? adj_head : 0.f) + ((m == M - 1) ? adj_tail : 0.f);
+            const bool em = ((m == 0) & (pad_head > 0)) | ((m == M - 1) & (pad_tail > 0));
+            const float ak = mine + adj;
+            const bool pass = (ak >= sbnd) | (em & lane_ok);
+            const unsigned long long mk = __ballot(pass);
+            const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
+            if (pass) cst[spos + rank] = make_uint2(__builtin_bit_cast(uint32_t, mine), ((uint32_t)lane << 16) | m);
+            spos += __popcll(mk);
+            // group top-2 (max / min as med3 with an infinite third operand)
+            float2 t = sG[gslot][tid];
+            t.y = __builtin_amdgcn_fmed3f(t.y, __builtin_amdgcn_fmed3f(t.x, ak, -FTA_INF), FTA_INF);
+            t.x = __builtin_amdgcn_fmed3f(t.x, ak, FTA_INF);
+            sG[gslot][tid] = t;
+            if (++gslot == NG) {
+                gslot = 0;
+                float bnd = sG[0][tid].y;
+#pragma unroll
+                for (int j = 1; j < NG; ++j) bnd = __builtin_amdgcn_fmed3f(bnd, sG[j][tid].y, -FTA_INF);
+                sbnd = lane_ok ? fta_stream_margin(bnd) : FTA_INF;
+            }
+        } else {
+            if (qi < N) blk_lse[((int64_t)bh * M + m) * N + qi] = mine;
+        }
+        if (!STREAM && kgroups > 0) {
             float key = mine;
             if (m == 0) key += adj_head;
             if (m == M - 1) key += adj_tail;
@@ -799,12 +860,20 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     block(M - 1);
 
     const int qi = qbase + lane;
+    if constexpr (STREAM) {
+        if (lane == 0) cand_count[(int64_t)wg * 4 + wave] = spos;
+    }
     if (qi < N) {
         const bool t1 = lane >= 32;
         const float Rr = t1 ? R[1] : R[0];
         const float Lr = t1 ? L[1] : L[0];
         row_lse[(int64_t)bh * N + qi] = (Lr > 0.f) ? Rr + fta_log2(Lr) : -FTA_INF;
-        if (kgroups > 0) {
+        if constexpr (STREAM) {
+            float bnd = sG[0][tid].y;
+#pragma unroll
+            for (int j = 1; j < NG; ++j) bnd = fminf(bnd, sG[j][tid].y);
+            tau_key[(int64_t)bh * N + qi] = bnd;
+        } else if (kgroups > 0) {
             if (curg >= 0 && gkey < tkey) tidx = gidx;
             tau_idx[(int64_t)bh * N + qi] = tidx;
         }
@@ -847,8 +916,25 @@ __global__ __launch_bounds__(256) void fta_block_normalize_kernel(const float* _
 // MODE 0 reads raw scores in[row * stride_row + m * stride_m];
 // MODE 1 reads the lse2 intermediate ([BH][M][N]) and row totals.
 // ----------------------------------------------------------------------------
+// (v, i) ranks above (w, j): larger value, ties to the lower index.  Bitwise
+// operators, not && / ||: the short-circuit form compiles to an exec-mask
+// branch per comparison inside the insertion network.
 __device__ __forceinline__ bool fta_better(float v, int i, float w, int j) {
-    return v > w || (v == w && i < j);
+    return (v > w) | ((v == w) & (i < j));
+}
+
+// raw / valid_count with IEEE division; for a power-of-two block size the
+// interior blocks' quotient is the (exact) product with 1 / b, which is the
+// same correctly rounded value, and the division sequence runs only when some
+// lane of the wave holds a partial edge block.
+__device__ __forceinline__ float fta_avg(float raw, int vc, int bsz, float inv_b) {
+    float a = raw * inv_b;
+    const bool slow = (vc != bsz) | (inv_b == 0.f);
+    if (__ballot(slow) != 0ull) {
+        const float q = raw / (float)vc;
+        a = slow ? q : a;
+    }
+    return a;
 }
 
 __device__ __forceinline__ int fta_valid_count(int m, int M, int bsz, int pad_head, int pad_tail) {
@@ -873,19 +959,21 @@ template <int KB, int CAP, int MODE>
 __device__ __forceinline__ void fta_topk_flush(float (&lv)[KB], int (&li)[KB], int& cnt, const float (&cv)[CAP][64],
                                                const int (&ci)[CAP][64], int lane, bool active, float rl, float pre,
                                                float thr_norm, int M, int bsz, int pad_head, int pad_tail,
-                                               int m_out, float& tv, int& ti) {
+                                               int m_out, float threshold, float& tv, int& ti) {
+    // 1 / b when b is a power of two (an exact reciprocal), else 0
+    const float inv_b = ((bsz & (bsz - 1)) == 0) ? 1.f / (float)bsz : 0.f;
     int mc = cnt;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) mc = max(mc, __shfl_xor(mc, off, 64));
     for (int j = 0; j < mc; ++j) {
         const float xs = cv[j][lane];
         const int m = ci[j][lane];
-        const bool edge = (m == 0 && pad_head > 0) || (m == M - 1 && pad_tail > 0);
+        const bool edge = ((m == 0) & (pad_head > 0)) | ((m == M - 1) & (pad_tail > 0));
         const float x = (MODE == 0) ? xs : xs - rl;
         const float raw = (MODE == 0) ? x : fta_exp2(x);
         const int vc = fta_valid_count(m, M, bsz, pad_head, pad_tail);
-        const float avg = raw / (float)vc;
-        const bool ok = active && j < cnt && (edge || (x >= pre && raw >= thr_norm)) &&
+        const float avg = fta_avg(raw, vc, bsz, inv_b);
+        const bool ok = active & (j < cnt) & (edge | ((x >= pre) & (raw >= thr_norm))) &
                         fta_better(avg, m, tv, ti);
         if (__ballot(ok) == 0ull) continue;  // no lane inserts: skip the network
         const float v = ok ? avg : -FTA_INF;
@@ -916,6 +1004,97 @@ __device__ __forceinline__ void fta_topk_flush(float (&lv)[KB], int (&li)[KB], i
             tv = lv[p];
             ti = li[p];
         }
+    // Threshold cut of the current list.  Later candidates only raise each
+    // prefix sum of the sorted raw values (the i-th largest of a superset is at
+    // least the i-th largest of the set, and fp32 rounding is monotone), so the
+    // final cut is at or before the current one, and a block ranked below the
+    // current cut entry is never output: that entry bounds the rest.
+    float cs = 0.f;
+    bool found = false;
+#pragma unroll
+    for (int p = 0; p < KB; ++p) {
+        const bool use = (p < m_out) & !found & (li[p] != 0x7fffffff);
+        const float rw = __fmul_rn(lv[p], (float)fta_valid_count(li[p], M, bsz, pad_head, pad_tail));
+        cs = use ? __fadd_rn(cs, rw) : cs;
+        const bool hit = use & (cs >= threshold);
+        if (hit & fta_better(lv[p], li[p], tv, ti)) {
+            tv = lv[p];
+            ti = li[p];
+        }
+        found = found | hit;
+    }
+}
+
+// Threshold cut and output of a wave's sorted register lists (rows wrow0 ..
+// wrow0 + nrows - 1, lane = row - wrow0): keep positions up to the first whose
+// sequential fp32 cumulative raw score reaches the threshold, -1 / 0 after.
+// Outputs are staged in the wave's LDS buffer `st` when every list fits.
+template <int KB, int CAP>
+__device__ __forceinline__ void fta_topk_emit(float (&lv)[KB], int (&li)[KB], int m_out, int M, int bsz,
+                                              int pad_head, int pad_tail, float threshold,
+                                              int32_t* __restrict__ out_idx, float* __restrict__ out_raw,
+                                              float* __restrict__ out_avg, int64_t wrow0, int nrows, int lane,
+                                              bool active, int64_t row, float (&stage)[CAP][64]) {
+    float cs = 0.f;
+    int cut = m_out;
+    bool found = false;
+#pragma unroll
+    for (int p = 0; p < KB; ++p) {
+        if (p < m_out && !found) {
+            const float rw = __fmul_rn(lv[p], (float)fta_valid_count(li[p], M, bsz, pad_head, pad_tail));
+            cs = __fadd_rn(cs, rw);
+            if (cs >= threshold) {
+                cut = p + 1;
+                found = true;
+            }
+        }
+    }
+    float rawv[KB];
+#pragma unroll
+    for (int p = 0; p < KB; ++p) {
+        const bool keep = p < cut;
+        rawv[p] = keep ? __fmul_rn(lv[p], (float)fta_valid_count(li[p], M, bsz, pad_head, pad_tail)) : 0.f;
+        lv[p] = keep ? lv[p] : 0.f;
+        li[p] = keep ? li[p] : -1;
+    }
+    const bool aligned = ((reinterpret_cast<uintptr_t>(out_idx) | reinterpret_cast<uintptr_t>(out_raw) |
+                           reinterpret_cast<uintptr_t>(out_avg)) & 15) == 0;
+    if (m_out <= CAP && aligned) {
+        // Stage each output's 64 x m_out block (contiguous in HBM) in this wave's
+        // candidate buffer, then write it with 16-byte stores over consecutive
+        // addresses instead of one 4-byte store per (lane, slot).
+        float* st = &stage[0][0];
+        const int total = nrows * m_out, n4 = total >> 2;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            float* out = (k == 0) ? reinterpret_cast<float*>(out_idx) : (k == 1) ? out_raw : out_avg;
+            out += wrow0 * m_out;
+#pragma unroll
+            for (int p = 0; p < KB; ++p)
+                if (p < m_out)
+                    st[lane * m_out + p] = (k == 0) ? __builtin_bit_cast(float, li[p]) : (k == 1) ? rawv[p] : lv[p];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (int c = lane; c < n4; c += 64)
+                reinterpret_cast<float4*>(out)[c] = reinterpret_cast<const float4*>(st)[c];
+            for (int e = (n4 << 2) + lane; e < total; e += 64) out[e] = st[e];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        return;
+    }
+    if (!active) return;
+    const int64_t o = (int64_t)row * m_out;
+#pragma unroll
+    for (int p = 0; p < KB; ++p) {
+        if (p < m_out) {
+            out_idx[o + p] = li[p];
+            out_avg[o + p] = lv[p];
+            out_raw[o + p] = rawv[p];
+        }
+    }
 }
 
 template <int KB, int MODE>
@@ -998,7 +1177,7 @@ __global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_select_kerne
     auto flush = [&] __attribute__((always_inline)) () {
         fta_topk_flush<KB, CAP, MODE>(lv, li, cnt, cand_v[wave], cand_i[wave], lane, active, rl,
                                       (MODE == 0) ? thr_norm : thr_log, thr_norm, M, bsz, pad_head, pad_tail,
-                                      m_out, tv, ti);
+                                      m_out, threshold, tv, ti);
         set_thr();
     };
     auto test_batch = [&] __attribute__((always_inline)) (int m1, const float (&xs)[LDB]) {
@@ -1049,66 +1228,140 @@ __global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_select_kerne
     const int64_t wrow0 = (int64_t)blockIdx.x * 256 + wave * 64;
     const int nrows = (int)min((int64_t)64, (int64_t)rows - wrow0);
     if (nrows <= 0) return;
-    float cs = 0.f;
-    int cut = m_out;
-    bool found = false;
+    fta_topk_emit<KB, CAP>(lv, li, m_out, M, bsz, pad_head, pad_tail, threshold, out_idx, out_raw, out_avg, wrow0,
+                           nrows, lane, active, row, cand_v[wave]);
+}
+
+// Top-k selection over the candidate streams of the pipelined scoring kernel
+// (STREAM = true).  One wave per scoring wave (64 consecutive queries of one
+// b*h, lane = query); the workgroup's 4 waves are one scoring workgroup's.
+// The wave reads its stream 64 entries at a time (coalesced), and each entry
+// that passes its owner's pre-filter (value >= the owner's bound, kept in LDS
+// in the value domain) is parked in the owner's LDS candidate list at a slot
+// taken with an LDS atomic.  When an entry finds its owner's list full, every
+// lane merges its parked candidates (fta_topk_flush: exact tests and the
+// insertion network) and the entry is parked again.  Each owner's bound starts
+// from tau_key (at least m_out blocks rank at or above it) and tightens as its
+// list fills.
+template <int KB>
+__global__ __launch_bounds__(256, 4) void fta_topk_stream_kernel(
+    const uint2* __restrict__ cand, const int* __restrict__ cand_count, const float* __restrict__ tau_key,
+    const float* __restrict__ row_lse, int N, int qtiles, int M, int m_out, int bsz, int pad_head, int pad_tail,
+    float threshold, int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg) {
+    constexpr int CAP = 16;
+    __shared__ __align__(16) float cand_v[4][CAP][64];
+    __shared__ int cand_i[4][CAP][64];
+    __shared__ int s_cnt[4][64];
+    __shared__ float s_pre[4][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bh = blockIdx.x / qtiles;
+    const int n0 = (blockIdx.x - bh * qtiles) * 256 + wave * 64;
+    const int n = n0 + lane;
+    const bool active = n < N;
+    const int64_t row = (int64_t)bh * N + (active ? n : 0);
+    const int64_t sw = (int64_t)blockIdx.x * 4 + wave;
+    const uint2* ent = cand + sw * 64 * M;
+    const int total = __builtin_amdgcn_readfirstlane(cand_count[sw]);
+
+    float lv[KB];
+    int li[KB];
 #pragma unroll
     for (int p = 0; p < KB; ++p) {
-        if (p < m_out && !found) {
-            const float rw = __fmul_rn(lv[p], (float)fta_valid_count(li[p], M, bsz, pad_head, pad_tail));
-            cs = __fadd_rn(cs, rw);
-            if (cs >= threshold) {
-                cut = p + 1;
-                found = true;
+        lv[p] = -FTA_INF;
+        li[p] = 0x7fffffff;
+    }
+    float tv = -FTA_INF;
+    int ti = 0x7fffffff;
+    int cnt = 0;
+    const float rl = row_lse[row];
+    {
+        // ranking key = value + log2(b / valid count), so its avg is 2^(key - rl) / b
+        const float at = fta_exp2(tau_key[row] - rl) / (float)bsz;
+        tv = at - fabsf(at) * 0x1p-8f;
+    }
+    float thr_norm = -FTA_INF, thr_log = -FTA_INF;
+    auto set_thr = [&] __attribute__((always_inline)) () {
+        const float t = tv * (float)bsz;
+        thr_norm = t - fabsf(t) * 9.5367431640625e-07f;
+        thr_log = (thr_norm > 0.f) ? fta_log2(thr_norm) - 2.44140625e-04f : -FTA_INF;
+        // the owner's pre-filter in the value domain: value >= rl + thr_log, lowered
+        // by a margin far above the rounding of the sum
+        const float pv = rl + thr_log;
+        s_pre[wave][lane] = active ? pv - (0x1p-12f + fabsf(pv) * 0x1p-20f) : FTA_INF;
+        s_cnt[wave][lane] = 0;
+    };
+    set_thr();
+    auto wave_sync = [] __attribute__((always_inline)) () {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    auto flush = [&] __attribute__((always_inline)) () {
+        wave_sync();
+        cnt = min(s_cnt[wave][lane], CAP);
+        fta_topk_flush<KB, CAP, 1>(lv, li, cnt, cand_v[wave], cand_i[wave], lane, active, rl, thr_log, thr_norm, M,
+                                   bsz, pad_head, pad_tail, m_out, threshold, tv, ti);
+        wave_sync();
+        set_thr();
+        wave_sync();
+    };
+    wave_sync();
+    // NC chunks of 64 entries per step, the next step's chunks loading meanwhile;
+    // the pre-filter reads, slot atomics and parking stores of a step's chunks
+    // are issued together, so their LDS latencies overlap.
+    constexpr int NC = 4;
+    auto load_step = [&] __attribute__((always_inline)) (int c0, uint2 (&e)[NC]) {
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            // unconditional (clamped) loads keep the next step's loads in flight;
+            // entries past the end are masked where they are used
+            e[i] = ent[min(c0 + i * 64 + lane, 64 * M - 1)];
+        }
+    };
+    uint2 ea[NC], eb[NC];
+    load_step(0, ea);
+    for (int c0 = 0; c0 < total; c0 += NC * 64) {
+        load_step(c0 + NC * 64, eb);
+        int owner[NC], m[NC];
+        float x[NC];
+        bool pend[NC];
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            owner[i] = (int)(ea[i].y >> 16) & 63;
+            m[i] = (int)(ea[i].y & 0xffffu);
+            x[i] = __builtin_bit_cast(float, ea[i].x);
+            const bool em = ((m[i] == 0) & (pad_head > 0)) | ((m[i] == M - 1) & (pad_tail > 0));
+            pend[i] = (c0 + i * 64 + lane < total) & (em | (x[i] >= s_pre[wave][owner[i]]));
+        }
+        bool any = false;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) any |= pend[i];
+        while (__ballot(any) != 0ull) {
+            int pos[NC];
+#pragma unroll
+            for (int i = 0; i < NC; ++i) pos[i] = pend[i] ? atomicAdd(&s_cnt[wave][owner[i]], 1) : CAP;
+            any = false;
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+                const bool ok = pend[i] & (pos[i] < CAP);
+                if (ok) {
+                    cand_v[wave][pos[i]][owner[i]] = x[i];
+                    cand_i[wave][pos[i]][owner[i]] = m[i];
+                }
+                pend[i] = pend[i] & !ok;
+                any |= pend[i];
             }
+            if (__ballot(any) != 0ull) flush();
         }
-    }
-    float rawv[KB];
 #pragma unroll
-    for (int p = 0; p < KB; ++p) {
-        const bool keep = p < cut;
-        rawv[p] = keep ? __fmul_rn(lv[p], (float)fta_valid_count(li[p], M, bsz, pad_head, pad_tail)) : 0.f;
-        lv[p] = keep ? lv[p] : 0.f;
-        li[p] = keep ? li[p] : -1;
+        for (int i = 0; i < NC; ++i) ea[i] = eb[i];
     }
-    const bool aligned = ((reinterpret_cast<uintptr_t>(out_idx) | reinterpret_cast<uintptr_t>(out_raw) |
-                           reinterpret_cast<uintptr_t>(out_avg)) & 15) == 0;
-    if (m_out <= CAP && aligned) {
-        // Stage each output's 64 x m_out block (contiguous in HBM) in this wave's
-        // candidate buffer, then write it with 16-byte stores over consecutive
-        // addresses instead of one 4-byte store per (lane, slot).
-        float* st = &cand_v[wave][0][0];
-        const int total = nrows * m_out, n4 = total >> 2;
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            float* out = (k == 0) ? reinterpret_cast<float*>(out_idx) : (k == 1) ? out_raw : out_avg;
-            out += wrow0 * m_out;
-#pragma unroll
-            for (int p = 0; p < KB; ++p)
-                if (p < m_out)
-                    st[lane * m_out + p] = (k == 0) ? __builtin_bit_cast(float, li[p]) : (k == 1) ? rawv[p] : lv[p];
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            for (int c = lane; c < n4; c += 64)
-                reinterpret_cast<float4*>(out)[c] = reinterpret_cast<const float4*>(st)[c];
-            for (int e = (n4 << 2) + lane; e < total; e += 64) out[e] = st[e];
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        }
-        return;
-    }
-    if (!active) return;
-    const int64_t o = (int64_t)row * m_out;
-#pragma unroll
-    for (int p = 0; p < KB; ++p) {
-        if (p < m_out) {
-            out_idx[o + p] = li[p];
-            out_avg[o + p] = lv[p];
-            out_raw[o + p] = rawv[p];
-        }
-    }
+    flush();
+    const int nrows = min(64, N - n0);
+    if (nrows <= 0) return;
+    fta_topk_emit<KB, CAP>(lv, li, m_out, M, bsz, pad_head, pad_tail, threshold, out_idx, out_raw, out_avg,
+                           (int64_t)bh * N + n0, nrows, lane, active, row, cand_v[wave]);
 }
 
 // Slow general path for m_out > 64: one workgroup per row, bitonic sort of the
@@ -1198,21 +1451,46 @@ __global__ __launch_bounds__(256) void fta_topk_select_sort_kernel(
 
 namespace {
 
+// The pipelined scoring kernel serves b = 64 with D <= 128 rounded to 64 or 128
+// and a K token stride whose 64-row offsets fit 32 bits.
+bool score_pipe_ok(int bsz, int Dk, const int64_t* ks) {
+    return bsz == 64 && (Dk == 64 || Dk == 128) && ks[2] >= 0 && ks[2] <= (1 << 24);
+}
+
+// Candidate streams of the pipelined kernel (STREAM = true): entries
+// [waves][64 * M] (value, lane << 16 | m), counts [waves], tau keys [B*H][N];
+// waves = B * H * ceil(N / 256) * 4.
+struct StreamBufs {
+    uint2* cand = nullptr;
+    int* count = nullptr;
+    float* tau_key = nullptr;
+    int ngroups = 0;
+};
+
+int64_t stream_waves(int B, int H, int N) { return (int64_t)B * H * ((N + 255) / 256) * 4; }
+
 template <int DT>
 int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D, int Dk, const int64_t* qs,
                         const int64_t* ks, int M, int bsz, int pad_head, int pad_tail, float scale,
-                        float* blk_lse, float* row_lse, int kgroups, int32_t* tau, hipStream_t st) {
+                        float* blk_lse, float* row_lse, int kgroups, int32_t* tau, const StreamBufs& sb,
+                        hipStream_t st) {
     const int qtiles = (N + 255) / 256;
     const int total = qtiles * B * H;
     const float c = scale * 1.4426950408889634f;
-    // the pipelined kernel keeps 64-row offsets (row * k token stride) in 32-bit registers
-    const bool k_sn_ok = ks[2] >= 0 && ks[2] <= (1 << 24);
+    const bool pipe = score_pipe_ok(bsz, Dk, ks);
+    if (sb.cand != nullptr && !pipe) return fta::arg_error("block_score: candidate streams need the pipelined kernel");
+#define FTA_LAUNCH_PIPE(DK, NG, CAND, CNT, TAU, KG, TI)                                                   \
+    hipLaunchKernelGGL((fta_block_score_lse_pipe_kernel<DT, (DK == 64) ? 64 : 128, NG>), dim3(total),       \
+                       dim3(256), 0, st, (const uint16_t*)q, (const uint16_t*)k, qs[0], qs[1], qs[2], ks[0],  \
+                       ks[1], ks[2], H, N, D, M, bsz, pad_head, pad_tail, c, blk_lse, row_lse, qtiles, total, KG, \
+                       TI, CAND, CNT, TAU)
 #define FTA_LAUNCH_SCORE(DK)                                                                               \
-    if (bsz == 64 && (DK == 64 || DK == 128) && k_sn_ok)                                                   \
-        hipLaunchKernelGGL((fta_block_score_lse_pipe_kernel<DT, (DK == 64) ? 64 : 128>), dim3(total),     \
-                           dim3(256), 0, st, (const uint16_t*)q, (const uint16_t*)k, qs[0], qs[1], qs[2],  \
-                           ks[0], ks[1], ks[2], H, N, D, M, bsz, pad_head, pad_tail, c, blk_lse, row_lse,  \
-                           qtiles, total, kgroups, tau);                                                   \
+    if (pipe && sb.cand != nullptr && sb.ngroups <= 4)                                                     \
+        FTA_LAUNCH_PIPE(DK, 4, sb.cand, sb.count, sb.tau_key, 0, nullptr);                                 \
+    else if (pipe && sb.cand != nullptr)                                                                   \
+        FTA_LAUNCH_PIPE(DK, 8, sb.cand, sb.count, sb.tau_key, 0, nullptr);                                 \
+    else if (pipe)                                                                                         \
+        FTA_LAUNCH_PIPE(DK, 0, nullptr, nullptr, nullptr, kgroups, tau);                                   \
     else if (bsz <= 64)                                                                                    \
         hipLaunchKernelGGL((fta_block_score_lse_fast_kernel<DT, DK, (DK > 128) ? 1 : 2>), dim3(total),    \
                            dim3(256 * (2 / ((DK > 128) ? 1 : 2))), 0, st,                                \
@@ -1232,21 +1510,22 @@ int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D
         default: return fta::arg_error("block_score: unsupported head dim");
     }
 #undef FTA_LAUNCH_SCORE
+#undef FTA_LAUNCH_PIPE
     return fta::check_launch("fta_block_score_lse_kernel");
 }
 
 int launch_score_lse(const void* q, const void* k, int dtype, int B, int H, int N, int D, const int64_t* qs,
                      const int64_t* ks, int M, int bsz, int pad_head, int pad_tail, float scale, float* blk_lse,
-                     float* row_lse, int kgroups, int32_t* tau, hipStream_t st) {
+                     float* row_lse, int kgroups, int32_t* tau, hipStream_t st, const StreamBufs& sb = StreamBufs()) {
     const int Dk = fta::kernel_head_dim(D);
     if (Dk < 0) return fta::arg_error("block_score: head dim must be <= 256");
     if (D % 8 != 0) return fta::arg_error("block_score: head dim must be a multiple of 8");
     if (dtype == FTA_DTYPE_BF16)
         return launch_score_lse_dt<FTA_DTYPE_BF16>(q, k, B, H, N, D, Dk, qs, ks, M, bsz, pad_head, pad_tail, scale,
-                                                   blk_lse, row_lse, kgroups, tau, st);
+                                                   blk_lse, row_lse, kgroups, tau, sb, st);
     if (dtype == FTA_DTYPE_F16)
         return launch_score_lse_dt<FTA_DTYPE_F16>(q, k, B, H, N, D, Dk, qs, ks, M, bsz, pad_head, pad_tail, scale,
-                                                  blk_lse, row_lse, kgroups, tau, st);
+                                                  blk_lse, row_lse, kgroups, tau, sb, st);
     return fta::arg_error("block_score: dtype must be bf16 or fp16");
 }
 
@@ -1339,8 +1618,14 @@ int fta_topk_select(const float* block_scores, int64_t rows, int M, int64_t stri
     FTA_TRY_END
 }
 
+// Either path's workspace: [BH][M][N] block values + row totals + tau ids, or
+// the candidate streams + row totals + tau keys.
 size_t fta_topk_score_workspace_size(int B, int H, int N, int M) {
-    return fta_block_score_workspace_size(B, H, N, M) + fta::align_up((size_t)B * H * N * sizeof(int32_t));
+    const size_t full = fta_block_score_workspace_size(B, H, N, M) + fta::align_up((size_t)B * H * N * sizeof(int32_t));
+    const size_t w = (size_t)stream_waves(B, H, N);
+    const size_t strm = fta::align_up(w * 64 * M * sizeof(uint2)) + fta::align_up(w * sizeof(int)) +
+                        2 * fta::align_up((size_t)B * H * N * sizeof(float));
+    return full > strm ? full : strm;
 }
 
 int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N, int D, const int64_t* q_strides,
@@ -1355,11 +1640,39 @@ int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N,
     if (max_topk < 0) return fta::arg_error("topk_score: max_topk must be >= 0");
     if (workspace_bytes < fta_topk_score_workspace_size(B, H, N, M))
         return fta::arg_error("topk_score: workspace too small");
+    hipStream_t s = (hipStream_t)stream;
+    const int m_out = (max_topk > 0 && max_topk < M) ? max_topk : M;
+    if (m_out <= kStreamMaxTopk && score_pipe_ok(score_block_size, fta::kernel_head_dim(D), k_strides)) {
+        // candidate streams: no [BH][M][N] intermediate
+        const size_t w = (size_t)stream_waves(B, H, N);
+        char* p = (char*)workspace;
+        StreamBufs sb;
+        sb.cand = (uint2*)p;
+        p += fta::align_up(w * 64 * M * sizeof(uint2));
+        sb.count = (int*)p;
+        p += fta::align_up(w * sizeof(int));
+        float* row_lse = (float*)p;
+        p += fta::align_up((size_t)B * H * N * sizeof(float));
+        sb.tau_key = (float*)p;
+        sb.ngroups = (m_out + 1) / 2;
+        st = launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, pad_tail,
+                              scale, nullptr, row_lse, 0, nullptr, s, sb);
+        if (st != FTA_OK) return st;
+        const int qtiles = (N + 255) / 256;
+#define FTA_LAUNCH_STREAM(KB)                                                                                     \
+    hipLaunchKernelGGL(fta_topk_stream_kernel<KB>, dim3((unsigned)(B * H * qtiles)), dim3(256), 0, s, sb.cand, \
+                       sb.count, sb.tau_key, row_lse, N, qtiles, M, m_out, score_block_size, pad_head, pad_tail,  \
+                       threshold, topk_indices, topk_raw, topk_avg)
+        if (m_out <= 8)
+            FTA_LAUNCH_STREAM(8);
+        else
+            FTA_LAUNCH_STREAM(16);
+#undef FTA_LAUNCH_STREAM
+        return fta::check_launch("fta_topk_stream_kernel");
+    }
     float* blk_lse = (float*)workspace;
     float* row_lse = (float*)((char*)workspace + fta::align_up((size_t)B * H * M * N * sizeof(float)));
-    hipStream_t s = (hipStream_t)stream;
     int32_t* tau = (int32_t*)((char*)workspace + fta_block_score_workspace_size(B, H, N, M));
-    const int m_out = (max_topk > 0 && max_topk < M) ? max_topk : M;
     const int kgroups = (m_out <= 64) ? m_out : 0;
     st = launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, pad_tail,
                           scale, blk_lse, row_lse, kgroups, tau, s);

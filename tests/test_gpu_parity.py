@@ -437,3 +437,66 @@ def test_flash_sparse_attn_func_reference_contract(N, Nphys, H, D, g, b, qph, kv
         assert a.grad.shape == (1, Nphys, H * D)
         assert torch.equal(a.grad[:, :N], c.grad)
         assert not a.grad[:, N:].any()
+
+
+def _pattern_qk(N, H, D, pattern, seed):
+    """q, k [1, N, H*D] bf16 whose block scores follow `pattern` over the blocks:
+    'increasing' / 'decreasing' (every block beats / loses to all earlier ones),
+    'ties' (all 64-key blocks identical, so every block score is exactly equal),
+    'peaked' (config 3's block-centred data) or 'iid'."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    C = H * D
+    if pattern == "peaked":
+        M = N // 64
+        cent = torch.randn(1, M, C, generator=g)
+        k = 0.3 * torch.randn(1, N, C, generator=g) + cent.repeat_interleave(64, dim=1)
+        pick = torch.randint(0, M, (1, N), generator=g)
+        q = 0.3 * torch.randn(1, N, C, generator=g) + torch.gather(cent, 1, pick.unsqueeze(-1).expand(1, N, C))
+    elif pattern == "iid":
+        q, k = torch.randn(1, N, C, generator=g), torch.randn(1, N, C, generator=g)
+    else:
+        u = torch.randn(1, 1, C, generator=g)
+        q = u + 0.1 * torch.randn(1, N, C, generator=g)
+        w = 0.5 * torch.randn(1, 64, C, generator=g)
+        k = w.repeat(1, (N + 63) // 64, 1)[:, :N]
+        if pattern != "ties":
+            j = torch.arange(N).div(64, rounding_mode="floor").float() / max(1, (N - 1) // 64)
+            ramp = j if pattern == "increasing" else 1.0 - j
+            k = k + (1.5 * ramp).view(1, N, 1) * u
+    return q.to(torch.bfloat16).cuda(), k.to(torch.bfloat16).cuda()
+
+
+STREAM_CASES = [
+    # N, H, D, score padding, topk, threshold, pattern
+    (4096, 2, 128, (0, 0), 16, 1.0, "increasing"),
+    (4096, 2, 64, (0, 0), 7, 0.9, "decreasing"),
+    (4096, 1, 128, (0, 0), 16, 1.0, "ties"),
+    (4096, 1, 64, (0, 0), 3, 1.0, "ties"),
+    (1000, 2, 64, (30, 58), 5, 0.95, "iid"),
+    (300, 3, 128, (0, 20), 16, 1.0, "iid"),   # M = 5 < topk: every block is listed
+    (8192, 2, 128, (0, 0), 1, 1.0, "peaked"),
+    (8192, 2, 64, (0, 0), 16, 0.9, "peaked"),
+    (8160, 2, 128, (10, 22), 12, 0.8, "increasing"),
+]
+
+
+@pytest.mark.parametrize("case", STREAM_CASES, ids=lambda c: f"N{c[0]}D{c[2]}k{c[4]}{c[6]}p{c[3][0]}")
+def test_topk_candidate_streams_exact(case):
+    """The pipelined scorer's candidate streams (b = 64, top-k <= 16) drop a
+    block only when enough earlier blocks rank above it: the fused result
+    equals the selection over the full score tensor bit for bit, including
+    adversarial block orders (every block a new maximum), exact ties and
+    partial edge blocks."""
+    N, H, D, pad, topk, thr, pattern = case
+    say(f"[topk streams] {case}")
+    q, k = _pattern_qk(N, H, D, pattern, 31)
+    scores = fta.flash_block_score(q, k, H, 64, pad)
+    fi, fr, fa = fta.flash_topk_score(q, k, H, 64, topk, pad, thr)
+    torch.cuda.synchronize()
+    ri, rr, ra = O.topk_select(scores.cpu().numpy(), thr, topk, 64, pad)
+    np.testing.assert_array_equal(fi.cpu().numpy(), ri)
+    np.testing.assert_array_equal(fr.cpu().numpy(), rr)
+    np.testing.assert_array_equal(fa.cpu().numpy(), ra)
+    if pattern == "increasing" and pad == (0, 0):
+        M = N // 64
+        assert (ri[..., 0] == M - 1).all()
