@@ -3,9 +3,11 @@
 One step = flash_topk_score -> build_qblock_topk_indices -> flash_topk_attn
 forward -> backward, on BASELINE config 3 (B=1, N=32768, H=32, D=128 bf16,
 peaked synthetic attention, b=64, topk=16, threshold=0.9, g=32, W=256).
-Prints one JSON line (driver contract).  Extra fields: per-stage ms, the
-C3-iid variant's forward/backward throughput, the scoring kernel's roofline
-(measured with HIP events on the stream it runs on) and a CPU baseline (the
+Prints one JSON line (driver contract).  Extra fields: the scoring kernel's
+roofline (HIP events on the stream it runs on), `stage_roofline` (every stage
+launched alone through its C entry point and timed with HIP events, with its
+MFMA or HBM fraction of peak), `configs` (the same per-stage figures for the
+C3-iid variant and configs C2, C4 and C5), the V1 rows and a CPU baseline (the
 numpy oracle on a bounded sample, host cores).
 """
 
@@ -24,35 +26,45 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
-# HBM bytes per fta_block_score_lse launch on the default workload (pipelined
-# kernel), from rocprofv3 --pmc FETCH_SIZE (6.544e5 KiB, x2.0) and WRITE_SIZE
-# (2.102e6 KiB, x1.0); the factors are what the same counters read for a 128 MiB
-# device copy (bench.py --only copy).  A PMC pass cannot run inside this process,
-# so the figure is the last measured one and is refreshed with the kernel.
-SCORE_TRAFFIC_BYTES = int((2.0 * 6.544e5 + 1.0 * 2.102e6) * 1024)
+# HBM bytes per launch of the scoring kernel (candidate streams) on the default
+# workload, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of
+# `bench.py --only scorer`, scaled by what the same counters read for a 128 MiB
+# device copy (`--only copy`: FETCH_SIZE x2.0, WRITE_SIZE x1.0).  A PMC pass
+# cannot run inside this process, so this is the last measured figure; it is
+# refreshed whenever the kernel changes.
+SCORE_FETCH_KIB, SCORE_WRITE_KIB = 6.602e5, 1.0e6
+SCORE_TRAFFIC_BYTES = int((2.0 * SCORE_FETCH_KIB + 1.0 * SCORE_WRITE_KIB) * 1024)
 
 
-def make_inputs(B, N, H, D, peaked, seed, dev):
+def make_inputs(B, N, H, D, peaked, seed, dev, dtype=None, scale=1.0):
+    """Synthetic q, k, v [B, N, H*D] generated in fp32 on the CPU (torch.Generator
+    on the CPU, seeded), then cast and moved: the recipe the full-size parity
+    tests use, so the timed data is the checked data.
+
+    peaked=True is config 3: block centres c ~ N(0, 1) per 64-token block,
+    k = 0.3 N(0, 1) + c[token // 64]; per 1024-query segment 8 block ids are
+    drawn without replacement and each query takes one of them uniformly,
+    q = 0.3 N(0, 1) + c[pick]; v ~ N(0, 1).  Otherwise q, k, v ~ scale * N(0, 1).
+    """
     import torch
 
-    g = torch.Generator(device=dev).manual_seed(seed)
+    dtype = dtype or torch.bfloat16
+    g = torch.Generator(device="cpu").manual_seed(seed)
     C = H * D
     if not peaked:
-        q, k, v = (torch.randn(B, N, C, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
-        return q, k, v
+        return tuple((torch.randn(B, N, C, generator=g) * scale).to(dtype).to(dev) for _ in range(3))
     b = 64
     M = N // b
-    cent = torch.randn(B, M, C, generator=g, device=dev)
-    k = 0.3 * torch.randn(B, N, C, generator=g, device=dev) + cent.repeat_interleave(b, dim=1)
+    cent = torch.randn(B, M, C, generator=g)
+    k = 0.3 * torch.randn(B, N, C, generator=g) + cent.repeat_interleave(b, dim=1)
     nseg = N // 1024
-    choice = torch.stack([torch.randperm(M, generator=g, device=dev)[:8] for _ in range(B * nseg)]).view(B, nseg, 8)
-    pick_slot = torch.randint(0, 8, (B, N), generator=g, device=dev)
-    seg = torch.arange(N, device=dev) // 1024
+    choice = torch.stack([torch.randperm(M, generator=g)[:8] for _ in range(B * nseg)]).view(B, nseg, 8)
+    pick_slot = torch.randint(0, 8, (B, N), generator=g)
+    seg = torch.arange(N) // 1024
     pick = torch.gather(choice[:, seg, :], 2, pick_slot.unsqueeze(-1)).squeeze(-1)  # [B, N]
-    q = 0.3 * torch.randn(B, N, C, generator=g, device=dev) + torch.gather(
-        cent, 1, pick.unsqueeze(-1).expand(B, N, C))
-    v = torch.randn(B, N, C, generator=g, device=dev)
-    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    q = 0.3 * torch.randn(B, N, C, generator=g) + torch.gather(cent, 1, pick.unsqueeze(-1).expand(B, N, C))
+    v = torch.randn(B, N, C, generator=g)
+    return tuple(x.to(dtype).to(dev) for x in (q, k, v))
 
 
 def cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, rows, heads):
@@ -146,18 +158,173 @@ def bench_v1(dev, stream):
     return res
 
 
+class Pipeline:
+    """One configuration's inputs, indices and stage launchers (C ABI calls on
+    the current stream), for per-stage HIP-event timing."""
+
+    def __init__(self, dev, B, N, H, D, b, topk, thr, g, W, pad=(0, 0), qpad=(0, 0), peaked=False, seed=0,
+                 dtype=None, scale=1.0, qkv=None):
+        import torch
+
+        import flash_topk_attn_v2 as fta
+        from flash_topk_attn_v2 import _lib
+        from flash_topk_attn_v2.sparse_attn_bwd import preprocess_delta
+
+        self.torch, self.fta, self._lib, self.delta_fn = torch, fta, _lib, preprocess_delta
+        self.dev, self.B, self.N, self.H, self.D, self.b = dev, B, N, H, D, b
+        self.topk, self.thr, self.g, self.W, self.pad, self.qpad = topk, thr, g, W, pad, qpad
+        self.dtype = dtype or torch.bfloat16
+        self.q, self.k, self.v = qkv if qkv is not None else make_inputs(B, N, H, D, peaked, seed, dev, self.dtype,
+                                                                           scale)
+        gd = torch.Generator(device="cpu").manual_seed(seed + 7)
+        self.do = torch.randn(B, N, H * D, generator=gd).to(self.dtype).to(dev)
+        self.stream = torch.cuda.current_stream(dev)
+        self.M = (pad[0] + N + pad[1]) // b
+        self.idx, self.raw, self.avg = fta.flash_topk_score(self.q, self.k, H, b, topk, pad, thr)
+        self.merged, self.counts, self.Wd = fta.build_qblock_topk_indices(self.idx, g, qpad, self.avg, W)
+        self.QM = self.merged.shape[2]
+        self.o, self.lse = fta.flash_topk_attn(self.q, self.k, self.v, self.merged, self.counts, H, g, b,
+                                               None, None, pad, qpad)
+        self.delta = preprocess_delta(self.o, self.do, H)
+        L = _lib.lib()
+        self.L = L
+        self.st = _lib.i64arr([N * H * D, D, H * D])
+        self.dt = _lib.dtype_code(self.dtype)
+        m_out = topk if 0 < topk < self.M else self.M
+        self.m_out = m_out
+        self.ws_score = _lib.workspace(L.fta_topk_score_workspace_size(B, H, N, self.M), dev)
+        geo = (B, H, N, D, g, b, qpad[0], qpad[1], pad[0], pad[1])
+        self.ws_bwd = _lib.workspace(L.fta_sparse_attn_bwd_workspace_size(*geo), dev)
+        self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
+        self.streams_ok = b == 64 and D in (64, 128) and m_out <= 16
+
+    # --- stage launchers
+    def score(self):
+        self.fta.flash_topk_score(self.q, self.k, self.H, self.b, self.topk, self.pad, self.thr)
+
+    def scorer(self):
+        L, _lib = self.L, self._lib
+        rc = L.fta_topk_score_candidates(self.q.data_ptr(), self.k.data_ptr(), self.dt, self.B, self.H, self.N,
+                                         self.D, self.st, self.st, self.b, self.pad[0], self.pad[1], self.D ** -0.5,
+                                         self.topk, self.ws_score.data_ptr(), self.ws_score.numel(),
+                                         self.stream.cuda_stream)
+        _lib.check(rc, "fta_topk_score_candidates")
+
+    def merge(self):
+        self.fta.build_qblock_topk_indices(self.idx, self.g, self.qpad, self.avg, self.W)
+
+    def fwd(self):
+        self.fta.flash_topk_attn(self.q, self.k, self.v, self.merged, self.counts, self.H, self.g, self.b,
+                                 None, None, self.pad, self.qpad)
+
+    def delta_stage(self):
+        self.delta_fn(self.o, self.do, self.H)
+
+    def _bwd_args(self):
+        s = self.st
+        return (self.q.data_ptr(), s, self.k.data_ptr(), s, self.v.data_ptr(), s, self.do.data_ptr(), s, self.dt,
+                self.B, self.H, self.H, self.N, self.D, self.merged.data_ptr(), self.QM, self.merged.shape[3],
+                self.g, self.b, self.qpad[0], self.qpad[1], self.pad[0], self.pad[1], self.D ** -0.5,
+                self.lse.data_ptr(), self.delta.data_ptr())
+
+    def dq_stage(self):
+        rc = self.L.fta_sparse_attn_bwd_dq(*self._bwd_args(), self.dq.data_ptr(), self.st, self.stream.cuda_stream)
+        self._lib.check(rc, "fta_sparse_attn_bwd_dq")
+
+    def dkv_stage(self):
+        rc = self.L.fta_sparse_attn_bwd_dkv(*self._bwd_args(), self.dk.data_ptr(), self.st, self.dv.data_ptr(),
+                                            self.st, self.ws_bwd.data_ptr(), self.ws_bwd.numel(),
+                                            self.stream.cuda_stream)
+        self._lib.check(rc, "fta_sparse_attn_bwd_dkv")
+
+    # --- measurement
+    def time(self, fn, reps=5):
+        """Mean ms per call over `reps` back-to-back calls, HIP events on the stream."""
+        torch = self.torch
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(self.stream)
+        for _ in range(reps):
+            fn()
+        e1.record(self.stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    def pairs(self):
+        """P = sum over (b, h, q-block) of valid query rows x valid KV tokens of the listed blocks."""
+        torch = self.torch
+        N, g, b = self.N, self.g, self.b
+        qs = torch.arange(self.QM, device=self.dev) * g - self.qpad[0]
+        qvalid = (torch.clamp(qs + g, max=N) - torch.clamp(qs, min=0)).clamp(min=0).float()
+        ks = torch.arange(self.M, device=self.dev) * b - self.pad[0]
+        kvalid = (torch.clamp(ks + b, max=N) - torch.clamp(ks, min=0)).clamp(min=0).float()
+        m = self.merged.long()
+        tok = torch.where(m >= 0, kvalid[m.clamp(min=0)], torch.zeros((), device=self.dev)).sum(-1)  # [B,H,QM]
+        return float((tok * qvalid).sum().item())
+
+    def selector_bytes(self):
+        """Bytes the stream selector moves: candidate entries read (8 B each), the
+        row total and start bound (8 B per row) and the three outputs."""
+        rows = self.B * self.H * self.N
+        waves = self.B * self.H * ((self.N + 255) // 256) * 4
+        off = -(-waves * 64 * self.M * 8 // 256) * 256
+        cnt = self.ws_score[off: off + waves * 4].view(self.torch.int32)
+        return float(cnt.sum().item()) * 8 + rows * 8 + rows * self.m_out * 12
+
+    def stages(self, bwd=True, reps=5):
+        """Per-stage ms and roofline fractions."""
+        B, H, N, D, b, g = self.B, self.H, self.N, self.D, self.b, self.g
+        P = self.pairs()
+        r = {}
+        f_score = 2.0 * B * H * N * N * D
+        t_score = self.time(self.score, reps)
+        r["score"] = {"ms": t_score, "tflops": f_score / t_score / 1e9}
+        if self.streams_ok:
+            t_k = self.time(self.scorer, reps)
+            sel_ms = max(t_score - t_k, 1e-6)
+            r["score_kernel"] = {"ms": t_k, "bound": "mfma", "tflops": f_score / t_k / 1e9,
+                                 "frac": f_score / t_k / 1e9 / PEAK_BF16_TFLOPS}
+            sb = self.selector_bytes()
+            r["topk_select"] = {"ms": sel_ms, "bound": "hbm", "gbs": sb / sel_ms / 1e6,
+                                "frac": sb / sel_ms / 1e6 / PEAK_HBM_GBS, "bytes": sb,
+                                "note": "score stage minus the scoring kernel alone"}
+        K = self.idx.shape[-1]
+        mb = 2.0 * B * H * N * K * 4 + B * H * self.QM * (self.merged.shape[3] + 1) * 4
+        t = self.time(self.merge, reps)
+        r["merge"] = {"ms": t, "bound": "hbm", "gbs": mb / t / 1e6, "frac": mb / t / 1e6 / PEAK_HBM_GBS}
+        t = self.time(self.fwd, reps)
+        r["fwd"] = {"ms": t, "bound": "mfma", "tflops": 4 * D * P / t / 1e9,
+                    "frac": 4 * D * P / t / 1e9 / PEAK_BF16_TFLOPS}
+        r["P_pairs"] = P
+        if bwd:
+            db = 2.0 * B * N * H * D * 2 + B * H * N * 4
+            t_d = self.time(self.delta_stage, reps)
+            r["delta"] = {"ms": t_d, "bound": "hbm", "gbs": db / t_d / 1e6, "frac": db / t_d / 1e6 / PEAK_HBM_GBS}
+            t_q = self.time(self.dq_stage, reps)
+            r["dq"] = {"ms": t_q, "bound": "mfma", "tflops_executed_6DP": 6 * D * P / t_q / 1e9,
+                       "frac": 6 * D * P / t_q / 1e9 / PEAK_BF16_TFLOPS}
+            t_kv = self.time(self.dkv_stage, reps)
+            r["dkv"] = {"ms": t_kv, "bound": "mfma", "tflops_executed_8DP": 8 * D * P / t_kv / 1e9,
+                        "frac": 8 * D * P / t_kv / 1e9 / PEAK_BF16_TFLOPS,
+                        "note": "includes the membership bitmap and log2-lse kernels"}
+            t_b = t_d + t_q + t_kv
+            r["bwd"] = {"ms": t_b, "tflops_10DP": 10 * D * P / t_b / 1e9,
+                        "frac": 10 * D * P / t_b / 1e9 / PEAK_BF16_TFLOPS}
+        return {k2: ({kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v2.items()}
+                     if isinstance(v2, dict) else v2) for k2, v2 in r.items()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-iid", action="store_true")
-    ap.add_argument("--no-v1", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C3-iid, C2, C4, C5 and V1 rows")
     ap.add_argument("--cpu-rows", type=int, default=32768)
     ap.add_argument("--cpu-heads", type=int, default=2)
-    ap.add_argument("--only", choices=["score", "topk", "merge", "fwd", "bwd", "copy", "v1"], default=None,
-                    help="profiling aid: run one stage of the C3 step --steps times and exit")
+    ap.add_argument("--only", choices=["score", "scorer", "topk", "merge", "fwd", "bwd", "dq", "dkv", "copy", "v1"],
+                    default=None, help="profiling aid: run one stage of the C3 step --steps times and exit")
     ap.add_argument("--iid", action="store_true",
                     help="with --only: the C3-iid variant (iid q/k/v, threshold 1.0, qblock_topk 512)")
     args = ap.parse_args()
@@ -169,7 +336,6 @@ def main():
     import torch
 
     import flash_topk_attn_v2 as fta
-    from flash_topk_attn_v2 import _lib
 
     dev = torch.device("cuda:0")
     if args.only == "v1":  # the V1 benchmark rows alone (profiling aid)
@@ -179,62 +345,36 @@ def main():
         print(json.dumps({"only": "v1", "steps": args.steps}), flush=True)
         return
     B, N, H, D, b, topk, thr, g, W = 1, 32768, 32, 128, 64, 16, 0.9, 32, 256
-    q, k, v = make_inputs(B, N, H, D, True, 2, dev)
-    gd = torch.Generator(device=dev).manual_seed(7)
-    do = torch.randn(B, N, H * D, generator=gd, device=dev).to(torch.bfloat16)
-    ql, kl, vl = (t.detach().requires_grad_(True) for t in (q, k, v))
-
     stream = torch.cuda.current_stream(dev)
-
-    def step(record=None):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)] if record is not None else None
-        ql.grad = kl.grad = vl.grad = None
-        if ev: ev[0].record(stream)
-        idx, raw, avg = fta.flash_topk_score(ql.detach(), kl.detach(), H, b, topk, (0, 0), thr)
-        if ev: ev[1].record(stream)
-        merged, counts, Wd = fta.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
-        if ev: ev[2].record(stream)
-        o, lse = fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, b)
-        if ev: ev[3].record(stream)
-        o.backward(do)
-        if ev:
-            ev[4].record(stream)
-            record.append(ev)
-        return counts
 
     if args.only:
         if args.iid:
-            thr, W = 1.0, 512
-            q, k, v = make_inputs(B, N, H, D, False, 3, dev)
-            ql, kl, vl = (t.detach().requires_grad_(True) for t in (q, k, v))
-        idx, raw, avg = fta.flash_topk_score(q, k, H, b, topk, (0, 0), thr)
-        merged, counts, Wd = fta.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
-        o, lse = fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, b)
-        M_ = N // b
-        blk = torch.empty(B * H * M_ * N, device=dev, dtype=torch.float32)
-        row = torch.empty(B * H * N, device=dev, dtype=torch.float32)
-        sst = _lib.i64arr([N * H * D, D, H * D])
+            pl = Pipeline(dev, B, N, H, D, b, topk, 1.0, g, 512, peaked=False, seed=3)
+        else:
+            pl = Pipeline(dev, B, N, H, D, b, topk, thr, g, W, peaked=True, seed=2)
         big = torch.empty(256 << 20, device=dev, dtype=torch.uint8)
+        fn = {"score": pl.score, "scorer": pl.scorer, "topk": pl.score, "merge": pl.merge, "fwd": pl.fwd,
+              "dq": pl.dq_stage, "dkv": pl.dkv_stage,
+              "bwd": lambda: (pl.delta_stage(), pl.dq_stage(), pl.dkv_stage()),
+              "copy": lambda: big[: 128 << 20].copy_(big[128 << 20:])}[args.only]
         for _ in range(args.steps):
-            if args.only == "score":
-                _lib.check(_lib.lib().fta_block_score_lse(q.data_ptr(), k.data_ptr(), 0, B, H, N, D, sst, sst, b, 0, 0,
-                                                          D ** -0.5, blk.data_ptr(), row.data_ptr(),
-                                                          stream.cuda_stream), "score")
-            elif args.only == "topk":
-                fta.flash_topk_score(q, k, H, b, topk, (0, 0), thr)
-            elif args.only == "merge":
-                fta.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
-            elif args.only == "fwd":
-                fta.flash_topk_attn(q, k, v, merged, counts, H, g, b)
-            elif args.only == "bwd":
-                ql.grad = kl.grad = vl.grad = None
-                o, lse = fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, b)
-                o.backward(do)
-            else:  # plain copy of 256 MiB: calibrates FETCH_SIZE / WRITE_SIZE
-                big[: 128 << 20].copy_(big[128 << 20:])
+            fn()
         torch.cuda.synchronize()
         print(json.dumps({"only": args.only, "steps": args.steps}), flush=True)
         return
+
+    q, k, v = make_inputs(B, N, H, D, True, 2, dev)
+    gd = torch.Generator(device="cpu").manual_seed(7)
+    do = torch.randn(B, N, H * D, generator=gd).to(torch.bfloat16).to(dev)
+    ql, kl, vl = (t.detach().requires_grad_(True) for t in (q, k, v))
+
+    def step():
+        ql.grad = kl.grad = vl.grad = None
+        idx, raw, avg = fta.flash_topk_score(ql.detach(), kl.detach(), H, b, topk, (0, 0), thr)
+        merged, counts, Wd = fta.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
+        o, lse = fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, b)
+        o.backward(do)
+        return counts
 
     for _ in range(args.warmup):
         step()
@@ -245,42 +385,20 @@ def main():
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
 
-    recs = []
-    for _ in range(3):
-        counts = step(recs)
-    torch.cuda.synchronize()
-    names = ["score", "merge", "fwd", "bwd"]
-    stage = {n: sorted(r[i].elapsed_time(r[i + 1]) for r in recs)[1] for i, n in enumerate(names)}
-
     P = g * b * float(counts.sum().item())
     f_score = 2.0 * B * H * N * N * D
     f_fwd, f_bwd = 4.0 * D * P, 10.0 * D * P
     flops = f_score + f_fwd + f_bwd
     value = flops / (ms * 1e-3) / 1e12
 
-    # dominant kernel: scoring stage 1 (fta_block_score_lse_kernel), timed alone
-    M = N // b
-    blk = torch.empty(B * H * M * N, device=dev, dtype=torch.float32)
-    row = torch.empty(B * H * N, device=dev, dtype=torch.float32)
-    qs = _lib.i64arr([N * H * D, D, H * D])
-    L = _lib.lib()
-
-    def score_lse():
-        rc = L.fta_block_score_lse(q.data_ptr(), k.data_ptr(), 0, B, H, N, D, qs, qs, b, 0, 0, D ** -0.5,
-                                   blk.data_ptr(), row.data_ptr(), stream.cuda_stream)
-        _lib.check(rc, "fta_block_score_lse")
-
-    score_lse()
-    reps = 10
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(reps):
-        score_lse()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    k_ms = e0.elapsed_time(e1) / reps
+    # per-stage times and rooflines, each stage launched alone (HIP events on the stream)
+    pl = Pipeline(dev, B, N, H, D, b, topk, thr, g, W, qkv=(q, k, v), seed=0)
+    pl.do = do
+    pl.delta = pl.delta_fn(pl.o, do, H)
+    stages = pl.stages(bwd=True)
+    # dominant kernel: the scoring kernel (candidate streams), 10 launches
+    k_ms = pl.time(pl.scorer, reps=10)
     achieved = f_score / (k_ms * 1e-3) / 1e12
-    del blk, row
 
     out = {
         "metric": "score+attn fwd+bwd ms and TFLOP/s at N=32K,D=128 bf16; % of MFMA peak",
@@ -294,49 +412,63 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (BASELINE config 3: peaked block-centred q/k, iid v, seed 2)",
+        "data": "synthetic (BASELINE config 3: peaked block-centred q/k, iid v, CPU generator seed 2)",
         "config": {"workload": "C3 threshold: B1 N32768 H32 D128, b64 topk16 thr0.9 g32 W256; "
                                "score+merge+sparse fwd+bwd",
                    "global_batch": B, "seq_len": N, "heads": H, "head_dim": D, "parallelism": "none"},
-        "stage_ms": {k2: round(v2, 3) for k2, v2 in stage.items()},
         "flops": {"score": f_score, "fwd": f_fwd, "bwd_10DP": f_bwd, "P_pairs": P},
-        "roofline": {"bound": "mfma", "kernel": "fta_block_score_lse_pipe_kernel", "achieved": round(achieved, 2),
-                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "kernel_ms": round(k_ms, 3),
-                     "traffic": SCORE_TRAFFIC_BYTES if (B, N, H, D, b) == (1, 32768, 32, 128, 64) else None,
-                     "algorithmic_bytes": 2 * B * H * N * D * 2 + 4 * B * H * (M + 1) * N},
+        "roofline": {"bound": "mfma", "kernel": "fta_block_score_lse_pipe_kernel (candidate streams)",
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "kernel_ms": round(k_ms, 3),
+                     "traffic": SCORE_TRAFFIC_BYTES,
+                     "algorithmic_bytes": 2 * B * H * N * D * 2},
+        "stage_roofline": stages,
     }
+    del pl, ql, kl, vl
+    torch.cuda.empty_cache()
 
-    if not args.no_iid:
-        # C3-iid variant (the MFMA gate for the sparse forward/backward)
-        del ql, kl, vl
+    if not args.no_extra:
+        extra = {}
+        # C3-iid: the MFMA gate for the sparse forward / backward (threshold 1.0, W 512)
+        pl = Pipeline(dev, B, N, H, D, b, topk, 1.0, g, 512, peaked=False, seed=3)
+        extra["C3_iid"] = pl.stages(bwd=True, reps=3)
+        extra["C3_iid"]["mean_count"] = float(pl.counts.float().mean().item())
+        del pl
         torch.cuda.empty_cache()
-        qi, ki, vi = make_inputs(B, N, H, D, False, 3, dev)
-        idx, raw, avg = fta.flash_topk_score(qi, ki, H, b, topk, (0, 0), 1.0)
-        merged, counts_i, _ = fta.build_qblock_topk_indices(idx, g, (0, 0), avg, 512)
-        qi.requires_grad_(True)
-        ki.requires_grad_(True)
-        vi.requires_grad_(True)
-        fw, bw = [], []
-        for it in range(4):
+        # C2: B2 N8192 H16 D64 fp16, top-16, g = 1 (W 16) and g = 32 (W 512), forward only
+        for name, gg, ww in (("C2_g1", 1, 16), ("C2_g32", 32, 512)):
+            pl = Pipeline(dev, 2, 8192, 16, 64, 64, 16, 1.0, gg, ww, peaked=False, seed=1, dtype=torch.float16)
+            extra[name] = pl.stages(bwd=False)
+            del pl
+        # C4: virtual padding, B2 N10000 H12 D64 fp16, padding (24, 24), top-8, g 16, forward + backward
+        pl = Pipeline(dev, 2, 10000, 12, 64, 64, 8, 1.0, 16, None, pad=(24, 24), peaked=False, seed=4,
+                      dtype=torch.float16)
+        extra["C4"] = pl.stages(bwd=True)
+        del pl
+        # C5: training, B1 N16384 H16 D128, q/k/v ~ N(0, 1) / sqrt(D); indices from layer 0 reused by 4 layers
+        pl = Pipeline(dev, 1, 16384, 16, 128, 64, 16, 1.0, 32, 512, peaked=False, seed=5, scale=D ** -0.5)
+        layers = []
+        for layer in range(4):
+            ql5, kl5, vl5 = (t.requires_grad_(True) for t in make_inputs(1, 16384, 16, 128, False, 50 + layer, dev,
+                                                                          scale=D ** -0.5))
             e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
             e[0].record(stream)
-            o, lse = fta.flash_topk_attn(qi, ki, vi, merged, counts_i, H, g, b)
+            o5, _ = fta.flash_topk_attn(ql5, kl5, vl5, pl.merged, pl.counts, 16, 32, 64)
             e[1].record(stream)
-            o.backward(do)
+            o5.backward(pl.do)
             e[2].record(stream)
             torch.cuda.synchronize()
-            if it:
-                fw.append(e[0].elapsed_time(e[1]))
-                bw.append(e[1].elapsed_time(e[2]))
-        Pi = g * b * float(counts_i.sum().item())
-        fms, bms = sorted(fw)[1], sorted(bw)[1]
-        out["c3_iid"] = {"fwd_ms": round(fms, 3), "bwd_ms": round(bms, 3),
-                         "fwd_tflops": round(4 * D * Pi / fms / 1e9, 2),
-                         "bwd_tflops_10DP": round(10 * D * Pi / bms / 1e9, 2),
-                         "mean_count": Pi / (g * b * B * H * (N // g))}
-
-    if not args.no_v1:
+            layers.append((e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])))
+        P5 = pl.pairs()
+        fw5 = sum(x[0] for x in layers[1:]) / 3
+        bw5 = sum(x[1] for x in layers[1:]) / 3
+        extra["C5"] = {"score_merge": pl.stages(bwd=False), "layers": 4, "P_pairs": P5,
+                       "fwd_ms_per_layer": round(fw5, 4), "bwd_ms_per_layer": round(bw5, 4),
+                       "fwd_frac": round(4 * 128 * P5 / fw5 / 1e9 / PEAK_BF16_TFLOPS, 4),
+                       "bwd_frac_10DP": round(10 * 128 * P5 / bw5 / 1e9 / PEAK_BF16_TFLOPS, 4)}
+        del pl
+        torch.cuda.empty_cache()
+        out["configs"] = extra
         out["v1_score"] = bench_v1(dev, stream)
 
     if not args.no_cpu:

@@ -1962,32 +1962,23 @@ size_t fta_sparse_attn_bwd_workspace_size(int B, int H, int N, int D, int q_bloc
     return bwd_bytes(B, H, N, G);  // membership bitmap KV block -> q-blocks, lse in log2 units
 }
 
-int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
-                            const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
-                            int dtype, int B, int H, int Hk, int N, int D, const int32_t* merged_indices, int QM,
-                            int W, int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail,
-                            int kv_pad_head, int kv_pad_tail, float scale, const float* lse, const float* delta,
-                            void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
-                            const int64_t* dv_strides, void* workspace, size_t workspace_bytes, void* stream) {
-    FTA_TRY_BEGIN
+}  // extern "C"
+
+namespace {
+// Arguments shared by the dQ and dK/dV launches (geometry checked here).
+int bwd_common(AttnArgs& a, Geo& G, const void* q, const int64_t* q_strides, const void* k,
+               const int64_t* k_strides, const void* v, const int64_t* v_strides, const void* dout,
+               const int64_t* do_strides, int B, int H, int Hk, int N, int D, const int32_t* merged_indices, int QM,
+               int W, int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head,
+               int kv_pad_tail, float scale, const float* lse, const float* delta) {
     if (Hk <= 0 || H % Hk != 0)
         return fta::arg_error("sparse_attn_bwd: num_heads must be a multiple of num_kv_heads");
-    Geo G;
     int rc = geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
                       &G);
     if (rc != FTA_OK) return rc;
     if (W <= 0) return fta::arg_error("sparse_attn_bwd: qblock_topk must be positive");
     if (G.Mkv > 0x3fffffff / 32) return fta::unsupported("sparse_attn_bwd: too many KV blocks");
-    if (workspace_bytes < bwd_bytes(B, H, N, G)) return fta::arg_error("sparse_attn_bwd: workspace too small");
-    hipStream_t st = (hipStream_t)stream;
-    uint32_t* sel = (uint32_t*)workspace;
-    if ((rc = fta::launch_sel_bitmap(merged_indices, B * H, QM, W, G.Mkv, sel, st)) != FTA_OK) return rc;
-    float* lse2 = (float*)((char*)workspace + sel_bytes(B, H, G));
-    const int64_t nl = (int64_t)B * H * N;
-    hipLaunchKernelGGL(fta_lse2_kernel, dim3((unsigned)((nl + 255) / 256)), dim3(256), 0, st, lse, lse2, nl);
-    if ((rc = fta::check_launch("fta_lse2_kernel")) != FTA_OK) return rc;
-
-    AttnArgs a = {};
+    a = AttnArgs{};
     a.q = (const uint16_t*)q;
     a.q_sb = q_strides[0];
     a.q_sh = q_strides[1];
@@ -2005,16 +1996,32 @@ int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void*
     a.d_sh = do_strides[1];
     a.d_sn = do_strides[2];
     a.merged = merged_indices;
-    a.sel = sel;
     a.W = W;
     a.lse_in = lse;
-    a.lse2_in = lse2;
     a.delta_in = delta;
     fill_common(a, H, N, D, q_block_size, kv_block_size, q_pad_head, kv_pad_head, scale, G);
     a.Hk = Hk;
     a.G = H / Hk;
+    return FTA_OK;
+}
+}  // namespace
 
-    // dQ
+extern "C" {
+
+int fta_sparse_attn_bwd_dq(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                           const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
+                           int dtype, int B, int H, int Hk, int N, int D, const int32_t* merged_indices, int QM, int W,
+                           int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head,
+                           int kv_pad_tail, float scale, const float* lse, const float* delta, void* dq,
+                           const int64_t* dq_strides, void* stream) {
+    FTA_TRY_BEGIN
+    AttnArgs a;
+    Geo G;
+    int rc = bwd_common(a, G, q, q_strides, k, k_strides, v, v_strides, dout, do_strides, B, H, Hk, N, D,
+                        merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head,
+                        kv_pad_tail, scale, lse, delta);
+    if (rc != FTA_OK) return rc;
+    hipStream_t st = (hipStream_t)stream;
     a.out0 = (uint16_t*)dq;
     a.o0_sb = dq_strides[0];
     a.o0_sh = dq_strides[1];
@@ -2022,15 +2029,39 @@ int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void*
     const int Tq = (G.Dk <= 128) ? 8 : 4;  // query tiles per dQ workgroup
     a.wg_per_bh = (G.Npq + 32 * Tq - 1) / (32 * Tq);
     a.total = a.wg_per_bh * B * H;
-    if (dtype == FTA_DTYPE_BF16)
-        rc = launch_dq_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);
-    else if (dtype == FTA_DTYPE_F16)
-        rc = launch_dq_dt<FTA_DTYPE_F16>(a, G.Dk, a.total, st);
-    else
-        rc = fta::arg_error("sparse_attn_bwd: dtype must be bf16 or fp16");
-    if (rc != FTA_OK) return rc;
+    if (dtype == FTA_DTYPE_BF16) return launch_dq_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);
+    if (dtype == FTA_DTYPE_F16) return launch_dq_dt<FTA_DTYPE_F16>(a, G.Dk, a.total, st);
+    return fta::arg_error("sparse_attn_bwd: dtype must be bf16 or fp16");
+    FTA_TRY_END
+}
 
-    // dK, dV
+int fta_sparse_attn_bwd_dkv(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                            const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
+                            int dtype, int B, int H, int Hk, int N, int D, const int32_t* merged_indices, int QM,
+                            int W, int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail,
+                            int kv_pad_head, int kv_pad_tail, float scale, const float* lse, const float* delta,
+                            void* dk, const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+    FTA_TRY_BEGIN
+    AttnArgs a;
+    Geo G;
+    int rc = bwd_common(a, G, q, q_strides, k, k_strides, v, v_strides, dout, do_strides, B, H, Hk, N, D,
+                        merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head,
+                        kv_pad_tail, scale, lse, delta);
+    if (rc != FTA_OK) return rc;
+    if (dtype != FTA_DTYPE_BF16 && dtype != FTA_DTYPE_F16)
+        return fta::arg_error("sparse_attn_bwd: dtype must be bf16 or fp16");
+    if (workspace_bytes < bwd_bytes(B, H, N, G)) return fta::arg_error("sparse_attn_bwd: workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    // membership bitmap (KV block -> q-blocks) and lse in log2 units, in the workspace
+    uint32_t* sel = (uint32_t*)workspace;
+    if ((rc = fta::launch_sel_bitmap(merged_indices, B * H, QM, W, G.Mkv, sel, st)) != FTA_OK) return rc;
+    float* lse2 = (float*)((char*)workspace + sel_bytes(B, H, G));
+    const int64_t nl = (int64_t)B * H * N;
+    hipLaunchKernelGGL(fta_lse2_kernel, dim3((unsigned)((nl + 255) / 256)), dim3(256), 0, st, lse, lse2, nl);
+    if ((rc = fta::check_launch("fta_lse2_kernel")) != FTA_OK) return rc;
+    a.sel = sel;
+    a.lse2_in = lse2;
     a.out0 = (uint16_t*)dk;
     a.o0_sb = dk_strides[0];
     a.o0_sh = dk_strides[1];
@@ -2045,6 +2076,23 @@ int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void*
     if (dtype == FTA_DTYPE_BF16) return launch_dkv_dt<FTA_DTYPE_BF16>(a, G.Dk, Tb, B, Hk, ntiles, st);
     return launch_dkv_dt<FTA_DTYPE_F16>(a, G.Dk, Tb, B, Hk, ntiles, st);
     FTA_TRY_END
+}
+
+int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                            const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
+                            int dtype, int B, int H, int Hk, int N, int D, const int32_t* merged_indices, int QM,
+                            int W, int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail,
+                            int kv_pad_head, int kv_pad_tail, float scale, const float* lse, const float* delta,
+                            void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                            const int64_t* dv_strides, void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = fta_sparse_attn_bwd_dq(q, q_strides, k, k_strides, v, v_strides, dout, do_strides, dtype, B, H, Hk, N, D,
+                                    merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail,
+                                    kv_pad_head, kv_pad_tail, scale, lse, delta, dq, dq_strides, stream);
+    if (rc != FTA_OK) return rc;
+    return fta_sparse_attn_bwd_dkv(q, q_strides, k, k_strides, v, v_strides, dout, do_strides, dtype, B, H, Hk, N, D,
+                                   merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail,
+                                   kv_pad_head, kv_pad_tail, scale, lse, delta, dk, dk_strides, dv, dv_strides,
+                                   workspace, workspace_bytes, stream);
 }
 
 int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,

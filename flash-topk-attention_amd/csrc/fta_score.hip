@@ -1628,33 +1628,72 @@ size_t fta_topk_score_workspace_size(int B, int H, int N, int M) {
     return full > strm ? full : strm;
 }
 
+}  // extern "C"
+
+namespace {
+// fta_topk_score's workspace as candidate streams: entries, per-wave counts,
+// row totals, tau keys (in that order).
+StreamBufs stream_layout(void* workspace, int B, int H, int N, int M, int m_out, float** row_lse) {
+    const size_t w = (size_t)stream_waves(B, H, N);
+    char* p = (char*)workspace;
+    StreamBufs sb;
+    sb.cand = (uint2*)p;
+    p += fta::align_up(w * 64 * M * sizeof(uint2));
+    sb.count = (int*)p;
+    p += fta::align_up(w * sizeof(int));
+    *row_lse = (float*)p;
+    p += fta::align_up((size_t)B * H * N * sizeof(float));
+    sb.tau_key = (float*)p;
+    sb.ngroups = (m_out + 1) / 2;
+    return sb;
+}
+
+// Shared checks of fta_topk_score and fta_topk_score_candidates; sets M and m_out.
+int topk_score_checks(int B, int H, int N, int D, int bsz, int pad_head, int pad_tail, int max_topk,
+                      size_t workspace_bytes, int* M, int* m_out) {
+    int st = fta::check_score_args(B, H, N, D, bsz, pad_head, pad_tail, M);
+    if (st != FTA_OK) return st;
+    if (*M > 4096) return fta::unsupported("topk_score: M exceeds 4096");
+    if (max_topk < 0) return fta::arg_error("topk_score: max_topk must be >= 0");
+    if (workspace_bytes < fta_topk_score_workspace_size(B, H, N, *M))
+        return fta::arg_error("topk_score: workspace too small");
+    *m_out = (max_topk > 0 && max_topk < *M) ? max_topk : *M;
+    return FTA_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int fta_topk_score_candidates(const void* q, const void* k, int dtype, int B, int H, int N, int D,
+                              const int64_t* q_strides, const int64_t* k_strides, int score_block_size, int pad_head,
+                              int pad_tail, float scale, int max_topk, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+    FTA_TRY_BEGIN
+    int M = 0, m_out = 0;
+    int st = topk_score_checks(B, H, N, D, score_block_size, pad_head, pad_tail, max_topk, workspace_bytes, &M, &m_out);
+    if (st != FTA_OK) return st;
+    if (!(m_out <= kStreamMaxTopk && score_pipe_ok(score_block_size, fta::kernel_head_dim(D), k_strides)))
+        return fta::unsupported("topk_score_candidates: needs b = 64, D <= 128 and at most 16 blocks per query");
+    float* row_lse = nullptr;
+    const StreamBufs sb = stream_layout(workspace, B, H, N, M, m_out, &row_lse);
+    return launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, pad_tail,
+                            scale, nullptr, row_lse, 0, nullptr, (hipStream_t)stream, sb);
+    FTA_TRY_END
+}
+
 int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N, int D, const int64_t* q_strides,
                    const int64_t* k_strides, int score_block_size, int pad_head, int pad_tail, float scale,
                    int max_topk, float threshold, int32_t* topk_indices, float* topk_raw, float* topk_avg,
                    void* workspace, size_t workspace_bytes, void* stream) {
     FTA_TRY_BEGIN
-    int M = 0;
-    int st = fta::check_score_args(B, H, N, D, score_block_size, pad_head, pad_tail, &M);
+    int M = 0, m_out = 0;
+    int st = topk_score_checks(B, H, N, D, score_block_size, pad_head, pad_tail, max_topk, workspace_bytes, &M, &m_out);
     if (st != FTA_OK) return st;
-    if (M > 4096) return fta::unsupported("topk_score: M exceeds 4096");
-    if (max_topk < 0) return fta::arg_error("topk_score: max_topk must be >= 0");
-    if (workspace_bytes < fta_topk_score_workspace_size(B, H, N, M))
-        return fta::arg_error("topk_score: workspace too small");
     hipStream_t s = (hipStream_t)stream;
-    const int m_out = (max_topk > 0 && max_topk < M) ? max_topk : M;
     if (m_out <= kStreamMaxTopk && score_pipe_ok(score_block_size, fta::kernel_head_dim(D), k_strides)) {
         // candidate streams: no [BH][M][N] intermediate
-        const size_t w = (size_t)stream_waves(B, H, N);
-        char* p = (char*)workspace;
-        StreamBufs sb;
-        sb.cand = (uint2*)p;
-        p += fta::align_up(w * 64 * M * sizeof(uint2));
-        sb.count = (int*)p;
-        p += fta::align_up(w * sizeof(int));
-        float* row_lse = (float*)p;
-        p += fta::align_up((size_t)B * H * N * sizeof(float));
-        sb.tau_key = (float*)p;
-        sb.ngroups = (m_out + 1) / 2;
+        float* row_lse = nullptr;
+        const StreamBufs sb = stream_layout(workspace, B, H, N, M, m_out, &row_lse);
         st = launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, pad_tail,
                               scale, nullptr, row_lse, 0, nullptr, s, sb);
         if (st != FTA_OK) return st;

@@ -40,6 +40,7 @@ _SIGNATURES = {
     "fta_topk_score_workspace_size": (_sz, [_i, _i, _i, _i]),
     "fta_topk_score": (_i, [_p, _p, _i, _i, _i, _i, _i, _i64p, _i64p, _i, _i, _i, _f, _i, _f, _p, _p, _p, _p,
                             _sz, _p]),
+    "fta_topk_score_candidates": (_i, [_p, _p, _i, _i, _i, _i, _i, _i64p, _i64p, _i, _i, _i, _f, _i, _p, _sz, _p]),
     "fta_qblock_merge": (_i, [_p, _p, _i64, _i, _i, _i, _i, _p, _p, _p, _p]),
     "fta_qblock_merge_maxid": (_i, [_p, _p, _i64, _i, _i, _p, _i, _p, _p, _p, _p]),
     "fta_qblock_union": (_i, [_p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p]),
@@ -58,6 +59,10 @@ _SIGNATURES = {
     "fta_sparse_attn_bwd_gqa": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _i, _p, _i,
                                      _i, _i, _i, _i, _i, _i, _i, _f, _p, _p, _p, _i64p, _p, _i64p, _p, _i64p, _p,
                                      _sz, _p]),
+    "fta_sparse_attn_bwd_dq": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _i, _p, _i, _i,
+                                    _i, _i, _i, _i, _i, _i, _f, _p, _p, _p, _i64p, _p]),
+    "fta_sparse_attn_bwd_dkv": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _i, _p, _i,
+                                     _i, _i, _i, _i, _i, _i, _i, _f, _p, _p, _p, _i64p, _p, _i64p, _p, _sz, _p]),
     "fta_sparse_attn_bwd_noalloc": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _i, _p,
                                          _i, _i, _i, _i, _i, _i, _i, _i, _f, _p, _p, _p, _i64p, _p, _i64p, _p,
                                          _i64p, _p]),

@@ -108,6 +108,23 @@ int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N,
                    int32_t* topk_indices, float* topk_raw, float* topk_avg, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/*
+ * Stage 1 of fta_topk_score alone, on its candidate-stream path (b = 64,
+ * D <= 128, at most 16 blocks per query; FTA_ERR_UNSUPPORTED otherwise): the
+ * scoring kernel writes, into the workspace, per-wave candidate streams of the
+ * blocks that can still be in a query's top-k, the row totals and the bound
+ * the selector starts from.  Exposed so that the scoring kernel can be timed
+ * and profiled on its own; fta_topk_score runs it and then the selector.
+ * Same arguments as fta_topk_score without threshold and outputs.  Stands for
+ * the block-score half of the reference's composition (block_score_launch,
+ * flash_topk_attn_v2/csrc/block_score_kernel.cu:19-258, as called from
+ * flash_topk_attn_v2/__init__.py:16-54).
+ */
+int fta_topk_score_candidates(const void* q, const void* k, int dtype, int B, int H, int N, int D,
+                              const int64_t* q_strides, const int64_t* k_strides,
+                              int score_block_size, int pad_head, int pad_tail, float scale,
+                              int max_topk, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- indices */
 
 /*
@@ -247,9 +264,43 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k,
                         void* stream);
 
 /*
+ * dQ alone ([B][N][H][D] strided; k, v with Hk heads): replaces
+ * sparse_attn_bwd_dq_launch (flash_topk_attn_v2/csrc/sparse_attn_bwd_dq.cpp:3-19)
+ * behind flash_sparse_attn_bwd_dq_cuda (sparse_attn_bwd_dq_cuda.py:44-108).
+ * Needs no workspace.
+ */
+int fta_sparse_attn_bwd_dq(const void* q, const int64_t* q_strides, const void* k,
+                           const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                           const void* dout, const int64_t* do_strides, int dtype, int B, int H,
+                           int Hk, int N, int D, const int32_t* merged_indices, int QM, int W,
+                           int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail,
+                           int kv_pad_head, int kv_pad_tail, float scale, const float* lse,
+                           const float* delta, void* dq, const int64_t* dq_strides, void* stream);
+
+/*
+ * dK / dV alone (Hk heads, each summed over its H / Hk query heads without
+ * atomics).  Builds the KV block -> q-block membership bitmap and the lse in
+ * log2 units in the workspace (fta_sparse_attn_bwd_workspace_size bytes) and
+ * walks it.  Replaces build_reverse_indices_launch + sparse_attn_bwd_dkv_launch
+ * (flash_topk_attn_v2/csrc/build_reverse_indices.cpp:3-14,
+ * sparse_attn_bwd_dkv.cpp:3-20) behind flash_sparse_attn_bwd_dkv_cuda
+ * (sparse_attn_bwd_dkv_cuda.py:44-118).
+ */
+int fta_sparse_attn_bwd_dkv(const void* q, const int64_t* q_strides, const void* k,
+                            const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                            const void* dout, const int64_t* do_strides, int dtype, int B, int H,
+                            int Hk, int N, int D, const int32_t* merged_indices, int QM, int W,
+                            int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail,
+                            int kv_pad_head, int kv_pad_tail, float scale, const float* lse,
+                            const float* delta, void* dk, const int64_t* dk_strides, void* dv,
+                            const int64_t* dv_strides, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/*
  * Grouped-query backward: dk and dv have Hk heads; each is the sum over the
  * H / Hk query heads that share the K/V head (accumulated in fp32 inside one
  * workgroup, no atomics).  Otherwise as fta_sparse_attn_bwd (= Hk = H).
+ * Runs fta_sparse_attn_bwd_dq, then fta_sparse_attn_bwd_dkv.
  * Extends the reference the same way as fta_sparse_attn_fwd_gqa.
  */
 int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void* k,

@@ -38,20 +38,10 @@ def _iid(shape, seed, dtype, scale=1.0):
 
 
 def _peaked(B, N, H, D, seed):
-    """Config 3 data: block-centred keys, queries near one of 8 blocks per 1024-query segment."""
-    g = torch.Generator(device="cpu").manual_seed(seed)
-    C, b = H * D, 64
-    M = N // b
-    cent = torch.randn(B, M, C, generator=g)
-    k = 0.3 * torch.randn(B, N, C, generator=g) + cent.repeat_interleave(b, dim=1)
-    nseg = N // 1024
-    choice = torch.stack([torch.randperm(M, generator=g)[:8] for _ in range(B * nseg)]).view(B, nseg, 8)
-    pick_slot = torch.randint(0, 8, (B, N), generator=g)
-    seg = torch.arange(N) // 1024
-    pick = torch.gather(choice[:, seg, :], 2, pick_slot.unsqueeze(-1)).squeeze(-1)
-    q = 0.3 * torch.randn(B, N, C, generator=g) + torch.gather(cent, 1, pick.unsqueeze(-1).expand(B, N, C))
-    v = torch.randn(B, N, C, generator=g)
-    return (x.to(torch.bfloat16).cuda() for x in (q, k, v))
+    """Config 3 data, generated exactly as bench.py times it (bench.make_inputs)."""
+    import bench
+
+    return bench.make_inputs(B, N, H, D, True, seed, "cuda")
 
 
 def _head(x, h, D):
