@@ -47,6 +47,19 @@ the HIP kernels follow the same rules:
 
 Floating-point attention maths (block scores, o, lse, gradients) is computed
 in float64 from the caller's (already bf16/fp16-rounded) inputs.
+
+``round_p`` ("bf16" / "fp16") of ``sparse_attn`` and ``sparse_attn_bwd``
+additionally rounds, to that 16-bit type with round-to-nearest-even, the
+operands that the reference's kernels convert to the input element type
+before a matrix product (P before P.V in the forward,
+v2/csrc/sparse_attn_kernel.cu:207-310; P before P^T.dO and dS before dS.K /
+dS^T.Q in the backward, v2/csrc/sparse_attn_bwd_dq_kernel.cu and
+sparse_attn_bwd_dkv_kernel.cu), everything else staying float64.  The forward
+rounds P relative to the row's final maximum (a kernel's online softmax
+rounds it relative to a running maximum, so the forward mode models the
+rounding, it does not replicate it bit for bit); the backward's P is
+normalised by the forward's lse in every implementation, so its rounding
+points are those of the kernels.
 """
 
 from __future__ import annotations
@@ -59,6 +72,24 @@ import numpy as np
 # --------------------------------------------------------------------------
 # helpers
 # --------------------------------------------------------------------------
+
+
+def round_to(x: np.ndarray, kind: Optional[str]) -> np.ndarray:
+    """x rounded to bfloat16 / float16 (round to nearest, ties to even), as
+    float64; ``kind`` None returns x unchanged."""
+    if kind is None:
+        return x
+    if kind == "fp16":  # from float32, as the kernels round their fp32 values
+        with np.errstate(over="ignore"):
+            return np.asarray(x, dtype=np.float64).astype(np.float32).astype(np.float16).astype(np.float64)
+    if kind != "bf16":
+        raise ValueError(f"unknown rounding {kind!r}")
+    f = np.ascontiguousarray(np.asarray(x, dtype=np.float64).astype(np.float32))
+    u = f.view(np.uint32).astype(np.uint64)
+    finite = np.isfinite(f)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    r = np.where(finite, r, u & 0xFFFF0000)
+    return r.astype(np.uint32).view(np.float32).astype(np.float64)
 
 
 def _to_bhnd(x: np.ndarray, num_heads: int) -> np.ndarray:
@@ -270,6 +301,47 @@ def _valid_tokens(blocks: Iterable[int], N: int, kv_block_size: int, kv_pad_head
     return valid
 
 
+def _chunk_starts(blocks: Iterable[int], N: int, kv_block_size: int, kv_pad_head: int) -> np.ndarray:
+    """For the valid tokens of ``_valid_tokens`` (ascending), the index of the
+    64-key chunk each belongs to: chunks are the ascending blocks split every 64
+    keys from the block start (virtual padding included)."""
+    ids = sorted(set(int(x) for x in blocks))
+    out, c = [], 0
+    for m in ids:
+        s0 = m * kv_block_size - kv_pad_head
+        for j in range(0, kv_block_size, 64):
+            lo, hi = max(0, s0 + j), min(N, s0 + min(j + 64, kv_block_size))
+            if hi > lo:
+                out.extend([c] * (hi - lo))
+            c += 1
+    return np.asarray(out, dtype=np.int64)
+
+
+def _online_pv(s: np.ndarray, v: np.ndarray, chunk: np.ndarray, c: float, round_p: str,
+               anchor_slack: float) -> np.ndarray:
+    """o = sum_j round(P_j) v_j / sum_j P_j with P anchored to a lazily updated
+    running maximum per row (see sparse_attn); s are the unscaled scores."""
+    rows = s.shape[0]
+    m = np.full(rows, -np.inf)
+    acc = np.zeros((rows, v.shape[1]))
+    l = np.zeros(rows)
+    for ch in np.unique(chunk):
+        sel = chunk == ch
+        sc = s[:, sel]
+        mx = sc.max(-1)
+        mn = np.maximum(m, mx)
+        with np.errstate(invalid="ignore"):
+            grow = (mn - m) * c > anchor_slack
+        alpha = np.where(grow, np.exp2(np.where(grow, (m - mn) * c, 0.0)), 1.0)
+        acc *= alpha[:, None]
+        l *= alpha
+        m = np.where(grow, mn, m)
+        p = np.exp2(sc * c - np.where(np.isfinite(m), m * c, 0.0)[:, None])
+        l += p.sum(-1)
+        acc += round_to(p, round_p) @ v[sel]
+    return acc / l[:, None]
+
+
 def sparse_attn(
     q: np.ndarray,
     k: np.ndarray,
@@ -282,10 +354,23 @@ def sparse_attn(
     q_padding: Tuple[int, int] = (0, 0),
     kv_padding: Tuple[int, int] = (0, 0),
     qblocks: Optional[Sequence[Tuple[int, int, int]]] = None,
+    round_p: Optional[str] = None,
+    anchor_slack: float = 8.0,
 ) -> Tuple[np.ndarray, np.ndarray]:
     """o [B, N, C] float64 and natural-log lse [B, H, N] (−inf and o = 0 for
     rows with no candidate token).  ``qblocks`` restricts the computation to the
-    listed (b, h, qm) triples; other rows are left at o = 0 / lse = NaN."""
+    listed (b, h, qm) triples; other rows are left at o = 0 / lse = NaN.
+
+    ``round_p``: the online-softmax schedule of a kernel, with P rounded to that
+    16-bit type before its product with V (the normaliser sums unrounded P).
+    The q-block's selected KV blocks are walked in ascending order in chunks of
+    64 keys (a block of more than 64 keys spans several chunks); each row keeps
+    a running maximum m and P = 2^(c s - c m), c = scale * log2(e).  m is
+    re-anchored to the row maximum seen so far when that exceeds it by more than
+    ``anchor_slack`` in log2 units (this build's kernels: 8; 0 re-anchors
+    whenever the maximum grows, as the reference's kernel does,
+    v2/csrc/sparse_attn_kernel.cuh:145-160), and the accumulators are scaled by
+    2^(c m_old - c m_new) then."""
     B, N, C = q.shape
     H = num_heads
     D = C // H
@@ -311,8 +396,13 @@ def sparse_attn(
             continue
         s = (q4[b, h, rs:re] * scale) @ k4[b, h, valid].T
         row_lse = _logsumexp(s)
-        p = np.exp(s - row_lse[:, None])
-        o[b, h, rs:re] = p @ v4[b, h, valid]
+        if round_p is None:
+            p = np.exp(s - row_lse[:, None])
+            o[b, h, rs:re] = p @ v4[b, h, valid]
+        else:
+            o[b, h, rs:re] = _online_pv(s / scale, v4[b, h, valid], _chunk_starts(ids[ids >= 0], N, kv_block_size,
+                                                                                    kph),
+                                        scale * math.log2(math.e), round_p, anchor_slack)
         lse[b, h, rs:re] = row_lse
     return _from_bhnd(o), lse
 
@@ -372,12 +462,21 @@ def sparse_attn_bwd(
     q_padding: Tuple[int, int] = (0, 0),
     kv_padding: Tuple[int, int] = (0, 0),
     qblocks: Optional[Sequence[Tuple[int, int, int]]] = None,
+    round_p: Optional[str] = None,
+    lse: Optional[np.ndarray] = None,
+    delta: Optional[np.ndarray] = None,
 ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
     """dQ, dK, dV (float64, [B, N, C]) following bwd_dq_naive / bwd_dkv_naive
     (v2/sparse_attn_bwd.py:111-294): P = softmax over the q-block's candidate
     tokens, dP = dO V^T, delta = rowsum(dO * (P V)), dS = P (dP - delta),
     dQ = scale dS K, dK = scale dS^T Q, dV = P^T dO.  ``qblocks`` restricts the
-    sum to the listed (b, h, qm) triples (dK/dV then hold partial sums)."""
+    sum to the listed (b, h, qm) triples (dK/dV then hold partial sums).
+
+    ``lse`` [B, H, N] (natural log) replaces the row normaliser, so that
+    P = exp(s - lse) as in the backward kernels, which read the forward's lse;
+    ``delta`` [B, H, N] replaces rowsum(dO * (P V)) (the reference computes it
+    from the forward's stored output, v2/sparse_attn.py:177).  ``round_p``
+    rounds P before P^T dO and dS before dS K / dS^T Q."""
     B, N, C = q.shape
     H = num_heads
     D = C // H
@@ -404,13 +503,18 @@ def sparse_attn_bwd(
         qq, dd = q4[b, h, rs:re], do4[b, h, rs:re]
         kk, vv = k4[b, h, valid], v4[b, h, valid]
         s = (qq * scale) @ kk.T
-        p = np.exp(s - _logsumexp(s)[:, None])
+        norm = _logsumexp(s) if lse is None else np.asarray(lse[b, h, rs:re], dtype=np.float64)
+        p = np.exp(s - norm[:, None])
         dp = dd @ vv.T
-        delta = (dd * (p @ vv)).sum(-1, keepdims=True)
-        ds = p * (dp - delta)
-        dq[b, h, rs:re] += scale * ds @ kk
-        dk[b, h, valid] += scale * ds.T @ qq
-        dv[b, h, valid] += p.T @ dd
+        if delta is None:
+            dl = (dd * (p @ vv)).sum(-1, keepdims=True)
+        else:
+            dl = np.asarray(delta[b, h, rs:re], dtype=np.float64)[:, None]
+        ds = p * (dp - dl)
+        dsr = round_to(ds, round_p)
+        dq[b, h, rs:re] += scale * dsr @ kk
+        dk[b, h, valid] += scale * dsr.T @ qq
+        dv[b, h, valid] += round_to(p, round_p).T @ dd
     return _from_bhnd(dq), _from_bhnd(dk), _from_bhnd(dv)
 
 

@@ -1,9 +1,13 @@
 """GPU parity: HIP kernels (through the C ABI via the Python API) vs the CPU oracle.
 
-Tolerances (from the task's north star): top-k indices identical except where
-the oracle's average scores of the swapped blocks differ by < 1e-6; merged
-indices / counts / reverse lists bit-exact given identical inputs; o, dQ, dK,
-dV within atol 2e-3 + rtol 1e-2 (fp16/bf16 outputs), lse rtol 1e-4.
+Tolerances (from the task's north star): top-k indices identical to the
+selection on float64 scores except where the swapped blocks' averages differ by
+< 1e-6 or the float64 cumulative sum at the cut lies within 1e-6 of the
+threshold, and bit-exact against the oracle fed the kernels' fp32 scores;
+merged indices / counts / reverse lists bit-exact given identical inputs; o,
+dQ, dK, dV within atol 2e-3 + rtol 1e-2 on every element against the oracle
+with the kernels' 16-bit rounding points (a float64 comparison is kept as a
+second, stated check); lse rtol 1e-4.
 """
 
 import math
@@ -13,7 +17,8 @@ import pytest
 import torch
 
 import fta_oracle as O
-from _helpers import assert_close_frac, check_topk_gap, np32, rand, say
+from _helpers import (assert_close_frac, assert_within, check_topk_f64, check_topk_gap, np32, rand, round_kind,
+                      say)
 
 pytestmark = pytest.mark.gpu
 
@@ -146,19 +151,22 @@ def test_drawn_scoring_geometries(seed):
 
 @pytest.mark.parametrize("case", SCORE_CASES[:4], ids=lambda c: f"N{c[1]}D{c[3]}b{c[4]}")
 def test_topk_score_vs_float64_oracle(case):
+    """Top-k (thresholds 1.0, 0.9, 0.5) against the selection on float64 block
+    scores: identical except near-ties (< 1e-6) and cuts where the float64
+    cumulative sum is within 1e-6 of the threshold."""
     B, N, H, D, b, pad, dt, layout = case
     say(f"[topk_score64] {case}")
     q, k = _qk(case, 30)
-    fi, _, _ = fta.flash_topk_score(q, k, H, b, 16, pad, 1.0)
-    torch.cuda.synchronize()
     qn, kn = _oracle_inputs(q, k)
     s64 = O.block_score(qn, kn, H, b, pad)
     M = s64.shape[-1]
     vc = O.valid_counts(M, b, pad).astype(np.float64)
-    avg64 = s64 / vc
-    ri, _, _ = O.topk_select(s64.astype(np.float32), 1.0, 16, b, pad)
-    bad, ndiff = check_topk_gap(fi.cpu().numpy(), avg64, ri)
-    assert bad == 0, f"{bad} of {ndiff} differing indices have score gap >= 1e-6"
+    for thr in (1.0, 0.9, 0.5):
+        fi, _, _ = fta.flash_topk_score(q, k, H, b, 16, pad, thr)
+        torch.cuda.synchronize()
+        gi = fi.cpu().numpy().reshape(-1, fi.shape[-1])
+        bad = check_topk_f64(gi, (s64 / vc).reshape(-1, M), s64.reshape(-1, M), thr, min(16, M))
+        assert bad == 0, f"thr={thr}: {bad} rows differ from the float64 selection beyond the 1e-6 rules"
 
 
 @pytest.mark.parametrize("g,K,Mt,W,pad", [(32, 16, 128, None, (0, 0)), (1, 16, 128, None, (0, 0)),
@@ -293,22 +301,56 @@ def test_sparse_attn_fwd_bwd_vs_oracle(case):
     do = rand((B, N, H * D), 99, o.dtype, "cuda")
     o.backward(do)
     torch.cuda.synchronize()
-    qn, kn, vn = _rounded(q), _rounded(k), _rounded(v)
-    ro, rl = O.sparse_attn(qn, kn, vn, merged, H, g, b, None, qpad, kvpad)
     assert o.dtype == dt
-    assert_close_frac(np32(o), ro, atol=2e-3, rtol=1e-2, name="o")
-    l = lse.cpu().numpy()
+    check_attn_vs_oracle(q, k, v, do, o, lse, merged, H, g, b, qpad, kvpad, dt)
+
+
+def check_attn_vs_oracle(q, k, v, do, o, lse, merged, H, g, b, qpad, kvpad, dt, gqa_repeat=1):
+    """o, lse, dQ, dK, dV of the kernels against the oracle.
+
+    Primary (the north-star bound on every element, atol 2e-3 + rtol 1e-2):
+    the oracle with the kernels' 16-bit rounding points (P before P.V with
+    the kernels' online-softmax anchors; P before P^T dO and dS before dS K /
+    dS^T Q in the backward, normalised by the forward's lse and with delta
+    from the stored output).  Secondary (stated): the unrounded float64 oracle,
+    which the rounding of P / dS separates from the kernels by more than the
+    bound on a few elements, at most 1e-4 (o) / 5e-4 (gradients) of them."""
+    from flash_topk_attn_v2.sparse_attn_bwd import preprocess_delta
+
+    B, N, C = q.shape
+    rk = round_kind(dt)
+    qn, kn, vn = _rounded(q), _rounded(k), _rounded(v)
+    if gqa_repeat > 1:
+        Dk = C // H
+        kn = kn.reshape(B, N, -1, Dk).repeat(gqa_repeat, axis=2).reshape(B, N, C)
+        vn = vn.reshape(B, N, -1, Dk).repeat(gqa_repeat, axis=2).reshape(B, N, C)
+    rr, rl = O.sparse_attn(qn, kn, vn, merged, H, g, b, None, qpad, kvpad, round_p=rk)
+    assert_within(np32(o), rr, name="o vs rounding oracle")
+    ro, _ = O.sparse_attn(qn, kn, vn, merged, H, g, b, None, qpad, kvpad)
+    assert_close_frac(np32(o), ro, atol=2e-3, rtol=1e-2, name="o vs float64")
+    l = lse.detach().cpu().numpy()
     np.testing.assert_array_equal(np.isneginf(l), np.isneginf(rl))
     fin = np.isfinite(rl)
     np.testing.assert_allclose(l[fin], rl[fin], rtol=1e-4, atol=1e-4)
-    dq, dk, dv = O.sparse_attn_bwd(qn, kn, vn, np32(do), merged, H, g, b, None, qpad, kvpad)
-    for name, got, ref in (("dq", q.grad, dq), ("dk", k.grad, dk), ("dv", v.grad, dv)):
-        # gradients are O(sqrt(#keys)) larger than o; the atol scales with their magnitude.  dS and P
-        # are rounded to 16 bits before the dQ / dK / dV products (as in the reference kernels); with
-        # few keys per query and small D those rounding errors do not average out, so up to 5e-4 of
-        # the elements may exceed the soft bound, none the hard one.
-        assert_close_frac(np32(got), ref, atol=2e-3 * max(1.0, np.abs(ref).max() / 4), rtol=1e-2, name=name,
-                          min_frac=0.9995, hard_atol=1e-2 * max(1.0, np.abs(ref).max() / 4))
+    if q.grad is None:
+        return
+    # the kernels' operands: dO in the compute type, delta from the stored (16-bit) output
+    oc = o.detach() if o.dtype != torch.float32 else o.detach().bfloat16()
+    doc = do.to(oc.dtype)
+    delta = preprocess_delta(oc, doc, H).cpu().numpy().astype(np.float64)
+    don = np32(doc)
+    grads = O.sparse_attn_bwd(qn, kn, vn, don, merged, H, g, b, None, qpad, kvpad, round_p=rk,
+                              lse=l.astype(np.float64), delta=delta)
+    g64 = O.sparse_attn_bwd(qn, kn, vn, don, merged, H, g, b, None, qpad, kvpad)
+    for name, t, rr_, r64 in (("dq", q, grads[0], g64[0]), ("dk", k, grads[1], g64[1]), ("dv", v, grads[2], g64[2])):
+        if name != "dq" and gqa_repeat > 1:
+            Dk = C // H
+            rr_ = rr_.reshape(B, N, -1, gqa_repeat, Dk).sum(3).reshape(B, N, -1)
+            r64 = r64.reshape(B, N, -1, gqa_repeat, Dk).sum(3).reshape(B, N, -1)
+        assert_within(np32(t.grad), rr_, name=f"{name} vs rounding oracle")
+        s2 = max(1.0, np.abs(r64).max() / 4)
+        assert_close_frac(np32(t.grad), r64, atol=2e-3 * s2, rtol=1e-2, name=f"{name} vs float64", min_frac=0.9995,
+                          hard_atol=1e-2 * s2)
 
 
 GQA_CASES = [
@@ -324,7 +366,8 @@ GQA_CASES = [
 def test_gqa_matches_repeated_kv(case):
     """Grouped-query attention (an extension: the reference raises for it) equals
     the multi-head path with each K/V head repeated for its query heads: o, lse
-    and dQ bit for bit, dK / dV as the sum of the repeated heads' gradients."""
+    and dQ bit for bit; dK / dV match the oracle's repeated-head gradients
+    summed over each group."""
     B, N, H, Hk, D, g, b, qpad, kvpad, W, dt = case
     say(f"[gqa] {case}")
     G = H // Hk
@@ -348,10 +391,9 @@ def test_gqa_matches_repeated_kv(case):
     torch.cuda.synchronize()
     assert torch.equal(o, o2) and torch.equal(lse, lse2), "GQA forward != repeated-K/V forward"
     assert torch.equal(q.grad, q2.grad), "GQA dQ != repeated-K/V dQ"
-    for name, got, ref in (("dk", k.grad, k2.grad), ("dv", v.grad, v2.grad)):
-        r = ref.float().view(B, N, Hk, G, D).sum(3).reshape(B, N, Hk * D).cpu().numpy()
-        s2 = max(1.0, np.abs(r).max() / 4)
-        assert_close_frac(np32(got), r, atol=2e-3 * s2, rtol=1e-2, name=name, min_frac=0.9995, hard_atol=1e-2 * s2)
+    # dK / dV sum the G query heads in fp32 and round once: checked against the oracle
+    # on repeated K / V heads, summed over each group
+    check_attn_vs_oracle(q, k, v, do, o, lse, merged.cpu().numpy(), H, g, b, qpad, kvpad, dt, gqa_repeat=G)
 
 
 def test_reverse_indices_and_sort_by_count():

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import fta_oracle as O
-from _helpers import assert_close_frac, check_topk_gap, np32, rand, say
+from _helpers import assert_close_frac, assert_within, check_topk_gap, np32, rand, round_kind, say
 
 pytestmark = pytest.mark.gpu
 
@@ -125,15 +125,26 @@ def test_score_with_dense_output_and_backward(case):
         if layout == "bhnd" else np32
     qn, kn, vn, don, on = (to3(t) for t in (q.detach(), k.detach(), v.detach(), do, o.detach()))
     ro, _, _ = O.v1_topk_score(qn, kn, vn, H, b, topk, pad)
-    assert_close_frac(on, ro, atol=2e-3, rtol=1e-2, name="o")
-    # dense = every 64-token KV block selected for every 64-query block
+    assert_close_frac(on, ro, atol=2e-3, rtol=1e-2, name="o vs f64")
+    # dense = every 64-token KV block selected for every 64-query block; primary check:
+    # the oracle with the kernels' 16-bit rounding points, every element within the bound
     nb = (N + 63) // 64
-    merged = np.broadcast_to(np.arange(nb, dtype=np.int32), (B, H, nb, nb))
+    merged = np.ascontiguousarray(np.broadcast_to(np.arange(nb, dtype=np.int32), (B, H, nb, nb)))
     pad64 = (0, nb * 64 - N)
-    dq, dk, dv = O.sparse_attn_bwd(qn, kn, vn, don, merged, H, 64, 64, None, pad64, pad64)
-    for name, got, ref in (("dq", q.grad, dq), ("dk", k.grad, dk), ("dv", v.grad, dv)):
-        s = max(1.0, np.abs(ref).max() / 4)
-        assert_close_frac(to3(got), ref, atol=2e-3 * s, rtol=1e-2, name=name, min_frac=0.9995, hard_atol=1e-2 * s)
+    rk = round_kind(dt)
+    rr, rl = O.sparse_attn(qn, kn, vn, merged, H, 64, 64, None, pad64, pad64, round_p=rk)
+    assert_within(on, rr, name="o vs rounding oracle")
+    from flash_topk_attn_v2.sparse_attn_bwd import preprocess_delta
+
+    delta = preprocess_delta(torch.from_numpy(on).to(dt).cuda(), torch.from_numpy(don).to(dt).cuda(), H)
+    kw = dict(round_p=rk, lse=rl, delta=delta.cpu().numpy().astype(np.float64))
+    dq, dk, dv = O.sparse_attn_bwd(qn, kn, vn, don, merged, H, 64, 64, None, pad64, pad64, **kw)
+    dq64, dk64, dv64 = O.sparse_attn_bwd(qn, kn, vn, don, merged, H, 64, 64, None, pad64, pad64)
+    for name, got, ref, r64 in (("dq", q.grad, dq, dq64), ("dk", k.grad, dk, dk64), ("dv", v.grad, dv, dv64)):
+        assert_within(to3(got), ref, name=f"{name} vs rounding oracle")
+        s = max(1.0, np.abs(r64).max() / 4)
+        assert_close_frac(to3(got), r64, atol=2e-3 * s, rtol=1e-2, name=f"{name} vs f64", min_frac=0.9995,
+                          hard_atol=1e-2 * s)
 
 
 ATTN_CASES = [
@@ -163,7 +174,17 @@ def test_attn_over_union_vs_oracle(case):
     ro, rl = O.v1_sparse_attn(np32(q), np32(k), np32(v), merged.cpu().numpy(), counts.cpu().numpy(), H, g, b,
                               None, kvpad, qpad, smax)
     assert o.dtype == dt
-    assert_close_frac(np32(o), ro, atol=2e-3, rtol=1e-2, name="o")
+    assert_close_frac(np32(o), ro, atol=2e-3, rtol=1e-2, name="o vs f64")
+    # primary: the V2 oracle with the kernels' rounding points on the lists the V1
+    # semantics select (first min(count, S_MAX) ids, one list for every head when H_BI = 1);
+    # a row's result depends only on its ascending block set, not on the q-block grouping
+    mv = merged.cpu().numpy().copy()
+    lim = counts.cpu().numpy() if smax is None else np.minimum(counts.cpu().numpy(), smax)
+    mv[np.arange(mv.shape[-1]) >= lim[..., None]] = -1
+    if mv.shape[1] == 1:
+        mv = np.repeat(mv, H, axis=1)
+    rr, _ = O.sparse_attn(np32(q), np32(k), np32(v), mv, H, g, b, None, qpad, kvpad, round_p=round_kind(dt))
+    assert_within(np32(o), rr, name="o vs rounding oracle")
     l = lse.cpu().numpy()
     np.testing.assert_array_equal(np.isneginf(l), np.isneginf(rl))
     fin = np.isfinite(rl)

@@ -369,3 +369,93 @@ def test_v1_sparse_attn_counts_and_shared_heads():
             ref_o = (p / p.sum(-1, keepdims=True)) @ v4[0, h, toks]
             np.testing.assert_allclose(lse[0, h, qm * g:(qm + 1) * g], ref_lse, rtol=1e-12)
             np.testing.assert_allclose(o.reshape(B, N, H, D)[0, qm * g:(qm + 1) * g, h], ref_o, rtol=1e-10)
+
+
+# ---------------------------------------------------------- 16-bit rounding modes
+
+
+def test_round_to_matches_torch_conversions():
+    """bf16 / fp16 round-to-nearest-even from float32, as torch converts (an
+    independent implementation), including ties, subnormals and overflow."""
+    rng = _rng(40)
+    x = rng.standard_normal(20000) * np.exp(rng.uniform(-40, 40, 20000))
+    # exact ties between two bf16 / fp16 neighbours
+    x = np.concatenate([x, [1 + 2.0 ** -8, 1 + 3 * 2.0 ** -8, 1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, 1e-40, 7e4, -np.inf]])
+    for kind, tdt in (("bf16", torch.bfloat16), ("fp16", torch.float16)):
+        ref = torch.from_numpy(x).float().to(tdt).double().numpy()
+        np.testing.assert_array_equal(O.round_to(x, kind), ref)
+    assert O.round_to(np.array([1 + 2.0 ** -8]), "bf16")[0] == 1.0  # tie to even
+    assert O.round_to(np.array([1 + 3 * 2.0 ** -8]), "bf16")[0] == 1 + 2.0 ** -6
+
+
+@pytest.mark.parametrize("slack", [0.0, 8.0, 1e9])
+def test_online_softmax_schedule_without_rounding_is_softmax(slack):
+    """The forward rounding mode's online softmax (chunked, lazily re-anchored
+    running maximum) equals softmax(s) V when nothing is rounded, for any
+    chunking and anchor slack: a wrong rescale factor, sign or a dropped
+    chunk fails this."""
+    rng = _rng(41)
+    R, T, D = 5, 300, 16
+    s = rng.standard_normal((R, T)) * 6
+    s[:, 150:] += 30  # a later chunk raises the maximum far beyond the slack
+    v = rng.standard_normal((T, D))
+    chunk = np.sort(rng.integers(0, 9, T))
+    c = 0.7
+    got = O._online_pv(s, v, chunk, c, None, slack)
+    w = np.exp2(c * (s - s.max(-1, keepdims=True)))
+    np.testing.assert_allclose(got, (w / w.sum(-1, keepdims=True)) @ v, rtol=1e-12, atol=1e-12)
+
+
+def test_rounding_modes_bound_and_exact_cases():
+    """With every P exactly representable (all scores equal, so P = 1 / n after
+    normalisation in the backward and 1 before it in the forward) the rounding
+    modes equal the float64 oracle; in general they differ from it by at most
+    the 16-bit rounding of P / dS (relative 2^-8 of bf16 per term)."""
+    rng = _rng(42)
+    B, N, H, D, g, b = 1, 128, 1, 16, 32, 64
+    merged = np.array([[[[0, 1], [1, -1], [0, -1], [0, 1]]]], dtype=np.int32)
+    q = np.zeros((B, N, H * D))
+    k = rng.standard_normal((B, N, H * D))
+    v = O.round_to(rng.standard_normal((B, N, H * D)), "bf16")
+    do = O.round_to(rng.standard_normal((B, N, H * D)), "bf16")
+    o64, l64 = O.sparse_attn(q, k, v, merged, H, g, b)
+    orr, lr = O.sparse_attn(q, k, v, merged, H, g, b, round_p="bf16")
+    np.testing.assert_allclose(orr, o64, rtol=1e-12, atol=1e-12)
+    np.testing.assert_array_equal(lr, l64)
+    # general inputs: |dV_r - dV| <= 2^-8 sum_q P |dO| (P rounded once per term)
+    q = rng.standard_normal((B, N, H * D))
+    o64, l64 = O.sparse_attn(q, k, v, merged, H, g, b)
+    d64 = O.sparse_attn_bwd(q, k, v, do, merged, H, g, b)
+    dr = O.sparse_attn_bwd(q, k, v, do, merged, H, g, b, round_p="bf16", lse=l64)
+    absdo = np.abs(do)
+    bound = np.zeros_like(d64[2])
+    for qm in range(4):
+        ids = merged[0, 0, qm]
+        keys = np.concatenate([np.arange(m * b, (m + 1) * b) for m in ids[ids >= 0]])
+        rows = slice(qm * g, (qm + 1) * g)
+        s = (q[0, rows] / math.sqrt(D)) @ k[0, keys].T
+        p = np.exp(s - l64[0, 0, rows][:, None])
+        bound[0, keys] += 2.0 ** -8 * p.T @ absdo[0, rows]
+    assert np.all(np.abs(dr[2] - d64[2]) <= bound + 1e-12)
+    assert np.abs(dr[2] - d64[2]).max() > 0  # the mode does round
+    # lse / delta passed in equal the ones the oracle derives itself
+    dl = (do * o64).reshape(B, N, H, D).sum(-1).transpose(0, 2, 1)
+    d2 = O.sparse_attn_bwd(q, k, v, do, merged, H, g, b, lse=l64, delta=dl)
+    for a, c in zip(d2, d64):
+        np.testing.assert_allclose(a, c, rtol=1e-10, atol=1e-10)
+
+
+def test_check_topk_f64_rules():
+    """The float64 top-k comparison used by the GPU tests accepts only near-ties
+    and near-threshold cuts."""
+    from _helpers import check_topk_f64
+
+    raw = np.array([[0.5, 0.3, 0.15, 0.05]])
+    avg = raw.copy()
+    assert check_topk_f64(np.array([[0, 1, 2, -1]]), avg, raw, 0.9, 4) == 0
+    assert check_topk_f64(np.array([[0, 1, -1, -1]]), avg, raw, 0.9, 4) == 1  # cut early, 0.8 far from 0.9
+    assert check_topk_f64(np.array([[1, 0, 2, -1]]), avg, raw, 0.9, 4) == 1  # swap with a 0.2 gap
+    raw2 = np.array([[0.5, 0.4 - 1e-9, 0.1]])
+    assert check_topk_f64(np.array([[0, 1, 2]]), raw2, raw2, 0.9, 3) == 0  # cum 0.9 - 1e-9: near the threshold
+    raw3 = np.array([[0.4, 0.4 + 1e-9, 0.2]])
+    assert check_topk_f64(np.array([[0, 1, 2]]), raw3, raw3, 1.0, 3) == 0  # near-tie swap
