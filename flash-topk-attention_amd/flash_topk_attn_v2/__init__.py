@@ -72,6 +72,9 @@ def flash_topk_score(
         _lib.ptr(idx), _lib.ptr(raw), _lib.ptr(avg), _lib.ptr(ws), ws.numel(), _lib.stream_ptr(dev),
     )
     _lib.check(rc, "flash_topk_score")
+    # every id is < M <= 4096: build_qblock_topk_indices need not read the max back
+    # (recorded with the tensor's version counter, so an in-place change voids it)
+    idx._fta_id_bound = (M, idx._version)
     return idx, raw, avg
 
 
@@ -146,6 +149,11 @@ def build_qblock_topk_indices(
         _lib.stream_ptr(device),
     )
     _lib.check(rc, "flash_qblock_merge")
+    bound = getattr(topk_indices, "_fta_id_bound", None)
+    if bound is not None and bound[0] <= 4096 and bound[1] == topk_indices._version:
+        # produced by flash_topk_score with M <= 4096 blocks: no id can exceed the
+        # limit, so the host does not wait for the max (the step stays asynchronous)
+        return merged_indices, counts, merged_indices.shape[-1]
     num_score_blocks = int(max_id.item()) + 1
     if num_score_blocks > 4096:
         raise NotImplementedError(

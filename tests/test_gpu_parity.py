@@ -208,6 +208,17 @@ def test_merge_device_max_edge_cases():
     with pytest.raises(NotImplementedError, match="4096"):
         fta.build_qblock_topk_indices(ti, 32, (0, 0), None, 8)
     torch.cuda.synchronize()
+    # indices from flash_topk_score carry their block bound (no host read of the max);
+    # an in-place change afterwards voids it and the limit is checked again
+    q = rand((1, 256, 64), 3, torch.bfloat16, "cuda")
+    idx, _, avg = fta.flash_topk_score(q, q, 1, 64, 2)
+    m1, c1, _ = fta.build_qblock_topk_indices(idx, 32, (0, 0), avg, 8)
+    m2, c2, _ = fta.build_qblock_topk_indices(idx.clone(), 32, (0, 0), avg, 8)
+    assert torch.equal(m1, m2) and torch.equal(c1, c2)
+    idx[0, 0, 3, 0] = 5000
+    with pytest.raises(NotImplementedError, match="4096"):
+        fta.build_qblock_topk_indices(idx, 32, (0, 0), avg, 8)
+    torch.cuda.synchronize()
 
 
 ATTN_CASES = [
