@@ -27,6 +27,7 @@
 
 namespace fta {
 int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint32_t* sel, hipStream_t st);
+int launch_kv_order(const uint32_t* sel, int B, int H, int Hk, int M, int QW, int32_t* order, hipStream_t st);
 }  // namespace fta
 
 constexpr int kSeg = 512;    // KV blocks per mask segment (forward / dQ)
@@ -44,6 +45,7 @@ struct AttnArgs {
     int64_t d_sb, d_sh, d_sn;
     const int32_t* merged;  // [BH][QM][W]
     const uint32_t* sel;    // [BH][Mkv][QW] membership bitmap (dK/dV)
+    const int32_t* kv_order;  // [B*Hk][Mkv] dK/dV launch order of the KV blocks (null: natural order)
     int QM, W, QW;
     uint16_t* out0;  // o (forward) / dq / dk
     int64_t o0_sb, o0_sh, o0_sn;
@@ -1485,7 +1487,8 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
 
     const int wgi = fta_xcd_remap(blockIdx.x, a.total);
     const int bhk = wgi / a.wg_per_bh;  // (b, K/V head)
-    const int wk = wgi - bhk * a.wg_per_bh;  // KV block
+    const int wk0 = wgi - bhk * a.wg_per_bh;
+    const int wk = a.kv_order ? a.kv_order[(int64_t)bhk * a.wg_per_bh + wk0] : wk0;  // KV block
     const int b = bhk / a.Hk, hk = bhk - (bhk / a.Hk) * a.Hk;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1883,9 +1886,10 @@ size_t sel_bytes(int B, int H, const Geo& G) {
     return fta::align_up((size_t)B * H * G.Mkv * ((G.QM + 31) / 32) * sizeof(uint32_t));
 }
 
-// the backward workspace: membership bitmap, then lse in log2 units
+// the backward workspace: membership bitmap, lse in log2 units, dK/dV launch order
 size_t bwd_bytes(int B, int H, int N, const Geo& G) {
-    return sel_bytes(B, H, G) + fta::align_up((size_t)B * H * N * sizeof(float));
+    return sel_bytes(B, H, G) + fta::align_up((size_t)B * H * N * sizeof(float)) +
+           fta::align_up((size_t)B * H * G.Mkv * sizeof(int32_t));
 }
 
 }  // namespace
@@ -2062,6 +2066,12 @@ int fta_sparse_attn_bwd_dkv(const void* q, const int64_t* q_strides, const void*
     if ((rc = fta::check_launch("fta_lse2_kernel")) != FTA_OK) return rc;
     a.sel = sel;
     a.lse2_in = lse2;
+    // 64-key blocks at D 64 / 128 (the split kernel): launch in first-q-block order
+    if (kv_block_size > 32 && kv_block_size <= 64 && (G.Dk == 64 || G.Dk == 128) && G.Mkv <= 4096) {
+        int32_t* order = (int32_t*)((char*)lse2 + fta::align_up((size_t)B * H * N * sizeof(float)));
+        if ((rc = fta::launch_kv_order(sel, B, H, Hk, G.Mkv, (QM + 31) / 32, order, st)) != FTA_OK) return rc;
+        a.kv_order = order;
+    }
     a.out0 = (uint16_t*)dk;
     a.o0_sb = dk_strides[0];
     a.o0_sh = dk_strides[1];

@@ -417,6 +417,40 @@ __global__ __launch_bounds__(256) void fta_argsort_desc_rows_kernel(const int32_
     }
 }
 
+// Launch order of the dK/dV workgroups of one (b, K/V head): the KV blocks
+// sorted by the first q-block that selected them (ties: ascending block id;
+// unselected blocks last), read from the membership bitmap of the group's
+// first query head.  KV blocks picked by the same run of q-blocks then run
+// side by side on one XCD and share its L2 copy of those q-blocks' Q and dO.
+__global__ __launch_bounds__(256) void fta_kv_order_kernel(const uint32_t* __restrict__ sel, int M, int QW, int H,
+                                                           int G, int32_t* __restrict__ order) {
+    __shared__ int key[4096];
+    const int64_t rk = blockIdx.x;               // (b, K/V head)
+    const int64_t bh = (rk / (H / G)) * H + (rk % (H / G)) * G;  // its first query head
+    const uint32_t* rows = sel + bh * (int64_t)M * QW;
+    for (int m = threadIdx.x; m < M; m += 256) {
+        int first = 0x7fffffff;
+        for (int w = 0; w < QW; ++w) {
+            const uint32_t bits = rows[(int64_t)m * QW + w];
+            if (bits) {
+                first = w * 32 + __builtin_ctz(bits);
+                break;
+            }
+        }
+        key[m] = first;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < M; i += 256) {
+        const int ki = key[i];
+        int rank = 0;
+        for (int j = 0; j < M; ++j) {
+            const int kj = key[j];
+            rank += (kj < ki) || (kj == ki && j < i);
+        }
+        order[rk * M + rank] = i;
+    }
+}
+
 // Global stable descending sort of counts (reference: sort_by_count_cuda.py:33-67):
 // rank_i = #{j : c_j > c_i} + #{j < i : c_j == c_i}.
 __global__ __launch_bounds__(256) void fta_sort_by_count_kernel(const int32_t* __restrict__ cnt, int n,
@@ -540,6 +574,12 @@ int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint3
     hipLaunchKernelGGL(fta_sel_bitmap_kernel, dim3((unsigned)((int64_t)BH * QW)), dim3(256), 0, st, merged, QM, W,
                        M, QW, sel);
     return check_launch("fta_sel_bitmap_kernel");
+}
+
+int launch_kv_order(const uint32_t* sel, int B, int H, int Hk, int M, int QW, int32_t* order, hipStream_t st) {
+    if (M <= 0 || B * Hk == 0) return FTA_OK;
+    hipLaunchKernelGGL(fta_kv_order_kernel, dim3((unsigned)(B * Hk)), dim3(256), 0, st, sel, M, QW, H, H / Hk, order);
+    return check_launch("fta_kv_order_kernel");
 }
 }  // namespace fta
 

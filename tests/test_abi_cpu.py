@@ -42,9 +42,9 @@ def test_error_path_returns_status_without_gpu():
     assert rc == _lib.FTA_ERR_UNSUPPORTED
     assert L.fta_sparse_attn_bwd_workspace_size(1, 1, 100, 64, 32, 64, 0, 0, 0, 0) == 0  # 100 % 32 != 0
     assert L.fta_sparse_attn_fwd_workspace_size(1, 2, 128, 64, 32, 64, 0, 0, 0, 0) == 0  # forward has no scratch
-    # backward scratch = membership bitmap [B*H][M_kv][ceil(QM/32)] uint32, then lse in log2
-    # units [B*H][N] fp32, each 256-byte aligned: 256 + 2 * 128 * 4
-    assert L.fta_sparse_attn_bwd_workspace_size(1, 2, 128, 64, 32, 64, 0, 0, 0, 0) == 256 + 1024
+    # backward scratch = membership bitmap [B*H][M_kv][ceil(QM/32)] uint32, lse in log2
+    # units [B*H][N] fp32, dK/dV launch order [B*H][M_kv] int32, each 256-byte aligned
+    assert L.fta_sparse_attn_bwd_workspace_size(1, 2, 128, 64, 32, 64, 0, 0, 0, 0) == 256 + 1024 + 256
 
 
 def test_api_validation_matches_reference_errors():
