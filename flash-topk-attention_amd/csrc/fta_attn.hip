@@ -24,6 +24,7 @@
 #include "fta_host.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace fta {
 int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint32_t* sel, hipStream_t st);
@@ -1442,16 +1443,17 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
 // ----------------------------------------------------------------------------
 // dK / dV with the work of each key tile split over two waves (KV blocks of 33
 // to 64 keys, D = 64 or 128).  The WG owns the two 32-key tiles of one KV block;
-// wave (tt, hv) holds K (hv = 0) or V (hv = 1) of tile tt and the dK / dV
-// accumulators of the d-half hv.  Per chunk of 32 queries:
-//   hv = 0:  S = Q K^T,  P = 2^{c S - lse2}   -> LDS
-//   hv = 1:  dP = dO V^T                       -> LDS
-//   both:    dS = P (dP - delta) from the exchanged values (same fp32 operations
-//            in both waves), dV[:, half] += P^T dO[:, half], dK[:, half] += dS^T Q[:, half].
-// Each wave keeps half the accumulators and one of K / V, so a WG fits twice on
-// a CU (registers <= 256 per lane, LDS < 80 KB): one WG's mask building and
-// gather latency overlap the other's MFMAs.  One chunk per step; NST steps of Q,
-// dO, lse and delta in flight through LDS DMA, as in fta_sparse_dkv_kernel.
+// wave (tt, 0) holds K of tile tt and accumulates dV, wave (tt, 1) holds V of
+// tile tt and accumulates dK, both over the full D.  Per chunk of 32 queries:
+//   wave (tt, 0):  S = Q K^T,  P = 2^{c S - lse2}  -> LDS;  dV += P^T dO
+//   wave (tt, 1):  dP = dO V^T;  (P from LDS)  dS = P (dP - delta);  dK += dS^T Q
+// P crosses once, in fp32, so dS is formed from the same fp32 P as with one
+// wave per tile.  Each wave evaluates only its own half of the elementwise work
+// (the exponentials or the dS products), one of K / V and one set of
+// accumulators, so a WG fits twice on a CU (registers <= 256 per lane, LDS <
+// 80 KB): one WG's mask building and gather latency overlap the other's MFMAs.
+// One chunk per step; NST steps of Q, dO, lse and delta in flight through LDS
+// DMA, as in fta_sparse_dkv_kernel.
 // ----------------------------------------------------------------------------
 template <int D>
 struct DkvSplitShape {
@@ -1465,6 +1467,7 @@ struct DkvSplitShape {
     static constexpr int STAGE_B = LD_OFF + NW * 256;
     static constexpr int NST = (D <= 64) ? 4 : 3;
     static_assert(2 * TILE % NTHR == 0, "whole DMA instructions per wave");
+    static_assert(NST >= 3, "steps k - 1 and k live, at least one in flight");
     static_assert(NST * STAGE_B + 2 * 2 * 32 * 32 * 4 + 3 * kSegC * 4 + 2 * kBitsW * 4 + 64 <= 80 * 1024,
                   "two WGs per CU");
 };
@@ -1476,10 +1479,10 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
     constexpr int NW = Sh::NW, QSEG = Sh::QSEG, TILE = Sh::TILE, LQ = Sh::LQ, NST = Sh::NST;
     using SW = FtaSwz<QSEG>;
     constexpr int KS = D / 16;
-    constexpr int DH = D / 64;  // 32-column d tiles per half
+    constexpr int DT32 = D / 32;  // 32-column d tiles
     constexpr int TT = 2;
     __shared__ __align__(1024) unsigned char sStage[NST][Sh::STAGE_B];
-    __shared__ float sX[TT][2][16][64];  // [tile][P, dP][i][lane]
+    __shared__ float sX[2][TT][16][64];  // [step parity][tile][i][lane]: P of the last two steps
     __shared__ uint32_t sMask[TT][kSegC];
     __shared__ int sList[kSegC];
     __shared__ uint32_t sBits[TT][kBitsW];
@@ -1493,7 +1496,8 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hf = lane >> 5;
-    const int tt = wave & 1, hv = wave >> 1;
+    const int tt = wave & 1;
+    const bool hv = (wave >> 1) != 0;  // wave-uniform role: false = K / P / dV, true = V / dS / dK
     const int Tb = 2;
 
     const int krel = 32 * tt + (lane & 31);  // key of this lane's column, relative to block start
@@ -1506,7 +1510,7 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
     const float* lsep = nullptr;
     const float* dlp = nullptr;
 
-    // K (hv = 0) or V (hv = 1) rows of this tile, full D
+    // K (role 0) or V (role 1) rows of this tile, full D
     uint4 kv[KS];
     {
         const uint16_t* src = hv ? a.v + b * a.v_sb + hk * a.v_sh : a.k + b * a.k_sb + hk * a.k_sh;
@@ -1543,163 +1547,201 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
     const int l_row = lv & 31;
     const uint32_t lds0 = fta_lds_addr(&sStage[0][0]);
 
-    f32x16 dka[DH], dva[DH];
+    // the rest runs in one copy per role, so each keeps only its own values live
+    auto run = [&](auto role) {
+        constexpr bool HV = decltype(role)::value;
+        f32x16 acc[DT32];  // dV (role 0) or dK / scale (role 1): rows = keys, lane column = d
 #pragma unroll
-    for (int dt = 0; dt < DH; ++dt)
+        for (int dt = 0; dt < DT32; ++dt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            dka[dt][i] = 0.f;
-            dva[dt][i] = 0.f;
-        }
+            for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
 
-    // the query heads that share this K/V head (one without GQA): their
-    // membership, Q, dO, lse and delta; dK / dV accumulate over all of them
-    const int ngq = GQA ? a.G : 1;  // a constant 1 without GQA: no head loop in that code
-    for (int gq = 0; gq < ngq; ++gq) {
-        const int h = hk * a.G + gq;
-        const int bh = b * a.H + h;
-        qp = a.q + b * a.q_sb + h * a.q_sh;
-        dp = a.dout + b * a.d_sb + h * a.d_sh;
-        lsep = a.lse2_in + (int64_t)bh * a.N;  // log2 units: no per-element scaling
-        dlp = a.delta_in + (int64_t)bh * a.N;
-        l_base = l_isd ? dlp : lsep;
-        if (gq > 0) {
-            __syncthreads();  // the previous head's membership rows are no longer read
-            bits_lds = fta_stage_kv_bits<TT>(a, bh, wk, Tb, sBits);
-        }
-        for (int seg0 = 0; seg0 < a.NC; seg0 += kSegC) {
-            const int segn = min(kSegC, a.NC - seg0);
-            const int U = fta_build_kv_masks<TT>(a, bh, wk, Tb, seg0, segn, bits_lds, sBits, sMask, sList, s_tmp);
-            if (U == 0) continue;
+        // the query heads that share this K/V head (one without GQA): their
+        // membership, Q, dO, lse and delta; dK / dV accumulate over all of them
+        const int ngq = GQA ? a.G : 1;  // a constant 1 without GQA: no head loop in that code
+        for (int gq = 0; gq < ngq; ++gq) {
+            const int h = hk * a.G + gq;
+            const int bh = b * a.H + h;
+            qp = a.q + b * a.q_sb + h * a.q_sh;
+            dp = a.dout + b * a.d_sb + h * a.d_sh;
+            lsep = a.lse2_in + (int64_t)bh * a.N;  // log2 units: no per-element scaling
+            dlp = a.delta_in + (int64_t)bh * a.N;
+            l_base = l_isd ? dlp : lsep;
+            if (gq > 0) {
+                __syncthreads();  // the previous head's membership rows are no longer read
+                bits_lds = fta_stage_kv_bits<TT>(a, bh, wk, Tb, sBits);
+            }
+            for (int seg0 = 0; seg0 < a.NC; seg0 += kSegC) {
+                const int segn = min(kSegC, a.NC - seg0);
+                const int U = fta_build_kv_masks<TT>(a, bh, wk, Tb, seg0, segn, bits_lds, sBits, sMask, sList, s_tmp);
+                if (U == 0) continue;
 
-            // gather chunk list entry k into stage buffer st
-            auto issue = [&](int st, int k) {
-                const uint32_t sbase = lds0 + st * Sh::STAGE_B;
-                const int c = __builtin_amdgcn_readfirstlane(seg0 + sList[k]);
-                const int t0 = 32 * c - a.q_pad;
-                if (t0 >= 0 && t0 + 31 < a.N) {
+                // gather chunk list entry k into stage buffer st
+                auto issue = [&](int st, int k) {
+                    const uint32_t sbase = lds0 + st * Sh::STAGE_B;
+                    const int c = __builtin_amdgcn_readfirstlane(seg0 + sList[k]);
+                    const int t0 = 32 * c - a.q_pad;
+                    if (t0 >= 0 && t0 + 31 < a.N) {
 #pragma unroll
-                    for (int i = 0; i < LQ; ++i) {
-                        const int blk = i * NW + wave;
-                        const int ten = (blk * 64) / TILE;
-                        const char* base =
-                            reinterpret_cast<const char*>(ten == 1 ? dp + (int64_t)t0 * a.d_sn : qp + (int64_t)t0 * a.q_sn);
-                        fta_dma16_at(base + roff[i], sbase + blk * 1024);
+                        for (int i = 0; i < LQ; ++i) {
+                            const int blk = i * NW + wave;
+                            const int ten = (blk * 64) / TILE;
+                            const char* base =
+                                reinterpret_cast<const char*>(ten == 1 ? dp + (int64_t)t0 * a.d_sn : qp + (int64_t)t0 * a.q_sn);
+                            fta_dma16_at(base + roff[i], sbase + blk * 1024);
+                        }
+                    } else {  // a chunk at a sequence edge: clamp its rows (masked off) into [0, N)
+#pragma unroll
+                        for (int i = 0; i < LQ; ++i) {
+                            const int blk = i * NW + wave;
+                            const int ten = (blk * 64) / TILE;
+                            const int r2 = (blk * 64 + lane) % TILE;
+                            const int row = r2 / QSEG;
+                            int j = SW::slot(row, r2 - row * QSEG);
+                            if (j * 8 >= a.Dreal) j = 0;
+                            const int t = min(max(t0 + row, 0), a.N - 1);
+                            fta_dma16_at((ten == 1 ? dp + (int64_t)t * a.d_sn : qp + (int64_t)t * a.q_sn) + j * 8,
+                                         sbase + blk * 1024);
+                        }
                     }
-                } else {  // a chunk at a sequence edge: clamp its rows (masked off) into [0, N)
-#pragma unroll
-                    for (int i = 0; i < LQ; ++i) {
-                        const int blk = i * NW + wave;
-                        const int ten = (blk * 64) / TILE;
-                        const int r2 = (blk * 64 + lane) % TILE;
-                        const int row = r2 / QSEG;
-                        int j = SW::slot(row, r2 - row * QSEG);
-                        if (j * 8 >= a.Dreal) j = 0;
-                        const int t = min(max(t0 + row, 0), a.N - 1);
-                        fta_dma16_at((ten == 1 ? dp + (int64_t)t * a.d_sn : qp + (int64_t)t * a.q_sn) + j * 8,
-                                     sbase + blk * 1024);
-                    }
-                }
-                const int t = min(max(t0 + l_row, 0), a.N - 1);
-                fta_dma4_at(l_base + t, sbase + Sh::LD_OFF + wave * 256);
-            };
+                    const int t = min(max(t0 + l_row, 0), a.N - 1);
+                    fta_dma4_at(l_base + t, sbase + Sh::LD_OFF + wave * 256);
+                };
 
+                // Software pipeline, one barrier per step: iteration k computes S_k / P_k
+                // and dV_k (role 0) and dP_k (role 1); role 1 forms dS_{k-1} from P_{k-1}
+                // (written to LDS in iteration k - 1) and adds dK_{k-1}, so the stage
+                // buffers of steps k - 1 and k are live and NST - 2 steps are in flight.
 #pragma unroll
-            for (int k = 0; k < NST - 1; ++k)
-                if (k < U) issue(k, k);
-            int cur = 0;
-            for (int k = 0; k < U; ++k) {
-                if (k + NST - 2 < U)
-                    fta_wait_vmcnt<Sh::L * (NST - 2)>();
-                else
-                    fta_wait_vmcnt<0>();
-                __syncthreads();  // step k visible; step k - 1's buffer and the exchange area are free
-                if (k + NST - 1 < U) issue(cur == 0 ? NST - 1 : cur - 1, k + NST - 1);
-                const uint32_t mk = __builtin_amdgcn_readfirstlane(sMask[tt][sList[k]]);
-                const uint16_t* qb = reinterpret_cast<const uint16_t*>(&sStage[cur][0]);
-                const uint16_t* ob = qb + TILE * 8;
-                const float* ld = reinterpret_cast<const float*>(&sStage[cur][Sh::LD_OFF]);
-                f32x16 own;  // P (hv = 0) or dP (hv = 1)
-                if (mk) {
-                    const uint16_t* ab = hv ? ob : qb;
+                for (int k = 0; k < NST - 2; ++k)
+                    if (k < U) issue(k, k);
+                int cur = 0;       // stage buffer of step k
+                bool pm = false;   // step k - 1 left its accumulation (dV or dK) to do
+                f32x16 dpp;        // role 1: dP_{k-1}
+                uint4 af[2];       // A operand of that accumulation: P_{k-1} (role 0) or dS_{k-1} (role 1)
+                for (int k = 0; k <= U; ++k) {
+                    if (k + NST - 3 < U)
+                        fta_wait_vmcnt<Sh::L * (NST - 3)>();
+                    else
+                        fta_wait_vmcnt<0>();
+                    // step k visible; step k - 2's buffer is free; P_{k-1} visible, sX[k & 1] free
+                    __syncthreads();
+                    if (k + NST - 2 < U) issue(cur >= 2 ? cur - 2 : cur + NST - 2, k + NST - 2);
+                    const int prv = cur == 0 ? NST - 1 : cur - 1;  // stage buffer of step k - 1
+                    const uint32_t mk = (k < U) ? __builtin_amdgcn_readfirstlane(sMask[tt][sList[k]]) : 0u;
+                    const uint16_t* qb = reinterpret_cast<const uint16_t*>(&sStage[cur][0]);
+                    const uint16_t* ob = qb + TILE * 8;
+                    const float* ld = reinterpret_cast<const float*>(&sStage[cur][Sh::LD_OFF]);
+                    // B operand of step k - 1's accumulation: dO^T (role 0, dV) or Q^T (role 1, dK)
+                    const uint16_t* bb1 =
+                        reinterpret_cast<const uint16_t*>(&sStage[pm ? prv : cur][0]) + (HV ? 0 : TILE * 8);
+                    if (!pm) af[0] = af[1] = fta_zero4();
+                    if (HV && pm) {  // dS_{k-1} = P_{k-1} (dP_{k-1} - delta)
+                        const float* ld1 = reinterpret_cast<const float*>(&sStage[prv][Sh::LD_OFF]);
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) own[i] = 0.f;
+                        for (int ks = 0; ks < 2; ++ks) {
+                            float dv8[8];
 #pragma unroll
-                    for (int ks = 0; ks < KS; ++ks)
-                        own = E::mma(*reinterpret_cast<const uint4*>(ab + SW::off(lane & 31, 2 * ks + hf)), kv[ks], own);
-                    if (hv == 0) {
-                        if (mk == 0xffffffffu && __ballot(!kok) == 0ull) {
-                            // every row of the chunk selected, every key valid: no mask
-#pragma unroll
-                            for (int i = 0; i < 16; ++i) own[i] = fta_exp2(fmaf(own[i], a.c, -ld[c_row(i, lane)]));
-                        } else {
-#pragma unroll
-                            for (int i = 0; i < 16; ++i) {
-                                const int r = c_row(i, lane);
-                                // a selected row with a valid key has a finite lse
-                                const bool ok = kok && ((mk >> r) & 1u);
-                                const float ex = fta_exp2(fmaf(own[i], a.c, -ld[r]));
-                                own[i] = ok ? ex : 0.f;
+                            for (int e = 0; e < 8; ++e) {
+                                const int i = 8 * ks + e;
+                                dv8[e] = sX[(k + 1) & 1][tt][i][lane] * (dpp[i] - ld1[32 + c_row(i, lane)]);
                             }
+                            af[ks] = make_uint4(E::pack2(dv8[0], dv8[1]), E::pack2(dv8[2], dv8[3]),
+                                                E::pack2(dv8[4], dv8[5]), E::pack2(dv8[6], dv8[7]));
                         }
                     }
+                    // S_k / dP_k (a dependent chain) interleaved with step k - 1's
+                    // accumulation (independent MFMAs): the matrix pipe stays fed
+                    f32x16 own;  // S_k then P_k (role 0) or dP_k (role 1)
+                    const uint16_t* ab = HV ? ob : qb;
+                    auto mmas = [&](auto with_s, auto with_acc) {
+                        constexpr bool WS = decltype(with_s)::value, WA = decltype(with_acc)::value;
+                        if (WS) {
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) sX[tt][hv][i][lane] = own[i];
+                            for (int i = 0; i < 16; ++i) own[i] = 0.f;
+                        }
+                        // fragments of link j + 1 load while link j's MFMAs run
+                        uint4 fs[2], fa2[2];
+                        auto load = [&](int j, int slot) {
+                            if (WS) fs[slot] = *reinterpret_cast<const uint4*>(ab + SW::off(lane & 31, 2 * j + hf));
+                            if (WA) fa2[slot] = fta_tr_frag_sw<QSEG>(bb1, (j / DT32) * 16, (j % DT32) * 32, lane);
+                        };
+                        constexpr int NR = (WS ? 1 : 0) + (WA ? 2 : 0);  // LDS reads per link
+                        constexpr int NM = (WS ? 1 : 0) + (WA ? 1 : 0);  // MFMAs per link
+                        load(0, 0);
+#pragma unroll
+                        for (int j = 0; j < KS; ++j) {  // KS = 2 * DT32: one accumulation MFMA per chain link
+                            if (j + 1 < KS) load(j + 1, (j + 1) & 1);
+                            if (WS) own = E::mma(fs[j & 1], kv[j], own);
+                            if (WA) acc[j % DT32] = E::mma(af[j / DT32], fa2[j & 1], acc[j % DT32]);
+                        }
+                        __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+#pragma unroll
+                        for (int j = 0; j < KS; ++j) {
+                            if (j + 1 < KS) __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+                        }
+                    };
+                    // One instruction stream for every case (separate variants cost the
+                    // register budget): without a pending accumulation the A operand is zero
+                    // and the B operand the current step's finite data (acc += 0 exactly);
+                    // without a chain the S / dP result is discarded.
+                    if (mk || pm) mmas(std::true_type{}, std::true_type{});
+                    if (mk) {
+                        if (!HV) {  // P_k = 2^{c S_k - lse2}: to LDS for role 1, packed for dV_k
+                            if (mk == 0xffffffffu && __ballot(!kok) == 0ull) {
+                                // every row of the chunk selected, every key valid: no mask
+#pragma unroll
+                                for (int i = 0; i < 16; ++i) own[i] = fta_exp2(fmaf(own[i], a.c, -ld[c_row(i, lane)]));
+                            } else {
+#pragma unroll
+                                for (int i = 0; i < 16; ++i) {
+                                    const int r = c_row(i, lane);
+                                    // a selected row with a valid key has a finite lse
+                                    const bool ok = kok && ((mk >> r) & 1u);
+                                    const float ex = fta_exp2(fmaf(own[i], a.c, -ld[r]));
+                                    own[i] = ok ? ex : 0.f;
+                                }
+                            }
+#pragma unroll
+                            for (int i = 0; i < 16; ++i) sX[k & 1][tt][i][lane] = own[i];
+#pragma unroll
+                            for (int ks = 0; ks < 2; ++ks)
+                                af[ks] = make_uint4(E::pack2(own[8 * ks], own[8 * ks + 1]),
+                                                    E::pack2(own[8 * ks + 2], own[8 * ks + 3]),
+                                                    E::pack2(own[8 * ks + 4], own[8 * ks + 5]),
+                                                    E::pack2(own[8 * ks + 6], own[8 * ks + 7]));
+                        } else {
+                            dpp = own;
+                        }
+                    }
+                    pm = mk != 0u;
+                    cur = (cur == NST - 1) ? 0 : cur + 1;
                 }
-                __syncthreads();  // both halves of every tile exchanged
-                if (mk) {
-                    uint4 pf[2], dsf[2];
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-                        float pv[8], dv8[8];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const int i = 8 * ks + e;
-                            const float other = sX[tt][hv ^ 1][i][lane];
-                            const float p = hv ? other : own[i];
-                            const float dpv = hv ? own[i] : other;
-                            pv[e] = p;
-                            dv8[e] = p * (dpv - ld[32 + c_row(i, lane)]);
-                        }
-                        pf[ks] = make_uint4(E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
-                                            E::pack2(pv[6], pv[7]));
-                        dsf[ks] = make_uint4(E::pack2(dv8[0], dv8[1]), E::pack2(dv8[2], dv8[3]),
-                                             E::pack2(dv8[4], dv8[5]), E::pack2(dv8[6], dv8[7]));
-                    }
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-                        for (int dt = 0; dt < DH; ++dt) {
-                            const int d0 = (hv * DH + dt) * 32;
-                            dva[dt] = E::mma(pf[ks], fta_tr_frag_sw<QSEG>(ob, ks * 16, d0, lane), dva[dt]);
-                            dka[dt] = E::mma(dsf[ks], fta_tr_frag_sw<QSEG>(qb, ks * 16, d0, lane), dka[dt]);
-                        }
-                    }
-                }
-                cur = (cur == NST - 1) ? 0 : cur + 1;
+                __syncthreads();  // all waves done with the stage buffers, sMask and sList
             }
-            __syncthreads();  // all waves done with the stage buffers, sMask and sList
         }
-    }
 
-    // C layout: lane column = d, rows = keys c_row(i, lane)
-    uint16_t* kout = a.out0 + b * a.o0_sb + hk * a.o0_sh;
-    uint16_t* vout = a.out1 + b * a.o1_sb + hk * a.o1_sh;
+        // C layout: lane column = d, rows = keys c_row(i, lane); role 0 stores dV, role 1 dK
+        uint16_t* out = HV ? a.out0 + b * a.o0_sb + hk * a.o0_sh : a.out1 + b * a.o1_sb + hk * a.o1_sh;
+        const int64_t osn = HV ? a.o0_sn : a.o1_sn;
+        const float osc = HV ? a.scale : 1.f;
 #pragma unroll
-    for (int dt = 0; dt < DH; ++dt) {
-        const int d = (hv * DH + dt) * 32 + (lane & 31);
-        if (d >= a.Dreal) continue;
+        for (int dt = 0; dt < DT32; ++dt) {
+            const int d = dt * 32 + (lane & 31);
+            if (d >= a.Dreal) continue;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int kr = 32 * tt + c_row(i, lane);
-            const int t = wk * a.kvb - a.kv_pad + kr;
-            if (kr < a.kvb && t >= 0 && t < a.N) {
-                const uint32_t pk = E::pack2(dka[dt][i] * a.scale, dva[dt][i]);
-                kout[(int64_t)t * a.o0_sn + d] = (uint16_t)(pk & 0xffffu);
-                vout[(int64_t)t * a.o1_sn + d] = (uint16_t)(pk >> 16);
+            for (int i = 0; i < 16; ++i) {
+                const int kr = 32 * tt + c_row(i, lane);
+                const int t = wk * a.kvb - a.kv_pad + kr;
+                if (kr < a.kvb && t >= 0 && t < a.N) out[(int64_t)t * osn + d] = (uint16_t)(E::pack2(acc[dt][i] * osc, 0.f) & 0xffffu);
             }
         }
-    }
+    };
+    if (hv)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
 }
 
 

@@ -418,33 +418,36 @@ __global__ __launch_bounds__(256) void fta_argsort_desc_rows_kernel(const int32_
 }
 
 // Launch order of the dK/dV workgroups of one (b, K/V head): the KV blocks
-// sorted by the first q-block that selected them (ties: ascending block id;
+// sorted by the first q-block that selected them, then by the number of
+// q-blocks that selected them (descending; ties: ascending block id;
 // unselected blocks last), read from the membership bitmap of the group's
 // first query head.  KV blocks picked by the same run of q-blocks then run
-// side by side on one XCD and share its L2 copy of those q-blocks' Q and dO.
+// side by side on one XCD and share its L2 copy of those q-blocks' Q and dO;
+// under dense selections (every block's first q-block near 0) the count order
+// makes the workgroups that start together walk q-block lists of the same
+// length and density, so they stay at nearby q-blocks until they finish.
 __global__ __launch_bounds__(256) void fta_kv_order_kernel(const uint32_t* __restrict__ sel, int M, int QW, int H,
                                                            int G, int32_t* __restrict__ order) {
-    __shared__ int key[4096];
+    __shared__ uint64_t key[4096];
     const int64_t rk = blockIdx.x;               // (b, K/V head)
     const int64_t bh = (rk / (H / G)) * H + (rk % (H / G)) * G;  // its first query head
     const uint32_t* rows = sel + bh * (int64_t)M * QW;
     for (int m = threadIdx.x; m < M; m += 256) {
-        int first = 0x7fffffff;
-        for (int w = 0; w < QW; ++w) {
+        uint32_t first = 0x7fffffffu;
+        uint32_t cnt = 0;
+        for (int w = QW - 1; w >= 0; --w) {
             const uint32_t bits = rows[(int64_t)m * QW + w];
-            if (bits) {
-                first = w * 32 + __builtin_ctz(bits);
-                break;
-            }
+            if (bits) first = (uint32_t)(w * 32 + __builtin_ctz(bits));
+            cnt += __builtin_popcount(bits);
         }
-        key[m] = first;
+        key[m] = ((uint64_t)first << 32) | (0xffffffffu - cnt);
     }
     __syncthreads();
     for (int i = threadIdx.x; i < M; i += 256) {
-        const int ki = key[i];
+        const uint64_t ki = key[i];
         int rank = 0;
         for (int j = 0; j < M; ++j) {
-            const int kj = key[j];
+            const uint64_t kj = key[j];
             rank += (kj < ki) || (kj == ki && j < i);
         }
         order[rk * M + rank] = i;
