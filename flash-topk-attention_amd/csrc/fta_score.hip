@@ -727,6 +727,9 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
         }
         __syncthreads();  // block m + 1 visible; every wave is past block m - 1
         if (m + 3 < M) issue(m + 3);
+        // this block's group top-2 entry, read now so its latency hides under the stages
+        float2 gtop = make_float2(0.f, 0.f);
+        if constexpr (STREAM) gtop = sG[gslot][tid];
 
         float e0[2], e1[2];
         const int kb = m * 64 - pad_head;
@@ -822,7 +825,7 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
             if (pass) cst[spos + rank] = make_uint2(__builtin_bit_cast(uint32_t, mine), ((uint32_t)lane << 16) | m);
             spos += __popcll(mk);
             // group top-2 (max / min as med3 with an infinite third operand)
-            float2 t = sG[gslot][tid];
+            float2 t = gtop;
             t.y = __builtin_amdgcn_fmed3f(t.y, __builtin_amdgcn_fmed3f(t.x, ak, -FTA_INF), FTA_INF);
             t.x = __builtin_amdgcn_fmed3f(t.x, ak, FTA_INF);
             sG[gslot][tid] = t;
