@@ -28,7 +28,10 @@
 
 namespace fta {
 int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint32_t* sel, hipStream_t st);
-int launch_kv_order(const uint32_t* sel, int B, int H, int Hk, int M, int QW, int32_t* order, hipStream_t st);
+int launch_kv_order(const uint32_t* sel, int B, int H, int Hk, int M, int QW, int32_t* order, int32_t* head_work,
+                    int32_t* head_perm, hipStream_t st);
+int launch_head_order_merged(const int32_t* merged, int BH, int QM, int W, int M, int32_t* head_work,
+                             int32_t* head_perm, hipStream_t st);
 }  // namespace fta
 
 constexpr int kSeg = 512;    // KV blocks per mask segment (forward / dQ)
@@ -47,6 +50,7 @@ struct AttnArgs {
     const int32_t* merged;  // [BH][QM][W]
     const uint32_t* sel;    // [BH][Mkv][QW] membership bitmap (dK/dV)
     const int32_t* kv_order;  // [B*Hk][Mkv] dK/dV launch order of the KV blocks (null: natural order)
+    const int32_t* head_perm;  // [B*Hk] (dK/dV) or [B*H] (forward, dQ): head at each head position (null: natural order)
     int QM, W, QW;
     uint16_t* out0;  // o (forward) / dq / dk
     int64_t o0_sb, o0_sh, o0_sn;
@@ -417,8 +421,9 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
     __shared__ int s_tmp[8];
 
     const int wgi = fta_xcd_remap(blockIdx.x, a.total);
-    const int bh = wgi / a.wg_per_bh;
-    const int wq = wgi - bh * a.wg_per_bh;
+    const int hp = wgi / a.wg_per_bh;                     // head position
+    const int bh = a.head_perm ? a.head_perm[hp] : hp;  // (b, h)
+    const int wq = wgi - hp * a.wg_per_bh;
     const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -832,8 +837,9 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
     __shared__ int s_tmp[8];
 
     const int wgi = fta_xcd_remap(blockIdx.x, a.total);
-    const int bh = wgi / a.wg_per_bh;
-    const int wq = wgi - bh * a.wg_per_bh;
+    const int hp = wgi / a.wg_per_bh;                     // head position
+    const int bh = a.head_perm ? a.head_perm[hp] : hp;  // (b, h)
+    const int wq = wgi - hp * a.wg_per_bh;
     const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1489,8 +1495,9 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
     __shared__ int s_tmp[8];
 
     const int wgi = fta_xcd_remap(blockIdx.x, a.total);
-    const int bhk = wgi / a.wg_per_bh;  // (b, K/V head)
-    const int wk0 = wgi - bhk * a.wg_per_bh;
+    const int hp = wgi / a.wg_per_bh;  // head position
+    const int bhk = a.head_perm ? a.head_perm[hp] : hp;  // (b, K/V head)
+    const int wk0 = wgi - hp * a.wg_per_bh;
     const int wk = a.kv_order ? a.kv_order[(int64_t)bhk * a.wg_per_bh + wk0] : wk0;  // KV block
     const int b = bhk / a.Hk, hk = bhk - (bhk / a.Hk) * a.Hk;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1928,10 +1935,14 @@ size_t sel_bytes(int B, int H, const Geo& G) {
     return fta::align_up((size_t)B * H * G.Mkv * ((G.QM + 31) / 32) * sizeof(uint32_t));
 }
 
-// the backward workspace: membership bitmap, lse in log2 units, dK/dV launch order
+// the forward workspace: per-head work, head placement (fta_head_balance_kernel)
+// and the 64 partial counts per head they are summed from
+size_t fwd_bytes(int B, int H) { return fta::align_up((size_t)B * H * (2 + 64) * sizeof(int32_t)); }
+
+// the backward workspace: membership bitmap, lse in log2 units, dK/dV launch order (KV blocks, then heads)
 size_t bwd_bytes(int B, int H, int N, const Geo& G) {
     return sel_bytes(B, H, G) + fta::align_up((size_t)B * H * N * sizeof(float)) +
-           fta::align_up((size_t)B * H * G.Mkv * sizeof(int32_t));
+           fta::align_up((size_t)B * H * G.Mkv * sizeof(int32_t)) + fta::align_up((size_t)B * H * 2 * sizeof(int32_t));
 }
 
 }  // namespace
@@ -1946,7 +1957,7 @@ size_t fta_sparse_attn_fwd_workspace_size(int B, int H, int N, int D, int q_bloc
     if (geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
                  &G) != FTA_OK)
         return 0;
-    return 0;  // the forward needs no scratch
+    return fwd_bytes(B, H);  // per-head work and XCD placement of the heads
 }
 
 int fta_sparse_attn_fwd_gqa(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -1962,10 +1973,18 @@ int fta_sparse_attn_fwd_gqa(const void* q, const int64_t* q_strides, const void*
                       &G);
     if (rc != FTA_OK) return rc;
     if (W <= 0) return fta::arg_error("sparse_attn: qblock_topk must be positive");
-    (void)workspace;
-    (void)workspace_bytes;
     hipStream_t st = (hipStream_t)stream;
     AttnArgs a = {};
+    // XCD placement of the heads by their work (only with a workspace: callers
+    // that pass none keep the natural order)
+    if (workspace != nullptr && workspace_bytes >= fwd_bytes(B, H)) {
+        int32_t* head_work = (int32_t*)workspace;
+        int32_t* head_perm = head_work + B * H;
+        if ((rc = fta::launch_head_order_merged(merged_indices, B * H, QM, W, G.Mkv, head_work, head_perm, st)) !=
+            FTA_OK)
+            return rc;
+        a.head_perm = head_perm;
+    }
     a.q = (const uint16_t*)q;
     a.q_sb = q_strides[0];
     a.q_sh = q_strides[1];
@@ -2050,16 +2069,33 @@ int bwd_common(AttnArgs& a, Geo& G, const void* q, const int64_t* q_strides, con
     a.G = H / Hk;
     return FTA_OK;
 }
-}  // namespace
 
-extern "C" {
+// 64-key blocks at D 64 / 128 (the split dK/dV kernel) run in the launch order
+// of fta_kv_order_kernel and the head placement of fta_head_balance_kernel
+bool uses_kv_order(int kv_block_size, const Geo& G) {
+    return kv_block_size > 32 && kv_block_size <= 64 && (G.Dk == 64 || G.Dk == 128) && G.Mkv <= 4096;
+}
 
-int fta_sparse_attn_bwd_dq(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
-                           const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
-                           int dtype, int B, int H, int Hk, int N, int D, const int32_t* merged_indices, int QM, int W,
-                           int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head,
-                           int kv_pad_tail, float scale, const float* lse, const float* delta, void* dq,
-                           const int64_t* dq_strides, void* stream) {
+// the head placement fta_sparse_attn_bwd_dkv left in the workspace (null if it made none)
+const int32_t* dkv_head_perm(const void* workspace, int B, int H, int N, int D, int QM, int q_block_size,
+                             int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head, int kv_pad_tail) {
+    Geo G;
+    if (geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM, &G) !=
+            FTA_OK ||
+        !uses_kv_order(kv_block_size, G))
+        return nullptr;
+    const char* p = (const char*)workspace + sel_bytes(B, H, G) + fta::align_up((size_t)B * H * N * sizeof(float)) +
+                    fta::align_up((size_t)B * H * G.Mkv * sizeof(int32_t));
+    return (const int32_t*)p + B * H;  // head work [B*Hk], then the placement
+}
+
+// dQ with an optional head placement (null: natural order)
+int bwd_dq_impl(const int32_t* head_perm, const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
+                int dtype, int B, int H, int Hk, int N, int D, const int32_t* merged_indices, int QM, int W,
+                int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head,
+                int kv_pad_tail, float scale, const float* lse, const float* delta, void* dq,
+                const int64_t* dq_strides, void* stream) {
     FTA_TRY_BEGIN
     AttnArgs a;
     Geo G;
@@ -2068,6 +2104,7 @@ int fta_sparse_attn_bwd_dq(const void* q, const int64_t* q_strides, const void* 
                         kv_pad_tail, scale, lse, delta);
     if (rc != FTA_OK) return rc;
     hipStream_t st = (hipStream_t)stream;
+    a.head_perm = head_perm;
     a.out0 = (uint16_t*)dq;
     a.o0_sb = dq_strides[0];
     a.o0_sh = dq_strides[1];
@@ -2079,6 +2116,20 @@ int fta_sparse_attn_bwd_dq(const void* q, const int64_t* q_strides, const void* 
     if (dtype == FTA_DTYPE_F16) return launch_dq_dt<FTA_DTYPE_F16>(a, G.Dk, a.total, st);
     return fta::arg_error("sparse_attn_bwd: dtype must be bf16 or fp16");
     FTA_TRY_END
+}
+}  // namespace
+
+extern "C" {
+
+int fta_sparse_attn_bwd_dq(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                           const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
+                           int dtype, int B, int H, int Hk, int N, int D, const int32_t* merged_indices, int QM, int W,
+                           int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head,
+                           int kv_pad_tail, float scale, const float* lse, const float* delta, void* dq,
+                           const int64_t* dq_strides, void* stream) {
+    return bwd_dq_impl(nullptr, q, q_strides, k, k_strides, v, v_strides, dout, do_strides, dtype, B, H, Hk, N, D,
+                       merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head,
+                       kv_pad_tail, scale, lse, delta, dq, dq_strides, stream);
 }
 
 int fta_sparse_attn_bwd_dkv(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -2109,10 +2160,15 @@ int fta_sparse_attn_bwd_dkv(const void* q, const int64_t* q_strides, const void*
     a.sel = sel;
     a.lse2_in = lse2;
     // 64-key blocks at D 64 / 128 (the split kernel): launch in first-q-block order
-    if (kv_block_size > 32 && kv_block_size <= 64 && (G.Dk == 64 || G.Dk == 128) && G.Mkv <= 4096) {
+    if (uses_kv_order(kv_block_size, G)) {
         int32_t* order = (int32_t*)((char*)lse2 + fta::align_up((size_t)B * H * N * sizeof(float)));
-        if ((rc = fta::launch_kv_order(sel, B, H, Hk, G.Mkv, (QM + 31) / 32, order, st)) != FTA_OK) return rc;
+        int32_t* head_work = (int32_t*)((char*)order + fta::align_up((size_t)B * H * G.Mkv * sizeof(int32_t)));
+        int32_t* head_perm = head_work + B * Hk;
+        if ((rc = fta::launch_kv_order(sel, B, H, Hk, G.Mkv, (QM + 31) / 32, order, head_work, head_perm, st)) !=
+            FTA_OK)
+            return rc;
         a.kv_order = order;
+        a.head_perm = head_perm;
     }
     a.out0 = (uint16_t*)dk;
     a.o0_sb = dk_strides[0];
@@ -2137,14 +2193,19 @@ int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void*
                             int kv_pad_head, int kv_pad_tail, float scale, const float* lse, const float* delta,
                             void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
                             const int64_t* dv_strides, void* workspace, size_t workspace_bytes, void* stream) {
-    int rc = fta_sparse_attn_bwd_dq(q, q_strides, k, k_strides, v, v_strides, dout, do_strides, dtype, B, H, Hk, N, D,
-                                    merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail,
-                                    kv_pad_head, kv_pad_tail, scale, lse, delta, dq, dq_strides, stream);
+    // dK / dV first: its launch-order pass also places the heads on XCDs by their
+    // work, which dQ reuses when every query head has its own K / V head
+    int rc = fta_sparse_attn_bwd_dkv(q, q_strides, k, k_strides, v, v_strides, dout, do_strides, dtype, B, H, Hk, N,
+                                     D, merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail,
+                                     kv_pad_head, kv_pad_tail, scale, lse, delta, dk, dk_strides, dv, dv_strides,
+                                     workspace, workspace_bytes, stream);
     if (rc != FTA_OK) return rc;
-    return fta_sparse_attn_bwd_dkv(q, q_strides, k, k_strides, v, v_strides, dout, do_strides, dtype, B, H, Hk, N, D,
-                                   merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail,
-                                   kv_pad_head, kv_pad_tail, scale, lse, delta, dk, dk_strides, dv, dv_strides,
-                                   workspace, workspace_bytes, stream);
+    const int32_t* perm = (Hk == H) ? dkv_head_perm(workspace, B, H, N, D, QM, q_block_size, kv_block_size,
+                                                    q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail)
+                                    : nullptr;
+    return bwd_dq_impl(perm, q, q_strides, k, k_strides, v, v_strides, dout, do_strides, dtype, B, H, Hk, N, D,
+                       merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head,
+                       kv_pad_tail, scale, lse, delta, dq, dq_strides, stream);
 }
 
 int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,

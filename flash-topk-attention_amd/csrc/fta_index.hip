@@ -417,41 +417,119 @@ __global__ __launch_bounds__(256) void fta_argsort_desc_rows_kernel(const int32_
     }
 }
 
-// Launch order of the dK/dV workgroups of one (b, K/V head): the KV blocks
-// sorted by the first q-block that selected them, then by the number of
-// q-blocks that selected them (descending; ties: ascending block id;
-// unselected blocks last), read from the membership bitmap of the group's
-// first query head.  KV blocks picked by the same run of q-blocks then run
-// side by side on one XCD and share its L2 copy of those q-blocks' Q and dO;
-// under dense selections (every block's first q-block near 0) the count order
-// makes the workgroups that start together walk q-block lists of the same
-// length and density, so they stay at nearby q-blocks until they finish.
+// Launch order of the dK/dV workgroups of one (b, K/V head): the KV blocks by
+// the number of q-blocks that selected them, most first (ties: ascending block
+// id), from the membership bitmap of the group's first query head.  Longest
+// first shortens the tail of each XCD's queue, and under dense selections the
+// WGs that start together walk q-block lists of the same length and density,
+// so they stay at nearby q-blocks and share their Q / dO in L2.  head_work
+// receives the head's total (selections plus one setup step per block) for
+// fta_head_balance_kernel.
 __global__ __launch_bounds__(256) void fta_kv_order_kernel(const uint32_t* __restrict__ sel, int M, int QW, int H,
-                                                           int G, int32_t* __restrict__ order) {
-    __shared__ uint64_t key[4096];
+                                                           int G, int32_t* __restrict__ order,
+                                                           int32_t* __restrict__ head_work) {
+    __shared__ uint32_t key[4096];
+    __shared__ int s_work;
+    if (threadIdx.x == 0) s_work = 0;
+    __syncthreads();
     const int64_t rk = blockIdx.x;               // (b, K/V head)
     const int64_t bh = (rk / (H / G)) * H + (rk % (H / G)) * G;  // its first query head
     const uint32_t* rows = sel + bh * (int64_t)M * QW;
     for (int m = threadIdx.x; m < M; m += 256) {
-        uint32_t first = 0x7fffffffu;
         uint32_t cnt = 0;
-        for (int w = QW - 1; w >= 0; --w) {
-            const uint32_t bits = rows[(int64_t)m * QW + w];
-            if (bits) first = (uint32_t)(w * 32 + __builtin_ctz(bits));
-            cnt += __builtin_popcount(bits);
-        }
-        key[m] = ((uint64_t)first << 32) | (0xffffffffu - cnt);
+        for (int w = 0; w < QW; ++w) cnt += __builtin_popcount(rows[(int64_t)m * QW + w]);
+        key[m] = 0xffffffffu - cnt;
+        atomicAdd(&s_work, (int)cnt + 1);  // steps of the block's WG, plus one for its setup
     }
     __syncthreads();
+    if (threadIdx.x == 0) head_work[rk] = s_work;
     for (int i = threadIdx.x; i < M; i += 256) {
-        const uint64_t ki = key[i];
+        const uint32_t ki = key[i];
         int rank = 0;
         for (int j = 0; j < M; ++j) {
-            const uint64_t kj = key[j];
+            const uint32_t kj = key[j];
             rank += (kj < ki) || (kj == ki && j < i);
         }
         order[rk * M + rank] = i;
     }
+}
+
+// XCD placement of the dK/dV heads.  The WGs of head position p run on XCD
+// p / (n / 8) (fta_xcd_remap gives each XCD a contiguous range of the grid), so
+// heads of unequal total work (head_work: selection counts plus setup) leave
+// some XCDs busy after others have drained.  Greedy longest-first placement of
+// the heads into 8 bins of n / 8 heads each evens the XCD totals; perm[p] is
+// the head at position p (bins in XCD order, heaviest first within a bin).
+// n not a multiple of 8, or above 4096 heads: identity.
+__global__ __launch_bounds__(256) void fta_head_balance_kernel(const int32_t* __restrict__ head_work, int n,
+                                                               int32_t* __restrict__ perm) {
+    __shared__ int w[4096];
+    __shared__ int by_rank[4096];
+    if (n % 8 != 0 || n > 4096) {
+        for (int i = threadIdx.x; i < n; i += 256) perm[i] = i;
+        return;
+    }
+    for (int i = threadIdx.x; i < n; i += 256) w[i] = head_work[i];
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const int wi = w[i];
+        int rank = 0;
+        for (int j = 0; j < n; ++j) rank += (w[j] > wi) || (w[j] == wi && j < i);
+        by_rank[rank] = i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int cap = n / 8;
+        long long load[8];
+        int fill[8];
+        for (int x = 0; x < 8; ++x) {
+            load[x] = 0;
+            fill[x] = 0;
+        }
+        for (int r = 0; r < n; ++r) {
+            const int hd = by_rank[r];
+            int best = -1;
+            for (int x = 0; x < 8; ++x)
+                if (fill[x] < cap && (best < 0 || load[x] < load[best])) best = x;
+            perm[best * cap + fill[best]] = hd;
+            ++fill[best];
+            load[best] += w[hd];
+        }
+    }
+}
+
+// Work of each (b, h) for the forward / dQ head placement: its valid merged
+// entries (KV blocks selected by its q-blocks) plus one setup step per four
+// q-blocks.  WG (bh, j) counts q-block rows j, j + kHeadParts, ... into
+// part[bh][j]; fta_head_sum_kernel adds the parts.
+constexpr int kHeadParts = 64;
+__global__ __launch_bounds__(256) void fta_head_work_merged_kernel(const int32_t* __restrict__ merged, int QM, int W,
+                                                                   int M, int32_t* __restrict__ part) {
+    __shared__ int s_work;
+    if (threadIdx.x == 0) s_work = 0;
+    __syncthreads();
+    const int bh = blockIdx.x / kHeadParts, j = blockIdx.x % kHeadParts;
+    int c = 0;
+    for (int qb = j; qb < QM; qb += kHeadParts) {
+        const int32_t* row = merged + ((int64_t)bh * QM + qb) * W;
+        for (int i = threadIdx.x; i < W; i += 256) {
+            const int m = row[i];
+            c += (m >= 0 && m < M);
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+    if ((threadIdx.x & 63) == 0) atomicAdd(&s_work, c);
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = s_work;
+}
+
+__global__ __launch_bounds__(256) void fta_head_sum_kernel(const int32_t* __restrict__ part, int BH, int QM,
+                                                           int32_t* __restrict__ head_work) {
+    const int bh = blockIdx.x * 256 + threadIdx.x;
+    if (bh >= BH) return;
+    int w = QM / 4;
+    for (int j = 0; j < kHeadParts; ++j) w += part[(int64_t)bh * kHeadParts + j];
+    head_work[bh] = w;
 }
 
 // Global stable descending sort of counts (reference: sort_by_count_cuda.py:33-67):
@@ -579,10 +657,31 @@ int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint3
     return check_launch("fta_sel_bitmap_kernel");
 }
 
-int launch_kv_order(const uint32_t* sel, int B, int H, int Hk, int M, int QW, int32_t* order, hipStream_t st) {
+int launch_kv_order(const uint32_t* sel, int B, int H, int Hk, int M, int QW, int32_t* order, int32_t* head_work,
+                    int32_t* head_perm, hipStream_t st) {
     if (M <= 0 || B * Hk == 0) return FTA_OK;
-    hipLaunchKernelGGL(fta_kv_order_kernel, dim3((unsigned)(B * Hk)), dim3(256), 0, st, sel, M, QW, H, H / Hk, order);
-    return check_launch("fta_kv_order_kernel");
+    hipLaunchKernelGGL(fta_kv_order_kernel, dim3((unsigned)(B * Hk)), dim3(256), 0, st, sel, M, QW, H, H / Hk, order,
+                       head_work);
+    int rc = check_launch("fta_kv_order_kernel");
+    if (rc != FTA_OK) return rc;
+    hipLaunchKernelGGL(fta_head_balance_kernel, dim3(1), dim3(256), 0, st, head_work, B * Hk, head_perm);
+    return check_launch("fta_head_balance_kernel");
+}
+
+int launch_head_order_merged(const int32_t* merged, int BH, int QM, int W, int M, int32_t* head_work,
+                             int32_t* head_perm, hipStream_t st) {
+    if (BH <= 0) return FTA_OK;
+    // part sums after head_work and head_perm: [BH][kHeadParts]
+    int32_t* part = head_perm + BH;
+    hipLaunchKernelGGL(fta_head_work_merged_kernel, dim3((unsigned)(BH * kHeadParts)), dim3(256), 0, st, merged, QM,
+                       W, M, part);
+    int rc = check_launch("fta_head_work_merged_kernel");
+    if (rc != FTA_OK) return rc;
+    hipLaunchKernelGGL(fta_head_sum_kernel, dim3((unsigned)((BH + 255) / 256)), dim3(256), 0, st, part, BH, QM,
+                       head_work);
+    if ((rc = check_launch("fta_head_sum_kernel")) != FTA_OK) return rc;
+    hipLaunchKernelGGL(fta_head_balance_kernel, dim3(1), dim3(256), 0, st, head_work, BH, head_perm);
+    return check_launch("fta_head_balance_kernel");
 }
 }  // namespace fta
 

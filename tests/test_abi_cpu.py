@@ -41,10 +41,11 @@ def test_error_path_returns_status_without_gpu():
     rc = L.fta_qblock_merge(None, None, 1, 32, 16, 5000, 16, None, None, None, None)
     assert rc == _lib.FTA_ERR_UNSUPPORTED
     assert L.fta_sparse_attn_bwd_workspace_size(1, 1, 100, 64, 32, 64, 0, 0, 0, 0) == 0  # 100 % 32 != 0
-    assert L.fta_sparse_attn_fwd_workspace_size(1, 2, 128, 64, 32, 64, 0, 0, 0, 0) == 0  # forward has no scratch
+    assert L.fta_sparse_attn_fwd_workspace_size(1, 2, 128, 64, 32, 64, 0, 0, 0, 0) == 768  # head work, placement and 64 partial counts per head
     # backward scratch = membership bitmap [B*H][M_kv][ceil(QM/32)] uint32, lse in log2
-    # units [B*H][N] fp32, dK/dV launch order [B*H][M_kv] int32, each 256-byte aligned
-    assert L.fta_sparse_attn_bwd_workspace_size(1, 2, 128, 64, 32, 64, 0, 0, 0, 0) == 256 + 1024 + 256
+    # units [B*H][N] fp32, dK/dV launch order [B*H][M_kv] int32, head work and head
+    # placement [B*H] int32 each, each region 256-byte aligned
+    assert L.fta_sparse_attn_bwd_workspace_size(1, 2, 128, 64, 32, 64, 0, 0, 0, 0) == 256 + 1024 + 256 + 256
 
 
 def test_api_validation_matches_reference_errors():
