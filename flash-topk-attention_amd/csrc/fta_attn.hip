@@ -946,25 +946,6 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
             if (mk) {
                 const uint16_t* kbase = reinterpret_cast<const uint16_t*>(&sStage[cur][0]);
                 const uint16_t* vbase = kbase + Sh::TEN_B / 2;
-                f32x16 s[2], dpv[2];
-#pragma unroll
-                for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        s[sb][i] = 0.f;
-                        dpv[sb][i] = 0.f;
-                    }
-                const int nsb = two ? 2 : 1;
-#pragma unroll
-                for (int sb = 0; sb < 2; ++sb) {
-                    if (sb >= nsb) break;
-#pragma unroll
-                    for (int ks = 0; ks < KS; ++ks) {
-                        const int off = SW::off(sb * 32 + (lane & 31), 2 * ks + hf);
-                        s[sb] = E::mma(*reinterpret_cast<const uint4*>(kbase + off), qf[ks], s[sb]);
-                        dpv[sb] = E::mma(*reinterpret_cast<const uint4*>(vbase + off), df[ks], dpv[sb]);
-                    }
-                }
                 // A lane whose query column is not selected uses an infinite lse:
                 // all its exps are exactly 0.  Keys outside [klo, khi) (chunks at
                 // a sequence end, or past a short block) get -inf scores in place
@@ -972,28 +953,55 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
                 const bool colok = rowlive && ((mk >> (lane & 31)) & 1u);
                 const float lse_c = colok ? lse2 : FTA_INF;
                 const int klo = max(0, -kb), khi = min(min(rem, 64), a.N - kb);
-                if (klo > 0 || khi < 64) {
-                    const unsigned kw = (unsigned)max(khi - klo, 0);  // a chunk past N has khi < klo
+                const int nsb = two ? 2 : 1;
+                uint4 dsf[4];
+                // one 32-key half at a time (S and dP of one half live), the K / V
+                // fragments loaded one MFMA pair ahead
 #pragma unroll
-                    for (int sb = 0; sb < 2; ++sb)
+                for (int sb = 0; sb < 2; ++sb) {
+                    if (sb >= nsb) break;
+                    f32x16 s, dpv;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        s[i] = 0.f;
+                        dpv[i] = 0.f;
+                    }
+                    // rows 32 sb + r share row r's swizzle: one offset per k slot
+                    const uint16_t* kh = kbase + sb * 32 * QSEG * 8;
+                    const uint16_t* vh = vbase + sb * 32 * QSEG * 8;
+                    uint4 kf[2], vf[2];
+                    kf[0] = *reinterpret_cast<const uint4*>(kh + SW::off(lane & 31, hf));
+                    vf[0] = *reinterpret_cast<const uint4*>(vh + SW::off(lane & 31, hf));
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) {
+                        if (ks + 1 < KS) {
+                            const int off = SW::off(lane & 31, 2 * (ks + 1) + hf);
+                            kf[(ks + 1) & 1] = *reinterpret_cast<const uint4*>(kh + off);
+                            vf[(ks + 1) & 1] = *reinterpret_cast<const uint4*>(vh + off);
+                        }
+                        s = E::mma(kf[ks & 1], qf[ks], s);
+                        dpv = E::mma(vf[ks & 1], df[ks], dpv);
+                    }
+                    if (klo > 0 || khi < 64) {
+                        const unsigned kw = (unsigned)max(khi - klo, 0);  // a chunk past N has khi < klo
 #pragma unroll
                         for (int i = 0; i < 16; ++i) {
                             const int rel = sb * 32 + c_row(i, lane);
-                            s[sb][i] = ((unsigned)(rel - klo) < kw) ? s[sb][i] : -FTA_INF;
+                            s[i] = ((unsigned)(rel - klo) < kw) ? s[i] : -FTA_INF;
                         }
-                }
-                uint4 dsf[4];
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    float dsv[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const int sb = ks >> 1, i = 8 * (ks & 1) + e;
-                        const float p = fta_exp2(fmaf(s[sb][i], a.c, -lse_c));
-                        dsv[e] = p * (dpv[sb][i] - dl);
                     }
-                    dsf[ks] = make_uint4(E::pack2(dsv[0], dsv[1]), E::pack2(dsv[2], dsv[3]),
-                                         E::pack2(dsv[4], dsv[5]), E::pack2(dsv[6], dsv[7]));
+#pragma unroll
+                    for (int k2 = 0; k2 < 2; ++k2) {
+                        float dsv[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const int i = 8 * k2 + e;
+                            const float p = fta_exp2(fmaf(s[i], a.c, -lse_c));
+                            dsv[e] = p * (dpv[i] - dl);
+                        }
+                        dsf[2 * sb + k2] = make_uint4(E::pack2(dsv[0], dsv[1]), E::pack2(dsv[2], dsv[3]),
+                                                      E::pack2(dsv[4], dsv[5]), E::pack2(dsv[6], dsv[7]));
+                    }
                 }
                 const int nks = two ? 4 : 2;
 #pragma unroll
