@@ -206,6 +206,9 @@ size_t fta_sparse_attn_fwd_workspace_size(int B, int H, int N, int D, int q_bloc
  * csrc/sparse_attn_kernel.cu:368-457) behind flash_sparse_attn_cuda
  * (flash_topk_attn_v2/sparse_attn_cuda.py:42-110); lse = softmax_max + softmax_lse
  * of the reference (flash_topk_attn_v2/sparse_attn.py:391).
+ * The workspace (fta_sparse_attn_fwd_workspace_size bytes: per-head work and
+ * the XCD placement of the heads) is optional: with workspace == NULL or too
+ * few bytes the heads run in natural order, with the same results.
  */
 int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k,
                         const int64_t* k_strides, const void* v, const int64_t* v_strides,
@@ -252,6 +255,8 @@ size_t fta_sparse_attn_bwd_workspace_size(int B, int H, int N, int D, int q_bloc
  * (flash_topk_attn_v2/sparse_attn_bwd_dq_cuda.py:44-108,
  * sparse_attn_bwd_dkv_cuda.py:44-118) as called from
  * FlashSparseAttnFunc.backward (flash_topk_attn_v2/sparse_attn.py:163-224).
+ * Runs dK/dV first, then dQ in the XCD head placement the dK/dV pass left in
+ * the workspace (when every query head has its own K/V head).
  */
 int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k,
                         const int64_t* k_strides, const void* v, const int64_t* v_strides,
@@ -267,7 +272,7 @@ int fta_sparse_attn_bwd(const void* q, const int64_t* q_strides, const void* k,
  * dQ alone ([B][N][H][D] strided; k, v with Hk heads): replaces
  * sparse_attn_bwd_dq_launch (flash_topk_attn_v2/csrc/sparse_attn_bwd_dq.cpp:3-19)
  * behind flash_sparse_attn_bwd_dq_cuda (sparse_attn_bwd_dq_cuda.py:44-108).
- * Needs no workspace.
+ * Needs no workspace (heads in natural order).
  */
 int fta_sparse_attn_bwd_dq(const void* q, const int64_t* q_strides, const void* k,
                            const int64_t* k_strides, const void* v, const int64_t* v_strides,
@@ -281,7 +286,8 @@ int fta_sparse_attn_bwd_dq(const void* q, const int64_t* q_strides, const void* 
  * dK / dV alone (Hk heads, each summed over its H / Hk query heads without
  * atomics).  Builds the KV block -> q-block membership bitmap and the lse in
  * log2 units in the workspace (fta_sparse_attn_bwd_workspace_size bytes) and
- * walks it.  Replaces build_reverse_indices_launch + sparse_attn_bwd_dkv_launch
+ * walks it; for 64-key blocks at D 64 / 128 the workspace also holds the launch
+ * order (KV blocks by selection count) and the XCD placement of the heads.  Replaces build_reverse_indices_launch + sparse_attn_bwd_dkv_launch
  * (flash_topk_attn_v2/csrc/build_reverse_indices.cpp:3-14,
  * sparse_attn_bwd_dkv.cpp:3-20) behind flash_sparse_attn_bwd_dkv_cuda
  * (sparse_attn_bwd_dkv_cuda.py:44-118).
