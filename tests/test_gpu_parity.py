@@ -553,3 +553,63 @@ def test_topk_candidate_streams_exact(case):
     if pattern == "increasing" and pad == (0, 0):
         M = N // 64
         assert (ri[..., 0] == M - 1).all()
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_head_placement_keeps_results(D):
+    """The XCD head placement (forward with a workspace, combined backward) only
+    reorders workgroups: o / lse equal the forward without a workspace, and the
+    combined backward's dq / dk / dv equal the dQ and dK/dV entries run apart,
+    bit for bit, on heads of very unequal work (16 heads: placement active)."""
+    from flash_topk_attn_v2 import _lib
+
+    B, H, N, g, b = 2, 8, 1024, 32, 64
+    say(f"[head placement] B{B} H{H} N{N} D{D}")
+    QM, M, W = N // g, N // b, 16
+    rng = np.random.default_rng(5)
+    merged = np.full((B, H, QM, W), -1, dtype=np.int32)
+    for bb in range(B):
+        for h in range(H):
+            n = 1 + (h * 5 + bb * 3) % W  # per-head list length: unequal work
+            for qm in range(QM):
+                merged[bb, h, qm, :n] = rng.permutation(M)[:n]
+    merged = torch.from_numpy(merged).cuda()
+    q, k, v, do = (rand((B, N, H * D), 90 + i, torch.bfloat16, "cuda") for i in range(4))
+    L = _lib.lib()
+    st = _lib.i64arr([N * H * D, D, H * D])
+    dt = _lib.dtype_code(torch.bfloat16)
+    stream = torch.cuda.current_stream().cuda_stream
+    geo = (B, H, N, D, g, b, 0, 0, 0, 0)
+    ws_f = _lib.workspace(L.fta_sparse_attn_fwd_workspace_size(*geo), "cuda")
+    assert ws_f.numel() > 0
+
+    def fwd(ws):
+        o = torch.empty_like(q)
+        lse = torch.empty(B, H, N, dtype=torch.float32, device="cuda")
+        rc = L.fta_sparse_attn_fwd(q.data_ptr(), st, k.data_ptr(), st, v.data_ptr(), st, dt, B, H, N, D,
+                                   merged.data_ptr(), QM, W, g, b, 0, 0, 0, 0, D ** -0.5, o.data_ptr(), st,
+                                   lse.data_ptr(), ws.data_ptr() if ws is not None else None,
+                                   ws.numel() if ws is not None else 0, stream)
+        _lib.check(rc, "fta_sparse_attn_fwd")
+        return o, lse
+
+    o1, lse1 = fwd(ws_f)
+    o2, lse2 = fwd(None)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(lse1, lse2)
+
+    from flash_topk_attn_v2.sparse_attn_bwd import preprocess_delta
+    delta = preprocess_delta(o1, do, H)
+    ws_b = _lib.workspace(L.fta_sparse_attn_bwd_workspace_size(*geo), "cuda")
+    args = (q.data_ptr(), st, k.data_ptr(), st, v.data_ptr(), st, do.data_ptr(), st, dt, B, H, H, N, D,
+            merged.data_ptr(), QM, W, g, b, 0, 0, 0, 0, D ** -0.5, lse1.data_ptr(), delta.data_ptr())
+    g1 = [torch.empty_like(q) for _ in range(3)]
+    _lib.check(L.fta_sparse_attn_bwd_gqa(*args, g1[0].data_ptr(), st, g1[1].data_ptr(), st, g1[2].data_ptr(), st,
+                                         ws_b.data_ptr(), ws_b.numel(), stream), "fta_sparse_attn_bwd_gqa")
+    g2 = [torch.empty_like(q) for _ in range(3)]
+    _lib.check(L.fta_sparse_attn_bwd_dq(*args, g2[0].data_ptr(), st, stream), "fta_sparse_attn_bwd_dq")
+    _lib.check(L.fta_sparse_attn_bwd_dkv(*args, g2[1].data_ptr(), st, g2[2].data_ptr(), st, ws_b.data_ptr(),
+                                         ws_b.numel(), stream), "fta_sparse_attn_bwd_dkv")
+    torch.cuda.synchronize()
+    for a, c in zip(g1, g2):
+        assert torch.equal(a, c)
