@@ -428,22 +428,35 @@ __global__ __launch_bounds__(256) void fta_argsort_desc_rows_kernel(const int32_
 __global__ __launch_bounds__(256) void fta_kv_order_kernel(const uint32_t* __restrict__ sel, int M, int QW, int H,
                                                            int G, int32_t* __restrict__ order,
                                                            int32_t* __restrict__ head_work) {
+    // WG (b, K/V head, slice): counts every block's selections (coalesced reads
+    // of the bitmap rows, LDS atomics), then ranks the blocks of its slice of 256
     __shared__ uint32_t key[4096];
     __shared__ int s_work;
-    if (threadIdx.x == 0) s_work = 0;
-    __syncthreads();
     const int64_t rk = blockIdx.x;               // (b, K/V head)
+    const int slice = blockIdx.y;
     const int64_t bh = (rk / (H / G)) * H + (rk % (H / G)) * G;  // its first query head
     const uint32_t* rows = sel + bh * (int64_t)M * QW;
-    for (int m = threadIdx.x; m < M; m += 256) {
-        uint32_t cnt = 0;
-        for (int w = 0; w < QW; ++w) cnt += __builtin_popcount(rows[(int64_t)m * QW + w]);
-        key[m] = 0xffffffffu - cnt;
-        atomicAdd(&s_work, (int)cnt + 1);  // steps of the block's WG, plus one for its setup
-    }
+    for (int m = threadIdx.x; m < M; m += 256) key[m] = 0xffffffffu;
+    if (threadIdx.x == 0) s_work = M;  // one setup step per block
     __syncthreads();
-    if (threadIdx.x == 0) head_work[rk] = s_work;
-    for (int i = threadIdx.x; i < M; i += 256) {
+    const int64_t nw = (int64_t)M * QW;
+    int cw = 0;
+    for (int64_t i0 = threadIdx.x; i0 < nw; i0 += 8 * 256) {
+        uint32_t wv[8];  // eight loads in flight before any use
+#pragma unroll
+        for (int u = 0; u < 8; ++u) wv[u] = (i0 + u * 256 < nw) ? rows[i0 + u * 256] : 0u;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = __builtin_popcount(wv[u]);
+            if (c) atomicSub(&key[(i0 + u * 256) / QW], (uint32_t)c);
+            cw += c;
+        }
+    }
+    atomicAdd(&s_work, cw);
+    __syncthreads();
+    if (slice == 0 && threadIdx.x == 0) head_work[rk] = s_work;
+    const int i = slice * 256 + threadIdx.x;
+    if (i < M) {
         const uint32_t ki = key[i];
         int rank = 0;
         for (int j = 0; j < M; ++j) {
@@ -478,22 +491,27 @@ __global__ __launch_bounds__(256) void fta_head_balance_kernel(const int32_t* __
         by_rank[rank] = i;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    // greedy placement by the first wave: lane x < 8 keeps bin x's load and fill
+    if (threadIdx.x < 64) {
+        const int x = threadIdx.x;
         const int cap = n / 8;
-        long long load[8];
-        int fill[8];
-        for (int x = 0; x < 8; ++x) {
-            load[x] = 0;
-            fill[x] = 0;
-        }
+        long long load = 0;
+        int fill = 0;
         for (int r = 0; r < n; ++r) {
             const int hd = by_rank[r];
-            int best = -1;
-            for (int x = 0; x < 8; ++x)
-                if (fill[x] < cap && (best < 0 || load[x] < load[best])) best = x;
-            perm[best * cap + fill[best]] = hd;
-            ++fill[best];
-            load[best] += w[hd];
+            // the open bin with the least load (ties: lowest bin)
+            long long key = (x < 8 && fill < cap) ? load * 8 + x : 0x7fffffffffffffffll;
+#pragma unroll
+            for (int off = 4; off > 0; off >>= 1) {
+                const long long o = __shfl_xor(key, off, 8);
+                key = o < key ? o : key;
+            }
+            const int best = (int)(key & 7);
+            if (x == best) {
+                perm[best * cap + fill] = hd;
+                ++fill;
+                load += w[hd];
+            }
         }
     }
 }
@@ -660,8 +678,8 @@ int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint3
 int launch_kv_order(const uint32_t* sel, int B, int H, int Hk, int M, int QW, int32_t* order, int32_t* head_work,
                     int32_t* head_perm, hipStream_t st) {
     if (M <= 0 || B * Hk == 0) return FTA_OK;
-    hipLaunchKernelGGL(fta_kv_order_kernel, dim3((unsigned)(B * Hk)), dim3(256), 0, st, sel, M, QW, H, H / Hk, order,
-                       head_work);
+    hipLaunchKernelGGL(fta_kv_order_kernel, dim3((unsigned)(B * Hk), (unsigned)((M + 255) / 256)), dim3(256), 0, st,
+                       sel, M, QW, H, H / Hk, order, head_work);
     int rc = check_launch("fta_kv_order_kernel");
     if (rc != FTA_OK) return rc;
     hipLaunchKernelGGL(fta_head_balance_kernel, dim3(1), dim3(256), 0, st, head_work, B * Hk, head_perm);
