@@ -1476,9 +1476,9 @@ struct DkvSplitShape {
     static constexpr int QSEG = D / 8;
     static constexpr int TILE = 32 * QSEG;              // 16-byte slots per 32-row tile
     static constexpr int LQ = 2 * TILE / NTHR;          // DMA instructions per wave per step (Q, dO)
-    static constexpr int L = LQ + 1;                    // + lse / delta
+    static constexpr int L = LQ + 1;                    // + lse / delta (wave 0)
     static constexpr int LD_OFF = 2 * TILE * 16;        // byte offset of lse / delta in a step
-    static constexpr int STAGE_B = LD_OFF + NW * 256;
+    static constexpr int STAGE_B = LD_OFF + 256;
     static constexpr int NST = (D <= 64) ? 4 : 3;
     static_assert(2 * TILE % NTHR == 0, "whole DMA instructions per wave");
     static_assert(NST >= 3, "steps k - 1 and k live, at least one in flight");
@@ -1555,7 +1555,7 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
         if (j * 8 >= a.Dreal) j = 0;  // columns past D: any finite data (never stored)
         roff[i] = 2 * ((int64_t)row * (ten == 1 ? a.d_sn : a.q_sn) + j * 8);
     }
-    // lse / delta: wave 0's 256 bytes hold [lse 32][delta 32] (other waves load a duplicate)
+    // lse / delta: wave 0's DMA writes [lse 32][delta 32] (256 bytes)
     const int lv = wave * 64 + lane;
     const bool l_isd = lv >= 32 && lv < 64;
     const float* l_base = nullptr;
@@ -1619,8 +1619,10 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
                                          sbase + blk * 1024);
                         }
                     }
-                    const int t = min(max(t0 + l_row, 0), a.N - 1);
-                    fta_dma4_at(l_base + t, sbase + Sh::LD_OFF + wave * 256);
+                    if (wave == 0) {  // lse and delta of the chunk's 32 rows: one 256-byte DMA
+                        const int t = min(max(t0 + l_row, 0), a.N - 1);
+                        fta_dma4_at(l_base + t, sbase + Sh::LD_OFF);
+                    }
                 };
 
                 // Software pipeline, one barrier per step: iteration k computes S_k / P_k
@@ -1635,10 +1637,12 @@ __global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a
                 f32x16 dpp;        // role 1: dP_{k-1}
                 uint4 af[2];       // A operand of that accumulation: P_{k-1} (role 0) or dS_{k-1} (role 1)
                 for (int k = 0; k <= U; ++k) {
-                    if (k + NST - 3 < U)
+                    if (k + NST - 3 >= U)
+                        fta_wait_vmcnt<0>();
+                    else if (wave == 0)  // wave 0 issues the lse / delta DMA as well
                         fta_wait_vmcnt<Sh::L * (NST - 3)>();
                     else
-                        fta_wait_vmcnt<0>();
+                        fta_wait_vmcnt<(Sh::L - 1) * (NST - 3)>();
                     // step k visible; step k - 2's buffer is free; P_{k-1} visible, sX[k & 1] free
                     __syncthreads();
                     if (k + NST - 2 < U) issue(cur >= 2 ? cur - 2 : cur + NST - 2, k + NST - 2);
