@@ -1337,14 +1337,13 @@ __global__ __launch_bounds__(256, 4) void fta_topk_stream_kernel(
             const bool em = ((m[i] == 0) & (pad_head > 0)) | ((m[i] == M - 1) & (pad_tail > 0));
             pend[i] = (c0 + i * 64 + lane < total) & (em | (x[i] >= s_pre[wave][owner[i]]));
         }
-        bool any = false;
-#pragma unroll
-        for (int i = 0; i < NC; ++i) any |= pend[i];
-        while (__ballot(any) != 0ull) {
+        // park the step's entries; while some find their owner's list full,
+        // merge every list (flush) and park those again
+        for (;;) {
             int pos[NC];
 #pragma unroll
             for (int i = 0; i < NC; ++i) pos[i] = pend[i] ? atomicAdd(&s_cnt[wave][owner[i]], 1) : CAP;
-            any = false;
+            bool any = false;
 #pragma unroll
             for (int i = 0; i < NC; ++i) {
                 const bool ok = pend[i] & (pos[i] < CAP);
@@ -1355,7 +1354,8 @@ __global__ __launch_bounds__(256, 4) void fta_topk_stream_kernel(
                 pend[i] = pend[i] & !ok;
                 any |= pend[i];
             }
-            if (__ballot(any) != 0ull) flush();
+            if (__ballot(any) == 0ull) break;
+            flush();
         }
 #pragma unroll
         for (int i = 0; i < NC; ++i) ea[i] = eb[i];
