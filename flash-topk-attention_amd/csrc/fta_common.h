@@ -188,6 +188,12 @@ __device__ __forceinline__ void fta_dma16_at(const void* g, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
                  "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
 }
+// The same DMA with a wave-uniform base (SGPR pair) and a 32-bit per-lane byte offset:
+// one VGPR per address instead of two.
+__device__ __forceinline__ void fta_dma16_so(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
+                 "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");
+}
 __device__ __forceinline__ void fta_dma4_at(const void* g, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g),
                  "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory", "m0");

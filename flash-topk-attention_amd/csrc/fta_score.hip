@@ -568,15 +568,15 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     fta_wait_vmcnt<0>();
 
     // Per-lane DMA sources within a K block: instruction i of this wave fills the
-    // 1 KB LDS block i * 4 + wave; roff = row * k_sn + column (elements).
-    int roff[LQ];
+    // 1 KB LDS block i * 4 + wave; roff = (row * k_sn + column) * 2 bytes.
+    uint32_t roff[LQ];
 #pragma unroll
     for (int i = 0; i < LQ; ++i) {
         const int sidx = (i * 4 + wave) * 64 + lane;
         const int row = sidx / QSEG;
         int j = SW::slot(row, sidx - row * QSEG);
         if (j * 8 >= Dreal) j = 0;  // columns past D meet zero q columns
-        roff[i] = row * (int)k_sn + j * 8;
+        roff[i] = (uint32_t)(row * (int)k_sn + j * 8) * 2u;
     }
     const uint32_t lds0 = fta_lds_addr(&sK[0][0]);
     auto issue = [&](int m) {
@@ -585,11 +585,14 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
         if (kb >= 0 && kb + 64 <= N) {
             const uint16_t* base = kp + (int64_t)kb * k_sn;
 #pragma unroll
-            for (int i = 0; i < LQ; ++i) fta_dma16_at(base + roff[i], sb + (i * 4 + wave) * 1024);
+            for (int i = 0; i < LQ; ++i) fta_dma16_so(base, roff[i], sb + (i * 4 + wave) * 1024);
         } else {  // block at a sequence edge: clamp rows (masked to -inf below)
+            // addresses formed here, not kept live across the loop for this rare case
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
 #pragma unroll
             for (int i = 0; i < LQ; ++i) {
-                const int sidx = (i * 4 + wave) * 64 + lane;
+                const int sidx = (i * 4 + wave) * 64 + ln;
                 const int row = sidx / QSEG;
                 int j = SW::slot(row, sidx - row * QSEG);
                 if (j * 8 >= Dreal) j = 0;
@@ -599,8 +602,8 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
         }
     };
     // scores of keys 32 s .. 32 s + 31 of block m for both query tiles
-    auto mma_half = [&](int m, int s, f32x16 (&acc)[2]) {
-        const uint16_t* base = reinterpret_cast<const uint16_t*>(&sK[m & (NBUF - 1)][0]) + s * 32 * QSEG * 8;
+    auto mma_half = [&](int bi, int s, f32x16 (&acc)[2]) {
+        const uint16_t* base = reinterpret_cast<const uint16_t*>(&sK[bi][0]) + s * 32 * QSEG * 8;
         const f32x16 zacc = {};
         uint4 a[KS];
 #pragma unroll
@@ -641,8 +644,8 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     // order by the compiler): group g's K fragment and a scalar copy of the
     // scale used by its exps pass through one, and its exp / add results feed
     // the next group's, so each group's MFMAs, exps and adds stay in their window.
-    auto stage = [&](int mb, int s, f32x16 (&dst)[2], const f32x16 (&src)[2], float* e_out) {
-        const uint16_t* base = reinterpret_cast<const uint16_t*>(&sK[mb & (NBUF - 1)][0]) + s * 32 * QSEG * 8;
+    auto stage = [&](int bi, int s, f32x16 (&dst)[2], const f32x16 (&src)[2], float* e_out) {
+        const uint16_t* base = reinterpret_cast<const uint16_t*>(&sK[bi][0]) + s * 32 * QSEG * 8;
         const f32x16 zacc = {};
         uint4 a[KS];
 #pragma unroll
@@ -693,7 +696,7 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     // candidate-stream state: this wave's key / mask streams, write position,
     // current filter bound and group slot
     uint2* cst = nullptr;
-    int spos = 0, gslot = 0;
+    int spos = 0;
     // lanes past N never pass: their bound is +inf
     const bool lane_ok = qbase + lane < N;
     float sbnd = lane_ok ? -FTA_INF : FTA_INF;
@@ -717,7 +720,12 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     f32x16 h0[2], h1[2];
     mma_half(0, 0, h0);
 
-    auto block = [&](int m) {
+    // Block m; jm = m mod 8, a compile-time constant in the unrolled main loop, so
+    // the K buffer (m mod 4) and the group slot (m mod NG) become immediate LDS
+    // offsets instead of per-read address arithmetic.
+    auto block = [&](int m, auto jm) {
+        const int bm = int(jm) & (NBUF - 1), bn = (int(jm) + 1) & (NBUF - 1);  // buffers of m, m + 1
+        const int gslot = m & (NG > 0 ? NG - 1 : 0);
         // block m + 1 resident: blocks issued so far = min(M, m + 3)
         if (m + 1 < M) {
             if (m + 3 <= M)
@@ -740,16 +748,16 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
             // their registers.  Masked scores are -inf: their exps are 0.
             const bool edge = kb < 0 || kb + 64 > N;
             if (edge) edge_mask(m, 0, h0);
-            stage(m, 1, h1, h0, e0);      // MFMAs of half 1 of block m, exps of half 0
+            stage(bm, 1, h1, h0, e0);     // MFMAs of half 1 of block m, exps of half 0
             if (edge) edge_mask(m, 1, h1);
-            stage(m + 1, 0, h0, h1, e1);  // MFMAs of half 0 of block m + 1, exps of half 1
+            stage(bn, 0, h0, h1, e1);     // MFMAs of half 0 of block m + 1, exps of half 1
         } else {
             edge_mask(m, 0, h0);
-            mma_half(m, 1, h1);
+            mma_half(bm, 1, h1);
             sums16(h0, R, e0);
             edge_mask(m, 1, h1);
             if (m + 1 < M) {
-                mma_half(m + 1, 0, h0);
+                mma_half(bn, 0, h0);
             }
             sums16(h1, R, e1);
         }
@@ -771,8 +779,8 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
         if (__ballot(bad) != 0ull) {
             // exact path: reference = this block's max (scores recomputed from LDS)
             f32x16 x0[2], x1[2];
-            mma_half(m, 0, x0);
-            mma_half(m, 1, x1);
+            mma_half(bm, 0, x0);
+            mma_half(bm, 1, x1);
             edge_mask(m, 0, x0);
             edge_mask(m, 1, x1);
 #pragma unroll
@@ -829,8 +837,7 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
             t.y = __builtin_amdgcn_fmed3f(t.y, __builtin_amdgcn_fmed3f(t.x, ak, -FTA_INF), FTA_INF);
             t.x = __builtin_amdgcn_fmed3f(t.x, ak, FTA_INF);
             sG[gslot][tid] = t;
-            if (++gslot == NG) {
-                gslot = 0;
+            if (gslot == NG - 1) {
                 float bnd = sG[0][tid].y;
 #pragma unroll
                 for (int j = 1; j < NG; ++j) bnd = __builtin_amdgcn_fmed3f(bnd, sG[j][tid].y, -FTA_INF);
@@ -859,8 +866,17 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
         }
     };
     // every block but the last always produces the next block's half 0
-    for (int m = 0; m + 1 < M; ++m) block(m);
-    block(M - 1);
+    {
+        int m = 0;
+        for (; m + 4 < M; m += 4) {
+            block(m, std::integral_constant<int, 0>{});
+            block(m + 1, std::integral_constant<int, 1>{});
+            block(m + 2, std::integral_constant<int, 2>{});
+            block(m + 3, std::integral_constant<int, 3>{});
+        }
+        for (; m + 1 < M; ++m) block(m, m & 3);
+        block(M - 1, (M - 1) & 3);
+    }
 
     const int qi = qbase + lane;
     if constexpr (STREAM) {
