@@ -723,11 +723,13 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     // Block m; jm = m mod 8, a compile-time constant in the unrolled main loop, so
     // the K buffer (m mod 4) and the group slot (m mod NG) become immediate LDS
     // offsets instead of per-read address arithmetic.
-    auto block = [&](int m, auto jm) {
+    // `interior`: 0 < m < M - 1 (no head / tail adjustment, a next block exists).
+    auto block = [&](int m, auto jm, auto interior) {
+        constexpr bool IN = decltype(interior)::value;
         const int bm = int(jm) & (NBUF - 1), bn = (int(jm) + 1) & (NBUF - 1);  // buffers of m, m + 1
         const int gslot = m & (NG > 0 ? NG - 1 : 0);
         // block m + 1 resident: blocks issued so far = min(M, m + 3)
-        if (m + 1 < M) {
+        if (IN || m + 1 < M) {
             if (m + 3 <= M)
                 fta_wait_vmcnt<LQ>();
             else
@@ -741,12 +743,14 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
 
         float e0[2], e1[2];
         const int kb = m * 64 - pad_head;
-        if (m + 1 < M) {
+        if (IN || m + 1 < M) {
             // Every block but the last runs the same two stages; a block at a
             // sequence edge first masks its scores in place (uniform branches),
             // so the loop-carried accumulators have one definition and keep
             // their registers.  Masked scores are -inf: their exps are 0.
-            const bool edge = kb < 0 || kb + 64 > N;
+            // pad_head, pad_tail < b and b | pad_head + N + pad_tail (checked on the host):
+            // only the first and the last block can reach past the sequence
+            const bool edge = !IN && (kb < 0 || kb + 64 > N);
             if (edge) edge_mask(m, 0, h0);
             stage(bm, 1, h1, h0, e0);     // MFMAs of half 1 of block m, exps of half 0
             if (edge) edge_mask(m, 1, h1);
@@ -823,9 +827,9 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
         const int qi = qbase + lane;
         if constexpr (STREAM) {
             // wave-uniform adjustment and edge flag (partial edge blocks always pass)
-            const float adj = ((m == 0) ? adj_head : 0.f) + ((m == M - 1) ? adj_tail : 0.f);
-            const bool em = ((m == 0) & (pad_head > 0)) | ((m == M - 1) & (pad_tail > 0));
-            const float ak = mine + adj;
+            const float adj = IN ? 0.f : ((m == 0) ? adj_head : 0.f) + ((m == M - 1) ? adj_tail : 0.f);
+            const bool em = !IN && (((m == 0) & (pad_head > 0)) | ((m == M - 1) & (pad_tail > 0)));
+            const float ak = IN ? mine : mine + adj;
             const bool pass = (ak >= sbnd) | (em & lane_ok);
             const unsigned long long mk = __ballot(pass);
             const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32),
@@ -867,15 +871,23 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     };
     // every block but the last always produces the next block's half 0
     {
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        using I3 = std::integral_constant<int, 3>;
         int m = 0;
-        for (; m + 4 < M; m += 4) {
-            block(m, std::integral_constant<int, 0>{});
-            block(m + 1, std::integral_constant<int, 1>{});
-            block(m + 2, std::integral_constant<int, 2>{});
-            block(m + 3, std::integral_constant<int, 3>{});
+        if (M > 1) {
+            block(0, I0{}, std::false_type{});
+            m = 1;
         }
-        for (; m + 1 < M; ++m) block(m, m & 3);
-        block(M - 1, (M - 1) & 3);
+        for (; m + 4 < M; m += 4) {  // m = 1 mod 4
+            block(m, I1{}, std::true_type{});
+            block(m + 1, I2{}, std::true_type{});
+            block(m + 2, I3{}, std::true_type{});
+            block(m + 3, I0{}, std::true_type{});
+        }
+        for (; m + 1 < M; ++m) block(m, m & 3, std::true_type{});
+        block(M - 1, (M - 1) & 3, std::false_type{});
     }
 
     const int qi = qbase + lane;
