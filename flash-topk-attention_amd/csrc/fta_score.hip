@@ -636,7 +636,10 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
             e[t] = fta_sum_exp2<16>(v, c, Rr[t]);
         }
     };
-    float R[2] = {-FTA_INF, -FTA_INF}, L[2] = {0.f, 0.f};
+    // R[t]: reference of tile t's query (lane & 31), used by this lane's exps of both
+    // tiles; L: running total of the lane's own (tile lane >> 5, query lane & 31)
+    float R[2] = {-FTA_INF, -FTA_INF}, L = 0.f;
+    const bool own1 = lane >= 32;
     // One pipeline stage, written in issue order: the MFMAs of half s of block mb
     // (into dst) interleaved with the exps of src, 32 / KS exps after each MFMA
     // pair.  The sums use the same 16-term tree as fta_sum_exp2<16>.
@@ -765,64 +768,74 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
             }
             sums16(h1, R, e1);
         }
-        // block totals: lanes l and l ^ 32 hold halves of the same query's sum;
-        // two lane-half swaps give every lane both tiles' totals (the same
-        // operand pairs as part + part[l ^ 32], so the results are identical)
-        float tot[2];
+        // block total of the lane's own (tile, query): lanes l and l ^ 32 hold halves
+        // of each query's sum; one lane-half swap adds them (the same operand pairs as
+        // part + part[l ^ 32], so the results are identical)
+        float tot_own;
         {
             float a = e0[0] + e1[0], b = e0[1] + e1[1];
             fta_swap32(a, b);
-            const float mine = a + b;  // tile (lane >> 5), query (lane & 31)
-            float x = mine, y = mine;
-            fta_swap32(x, y);
-            const float other = (lane < 32) ? y : x;  // the other tile, same query
-            tot[0] = (lane < 32) ? mine : other;
-            tot[1] = (lane < 32) ? other : mine;
+            tot_own = a + b;
         }
-        const bool bad = !(tot[0] < 0x1p100f) || !(tot[1] < 0x1p100f);
-        if (__ballot(bad) != 0ull) {
-            // exact path: reference = this block's max (scores recomputed from LDS)
-            f32x16 x0[2], x1[2];
-            mma_half(bm, 0, x0);
-            mma_half(bm, 1, x1);
-            edge_mask(m, 0, x0);
-            edge_mask(m, 1, x1);
+        // every (tile, query) is owned by one lane, so wave votes on tot_own cover both
+        // tiles.  The rare cases (a total that overflows the reference or grows large)
+        // share one branch, so the common path keeps R and L in place.
+        float mine;
+        if (__ballot(!(tot_own < 0x1p100f) || tot_own > 0x1p40f) != 0ull) {
+            if (__ballot(!(tot_own < 0x1p100f)) != 0ull) {
+                // exact path: reference = this block's max (scores recomputed from LDS)
+                f32x16 x0[2], x1[2];
+                mma_half(bm, 0, x0);
+                mma_half(bm, 1, x1);
+                edge_mask(m, 0, x0);
+                edge_mask(m, 1, x1);
+                const float R_old = own1 ? R[1] : R[0];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                float mx = x0[t][0];
+                for (int t = 0; t < 2; ++t) {
+                    float mx = x0[t][0];
 #pragma unroll
-                for (int i = 1; i < 16; ++i) mx = fmaxf(mx, x0[t][i]);
+                    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, x0[t][i]);
 #pragma unroll
-                for (int i = 0; i < 16; ++i) mx = fmaxf(mx, x1[t][i]);
-                mx = fmaxf(mx, fta_xor32(mx));
-                const float Rn = (mx == -FTA_INF) ? 0.f : mx * c;
-                L[t] = (L[t] > 0.f) ? L[t] * fta_exp2(R[t] - Rn) : 0.f;
-                R[t] = Rn;
-            }
-            float f0[2], f1[2];
-            sums16(x0, R, f0);
-            sums16(x1, R, f1);
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const float part = f0[t] + f1[t];
-                tot[t] = part + fta_xor32(part);
-            }
-        }
-        // lane owns query (lane & 31) of tile (lane >> 5): only its block lse is stored
-        const float tot_m = (lane >= 32) ? tot[1] : tot[0];
-        const float R_m = (lane >= 32) ? R[1] : R[0];
-        const float mine = (tot_m > 0.f) ? R_m + fta_log2(tot_m) : -FTA_INF;
-        L[0] += tot[0];
-        L[1] += tot[1];
-        if (__ballot(tot[0] > 0x1p40f || tot[1] > 0x1p40f) != 0ull) {
-            // rare: rebase a large row total on this block's lse
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-                if (tot[t] > 0x1p40f) {
-                    const float Rn = R[t] + fta_log2(tot[t]);
-                    L[t] *= fta_exp2(R[t] - Rn);
-                    R[t] = Rn;
+                    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, x1[t][i]);
+                    mx = fmaxf(mx, fta_xor32(mx));
+                    R[t] = (mx == -FTA_INF) ? 0.f : mx * c;
                 }
+                const float R_new = own1 ? R[1] : R[0];
+                L = (L > 0.f) ? L * fta_exp2(R_old - R_new) : 0.f;
+                float f0[2], f1[2];
+                sums16(x0, R, f0);
+                sums16(x1, R, f1);
+                float tot[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const float part = f0[t] + f1[t];
+                    tot[t] = part + fta_xor32(part);
+                }
+                tot_own = own1 ? tot[1] : tot[0];
+            }
+            // only the lane's own block lse is stored
+            const float R_m = own1 ? R[1] : R[0];
+            mine = (tot_own > 0.f) ? R_m + fta_log2(tot_own) : -FTA_INF;
+            L += tot_own;
+            if (__ballot(tot_own > 0x1p40f) != 0ull) {
+                // rebase a large row total on this block's lse (both tiles' references,
+                // so this lane's exps of the other tile stay in step with its owner)
+                float x = tot_own, y = tot_own;
+                fta_swap32(x, y);
+                const float other = own1 ? x : y;
+                const float tot[2] = {own1 ? other : tot_own, own1 ? tot_own : other};
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    if (tot[t] > 0x1p40f) {
+                        const float Rn = R[t] + fta_log2(tot[t]);
+                        if ((t == 1) == own1) L *= fta_exp2(R[t] - Rn);
+                        R[t] = Rn;
+                    }
+            }
+        } else {
+            const float R_m = own1 ? R[1] : R[0];
+            mine = (tot_own > 0.f) ? R_m + fta_log2(tot_own) : -FTA_INF;
+            L += tot_own;
         }
         const int qi = qbase + lane;
         if constexpr (STREAM) {
@@ -834,13 +847,19 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
             const unsigned long long mk = __ballot(pass);
             const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32),
                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
-            if (pass) cst[spos + rank] = make_uint2(__builtin_bit_cast(uint32_t, mine), ((uint32_t)lane << 16) | m);
+            if (pass) {  // wave-uniform base, 32-bit lane offset
+                uint2* dst = cst + spos;
+                dst[(uint32_t)rank] = make_uint2(__builtin_bit_cast(uint32_t, mine), ((uint32_t)lane << 16) | m);
+            }
             spos += __popcll(mk);
-            // group top-2 (max / min as med3 with an infinite third operand)
+            // group top-2 (t.y <= t.x): new second = med3(t.x, t.y, ak), new first =
+            // max(t.x, ak).  Written as instructions: the compiler's max / med3 first
+            // quiet every operand (three extra instructions), and no value here is a NaN.
             float2 t = gtop;
-            t.y = __builtin_amdgcn_fmed3f(t.y, __builtin_amdgcn_fmed3f(t.x, ak, -FTA_INF), FTA_INF);
-            t.x = __builtin_amdgcn_fmed3f(t.x, ak, FTA_INF);
-            sG[gslot][tid] = t;
+            float nx, ny;
+            asm("v_med3_f32 %0, %1, %2, %3" : "=v"(ny) : "v"(t.x), "v"(t.y), "v"(ak));
+            asm("v_max_f32 %0, %1, %2" : "=v"(nx) : "v"(t.x), "v"(ak));
+            sG[gslot][tid] = make_float2(nx, ny);
             if (gslot == NG - 1) {
                 float bnd = sG[0][tid].y;
 #pragma unroll
@@ -895,10 +914,8 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
         if (lane == 0) cand_count[(int64_t)wg * 4 + wave] = spos;
     }
     if (qi < N) {
-        const bool t1 = lane >= 32;
-        const float Rr = t1 ? R[1] : R[0];
-        const float Lr = t1 ? L[1] : L[0];
-        row_lse[(int64_t)bh * N + qi] = (Lr > 0.f) ? Rr + fta_log2(Lr) : -FTA_INF;
+        const float Rr = own1 ? R[1] : R[0];
+        row_lse[(int64_t)bh * N + qi] = (L > 0.f) ? Rr + fta_log2(L) : -FTA_INF;
         if constexpr (STREAM) {
             float bnd = sG[0][tid].y;
 #pragma unroll
