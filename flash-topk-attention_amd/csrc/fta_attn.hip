@@ -444,8 +444,8 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
             qf[ks] = (ok && d < a.Dreal) ? *reinterpret_cast<const uint4*>(qp + (int64_t)t * a.q_sn + d) : fta_zero4();
         }
     }
-    // complete the register loads: the DMAs below are invisible to the compiler
-    fta_wait_vmcnt<0>();
+    // the Q loads stay in flight while the masks are built (their wait is before the
+    // first DMA below: the DMAs are invisible to the compiler's wait counting)
 
     f32x16 oacc[DT32];
 #pragma unroll
@@ -503,6 +503,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
             }
         };
 
+        fta_wait_vmcnt<0>();  // register loads complete before the DMA stream
 #pragma unroll
         for (int k = 0; k < NST - 1; ++k)
             if (k < iters) issue(k, k);
@@ -867,8 +868,8 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
         dl = a.delta_in[(int64_t)bh * a.N + tq];
     }
     const bool rowlive = lse2 != -FTA_INF;
-    // complete the register loads: the DMAs below are invisible to the compiler
-    fta_wait_vmcnt<0>();
+    // the Q / dO loads stay in flight while the masks are built (their wait is before
+    // the first DMA below: the DMAs are invisible to the compiler's wait counting)
 
     f32x16 acc[DT32];
 #pragma unroll
@@ -924,6 +925,7 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
             }
         };
 
+        fta_wait_vmcnt<0>();  // register loads complete before the DMA stream
 #pragma unroll
         for (int k = 0; k < NST - 1; ++k)
             if (k < iters) issue(k, k);
