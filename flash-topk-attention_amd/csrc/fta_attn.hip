@@ -30,7 +30,7 @@ namespace fta {
 int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint32_t* sel, hipStream_t st);
 int launch_kv_order(const uint32_t* sel, int B, int H, int Hk, int M, int QW, int32_t* order, int32_t* head_work,
                     int32_t* head_perm, hipStream_t st);
-int launch_head_order_merged(const int32_t* merged, int BH, int QM, int W, int M, int32_t* head_work,
+int launch_head_order_merged(const int32_t* merged, int BH, int QM, int W, int M, int qpg, int32_t* head_work,
                              int32_t* head_perm, hipStream_t st);
 }  // namespace fta
 
@@ -1994,7 +1994,7 @@ int fta_sparse_attn_fwd_gqa(const void* q, const int64_t* q_strides, const void*
     if (workspace != nullptr && workspace_bytes >= fwd_bytes(B, H)) {
         int32_t* head_work = (int32_t*)workspace;
         int32_t* head_perm = head_work + B * H;
-        if ((rc = fta::launch_head_order_merged(merged_indices, B * H, QM, W, G.Mkv, head_work, head_perm, st)) !=
+        if ((rc = fta::launch_head_order_merged(merged_indices, B * H, QM, W, G.Mkv, max(1, 256 / q_block_size), head_work, head_perm, st)) !=
             FTA_OK)
             return rc;
         a.head_perm = head_perm;

@@ -534,6 +534,41 @@ __global__ __launch_bounds__(256) void fta_head_balance_kernel(int32_t* __restri
 // part[bh][j]; fta_head_balance_kernel adds the parts.  (Counting every fourth
 // row only placed the C3 heads 5% worse.)
 constexpr int kHeadParts = 64;
+// Union-based work of each (b, h) for the forward placement: WG (bh, j) takes
+// the forward's workgroup groups of qpg consecutive q-blocks j, j + kHeadParts,
+// ...; a group costs the size of the union of its lists (the chunks its
+// workgroup walks) plus `setup` chunk-steps.  M <= 4096.
+__global__ __launch_bounds__(256) void fta_head_work_union_kernel(const int32_t* __restrict__ merged, int QM, int W,
+                                                                  int M, int qpg, int setup,
+                                                                  int32_t* __restrict__ part) {
+    __shared__ uint32_t bits[128];
+    __shared__ int s_u;
+    const int tid = threadIdx.x;
+    const int bh = blockIdx.x / kHeadParts, j = blockIdx.x % kHeadParts;
+    const int ngroups = (QM + qpg - 1) / qpg;
+    int work = 0;
+    for (int gi = j; gi < ngroups; gi += kHeadParts) {
+        if (tid < 128) bits[tid] = 0u;
+        if (tid == 0) s_u = 0;
+        __syncthreads();
+        const int q0 = gi * qpg, q1 = min(QM, q0 + qpg);
+        const int32_t* rows = merged + ((int64_t)bh * QM + q0) * W;
+        const int n = (q1 - q0) * W;
+        for (int e = tid; e < n; e += 256) {
+            const int m = rows[e];
+            if (m >= 0 && m < M) atomicOr(&bits[m >> 5], 1u << (m & 31));
+        }
+        __syncthreads();
+        int c = (tid < 128) ? __popc(bits[tid]) : 0;
+        for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+        if ((tid & 63) == 0 && c) atomicAdd(&s_u, c);
+        __syncthreads();
+        work += s_u + setup;
+        __syncthreads();
+    }
+    if (tid == 0) part[blockIdx.x] = work;
+}
+
 __global__ __launch_bounds__(256) void fta_head_work_merged_kernel(const int32_t* __restrict__ merged, int QM, int W,
                                                                    int M, int32_t* __restrict__ part) {
     __shared__ int s_work;
@@ -691,14 +726,23 @@ int launch_kv_order(const uint32_t* sel, int B, int H, int Hk, int M, int QW, in
     return check_launch("fta_head_balance_kernel");
 }
 
-int launch_head_order_merged(const int32_t* merged, int BH, int QM, int W, int M, int32_t* head_work,
+int launch_head_order_merged(const int32_t* merged, int BH, int QM, int W, int M, int qpg, int32_t* head_work,
                              int32_t* head_perm, hipStream_t st) {
     if (BH <= 0) return FTA_OK;
     // part sums after head_work and head_perm: [BH][kHeadParts]
     int32_t* part = head_perm + BH;
+    int rc;
+    if (M <= 4096) {
+        hipLaunchKernelGGL(fta_head_work_union_kernel, dim3((unsigned)(BH * kHeadParts)), dim3(256), 0, st, merged,
+                           QM, W, M, qpg, 3, part);
+        if ((rc = check_launch("fta_head_work_union_kernel")) != FTA_OK) return rc;
+        hipLaunchKernelGGL(fta_head_balance_kernel, dim3(1), dim3(256), 0, st, head_work, part, kHeadParts, 0, 1, BH,
+                           head_perm);
+        return check_launch("fta_head_balance_kernel");
+    }
     hipLaunchKernelGGL(fta_head_work_merged_kernel, dim3((unsigned)(BH * kHeadParts)), dim3(256), 0, st, merged, QM,
                        W, M, part);
-    int rc = check_launch("fta_head_work_merged_kernel");
+    rc = check_launch("fta_head_work_merged_kernel");
     if (rc != FTA_OK) return rc;
     hipLaunchKernelGGL(fta_head_balance_kernel, dim3(1), dim3(256), 0, st, head_work, part, kHeadParts, QM / 4, 1, BH,
                        head_perm);
