@@ -534,10 +534,10 @@ __global__ __launch_bounds__(256) void fta_head_balance_kernel(int32_t* __restri
 // part[bh][j]; fta_head_balance_kernel adds the parts.  (Counting every fourth
 // row only placed the C3 heads 5% worse.)
 constexpr int kHeadParts = 64;
-// Union-based work of each (b, h) for the forward placement: WG (bh, j) takes
-// the forward's workgroup groups of qpg consecutive q-blocks j, j + kHeadParts,
-// ...; a group costs the size of the union of its lists (the chunks its
-// workgroup walks) plus `setup` chunk-steps.  M <= 4096.
+// Union-based work of each (b, h) for the forward placement.  Group gi holds the
+// qpg consecutive q-blocks of one forward workgroup; WG (bh, j) takes groups j,
+// j + kHeadParts, ...  A group costs the size of the union of its q-blocks'
+// lists (the chunks its workgroup walks) plus `setup` chunk-steps.  M <= 4096.
 __global__ __launch_bounds__(256) void fta_head_work_union_kernel(const int32_t* __restrict__ merged, int QM, int W,
                                                                   int M, int qpg, int setup,
                                                                   int32_t* __restrict__ part) {
