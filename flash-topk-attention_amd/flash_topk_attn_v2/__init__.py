@@ -136,24 +136,31 @@ def build_qblock_topk_indices(
     if indices_int.device.type != "cuda":
         raise ValueError("flash_qblock_merge requires CUDA tensors")
 
+    merged_indices = torch.empty(B, H, QM, qblock_topk, device=device, dtype=torch.int32)
+    merged_scores = torch.empty(B, H, QM, qblock_topk, device=device, dtype=torch.float32)
+    bound = getattr(topk_indices, "_fta_id_bound", None)
+    if bound is not None and bound[0] <= 4096 and bound[1] == topk_indices._version:
+        # produced by flash_topk_score with M <= 4096 blocks: every id is below M,
+        # so num_score_blocks = M keeps exactly the ids that max id + 1 keeps, and
+        # neither the device max nor a host wait is needed
+        rc = _lib.lib().fta_qblock_merge(
+            _lib.ptr(indices_int), _lib.ptr(scores_float), B * H * QM, q_block_size, topk_width,
+            int(bound[0]), qblock_topk, _lib.ptr(merged_indices), _lib.ptr(merged_scores), _lib.ptr(counts),
+            _lib.stream_ptr(device),
+        )
+        _lib.check(rc, "flash_qblock_merge")
+        return merged_indices, counts, merged_indices.shape[-1]
     # num_score_blocks = max id + 1, as in the reference (:101-105).  The max is
     # taken on the device and read by the merge kernel, and the host reads it
     # (to report ids past the 4096-block limit) only after the merge is queued,
     # so the GPU does not idle through the host round trip.
     max_id = indices_int.max().reshape(1)
-    merged_indices = torch.empty(B, H, QM, qblock_topk, device=device, dtype=torch.int32)
-    merged_scores = torch.empty(B, H, QM, qblock_topk, device=device, dtype=torch.float32)
     rc = _lib.lib().fta_qblock_merge_maxid(
         _lib.ptr(indices_int), _lib.ptr(scores_float), B * H * QM, q_block_size, topk_width,
         _lib.ptr(max_id), qblock_topk, _lib.ptr(merged_indices), _lib.ptr(merged_scores), _lib.ptr(counts),
         _lib.stream_ptr(device),
     )
     _lib.check(rc, "flash_qblock_merge")
-    bound = getattr(topk_indices, "_fta_id_bound", None)
-    if bound is not None and bound[0] <= 4096 and bound[1] == topk_indices._version:
-        # produced by flash_topk_score with M <= 4096 blocks: no id can exceed the
-        # limit, so the host does not wait for the max (the step stays asynchronous)
-        return merged_indices, counts, merged_indices.shape[-1]
     num_score_blocks = int(max_id.item()) + 1
     if num_score_blocks > 4096:
         raise NotImplementedError(
