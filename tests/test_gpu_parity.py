@@ -87,6 +87,37 @@ def test_topk_select_bit_exact_and_fused(case, thr, topk):
     np.testing.assert_array_equal(fa.cpu().numpy(), ra)
 
 
+# Short sequences through the pipelined scoring kernel (b = 64, D 64 / 128): 1 to 9
+# blocks cover the peeled first block, the 4-block unrolled loop, its remainder and
+# the last block, with and without partial edge blocks.
+SHORT_CASES = [
+    (1, 64, 2, 128, 64, (0, 0), torch.bfloat16, "bnc"),    # M = 1
+    (1, 100, 2, 64, 64, (10, 18), torch.bfloat16, "bnc"),  # M = 2, both blocks partial
+    (1, 150, 1, 128, 64, (0, 42), torch.float16, "bnc"),   # M = 3
+    (1, 320, 2, 64, 64, (0, 0), torch.bfloat16, "bnc"),    # M = 5: one unrolled pass
+    (1, 560, 2, 128, 64, (30, 50), torch.bfloat16, "bnc"), # M = 10, partial edges
+    (1, 576, 1, 64, 64, (0, 0), torch.float16, "bnc"),     # M = 9: unrolled twice, no remainder
+]
+
+
+@pytest.mark.parametrize("case", SHORT_CASES, ids=lambda c: f"N{c[1]}D{c[3]}p{c[5]}")
+def test_score_short_sequences(case):
+    B, N, H, D, b, pad, dt, layout = case
+    say(f"[short score] {case}")
+    q, k = _qk(case, 30)
+    got = fta.flash_block_score(q, k, H, b, pad)
+    fi, fr, fa = fta.flash_topk_score(q, k, H, b, 4, pad, 0.9)
+    torch.cuda.synchronize()
+    qn, kn = _oracle_inputs(q, k)
+    ref = O.block_score(qn, kn, H, b, pad)
+    g = got.cpu().numpy()
+    np.testing.assert_allclose(g, ref, rtol=2e-4, atol=2e-7)
+    ri, rr, ra = O.topk_select(g, 0.9, 4, b, pad)
+    np.testing.assert_array_equal(fi.cpu().numpy(), ri)
+    np.testing.assert_array_equal(fr.cpu().numpy(), rr)
+    np.testing.assert_array_equal(fa.cpu().numpy(), ra)
+
+
 WIDE_K_CASES = [
     # B, N, H, D, b, padding, dtype, layout, thr, topk: register lists of 32 and 64 entries
     (1, 2048, 2, 64, 32, (0, 0), torch.bfloat16, "bnc", 1.0, 32),
