@@ -7,8 +7,9 @@ Prints one JSON line (driver contract).  Extra fields: the scoring kernel's
 roofline (HIP events on the stream it runs on), `stage_roofline` (every stage
 launched alone through its C entry point and timed with HIP events, with its
 MFMA or HBM fraction of peak), `configs` (the same per-stage figures for the
-C3-iid variant and configs C2, C4 and C5), the V1 rows and a CPU baseline (the
-numpy oracle on a bounded sample, host cores).
+C3-iid variant and configs C2, C4 and C5), the V1 rows, the reference's
+published V2 shapes, and a CPU baseline (a PyTorch-CPU fp32 restatement of the
+reference's path on two of the 32 heads, host cores).
 """
 
 from __future__ import annotations
@@ -67,40 +68,33 @@ def make_inputs(B, N, H, D, peaked, seed, dev, dtype=None, scale=1.0):
     return tuple(x.to(dtype).to(dev) for x in (q, k, v))
 
 
-def cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, rows, heads):
-    """Numpy oracle (oracle/fta_oracle.py) on heads 0 .. heads-1, first `rows` queries of each."""
-    import numpy as np
+def cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, heads):
+    """The reference algorithm's PyTorch path, restated in fp32 torch ops on the
+    CPU (oracle/fta_torch_cpu.py), on heads 0 .. heads-1 of the workload at the
+    full sequence length: score -> top-k -> merge -> sparse attention forward
+    and autograd backward.  Work is counted as for the GPU value (2 N^2 D for
+    the scores, 4 D P forward, 10 D P backward)."""
+    import torch
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import fta_oracle as O
+    import fta_torch_cpu as T
 
     N = q.shape[1]
     secs, flops = 0.0, 0.0
     for h in range(heads):
-        f = lambda t: t[:, :, h * D:(h + 1) * D].float().cpu().numpy()
-        qn, kn, vn, dn = f(q), f(k), f(v), f(do)
+        f = lambda t: t[0, :, h * D:(h + 1) * D].float().cpu().contiguous()
+        qh, kh, vh, dh = f(q), f(k), f(v), f(do)
         t0 = time.perf_counter()
-        sc = O.block_score(qn, kn, 1, b, rows=np.arange(rows))
-        idx, raw, avg = O.topk_select(sc.astype(np.float32), thr, topk, b)
-        merged, counts, _ = O.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
-        qbl = [(0, 0, qm) for qm in range(rows // g)]
-        full = np.full((1, 1, N // g, W), -1, dtype=np.int32)
-        full[:, :, : rows // g] = merged
-        O.sparse_attn(qn, kn, vn, full, 1, g, b, None, qblocks=qbl)
-        O.sparse_attn_bwd(qn, kn, vn, dn, full, 1, g, b, None, qblocks=qbl)
+        merged, counts, *_ = T.pipeline_head(qh, kh, vh, dh, b, topk, thr, g, W)
         secs += time.perf_counter() - t0
         P = g * b * int(counts.sum())
-        flops += 2.0 * rows * N * D + 14.0 * D * P
-    try:  # threads of numpy's BLAS pool (the only multi-threaded part of the oracle)
-        import threadpoolctl
-
-        cores = max(int(i.get("num_threads", 1)) for i in threadpoolctl.threadpool_info()) or 1
-    except Exception:
-        cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "seconds": secs,
-            "sample": f"numpy oracle, {heads} head(s) x {rows} queries of the C3 workload "
-                      f"(score+select+merge+fwd+bwd), float64 BLAS"}
+        flops += 2.0 * N * N * D + 14.0 * D * P
+    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "host_cpus": os.cpu_count(), "kind": "port", "seconds": round(secs, 3),
+            "full_config_seconds_extrapolated": round(secs * H / heads, 2),
+            "sample": f"PyTorch-CPU fp32 restatement of the reference's path (oracle/fta_torch_cpu.py), "
+                      f"{heads} of {H} heads at N={N} of the C3 workload (score+select+merge+fwd+bwd); "
+                      f"full_config_seconds_extrapolated = seconds x {H}/{heads}"}
 
 
 # V1 fused scoring rows of the reference's BENCHMARK.md (other hardware; D not
@@ -158,6 +152,72 @@ def bench_v1(dev, stream):
     return res
 
 
+# Rows of the reference's V2_BENCHMARK.md (RTX 4090, bf16, q_block_size =
+# score_block_size, threshold 1.0, qblock_topk = q_block_size * K): (B, N, H, D,
+# b, K, published V2 scoring ms, sparse attention ms, end-to-end ms, lines)
+V2_ROWS = [
+    (1, 4096, 32, 128, 64, 16, 2.67, 4.44, 7.26, "12,31,62"),
+    (1, 8192, 32, 128, 64, 16, 10.56, 17.37, 28.15, "13,32,63"),
+    (1, 4096, 32, 128, 128, 16, 2.42, 4.48, None, "14,33"),
+    (1, 4096, 32, 128, 64, 32, 2.69, 4.53, 7.37, "15,34,64"),
+    (2, 4096, 32, 128, 64, 16, 5.28, 8.95, 14.42, "16,35,65"),
+]
+
+
+def bench_v2_rows(dev, stream):
+    """The reference's published V2 shapes: flash_topk_score (scoring + top-k),
+    flash_topk_attn forward given the merged indices, and the end-to-end
+    forward pipeline (score + merge + attention), HIP events, median of 5."""
+    import torch
+
+    import flash_topk_attn_v2 as fta
+
+    res = []
+    for B, N, H, D, b, K, r_sc, r_at, r_e2e, lines in V2_ROWS:
+        q, k, v = make_inputs(B, N, H, D, False, 11, dev)
+        # q_block_size = score_block_size as the reference's table states; its
+        # flash_sparse_attn accepts q blocks of at most 64 (sparse_attn.py:279),
+        # so the 128-token row uses 64
+        g = min(b, 64)
+        W = g * K
+
+        def score():
+            return fta.flash_topk_score(q, k, H, b, K, (0, 0), 1.0)
+
+        idx, raw, avg = score()
+        merged, counts, _ = fta.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
+
+        def attn():
+            return fta.flash_topk_attn(q, k, v, merged, counts, H, g, b)
+
+        def e2e():
+            i, _, a = score()
+            m, c, _ = fta.build_qblock_topk_indices(i, g, (0, 0), a, W)
+            return fta.flash_topk_attn(q, k, v, m, c, H, g, b)
+
+        row = {"config": f"B{B} N{N} H{H} D{D} b{b} K{K} g{g} bf16", "reference_source": f"V2_BENCHMARK.md:{lines}"}
+        P = float(g * b * counts.sum().item())  # valid (query, key) pairs of the merged lists
+        f = {"score": 2.0 * B * H * N * N * D, "attn_fwd": 4.0 * D * P}
+        f["end_to_end"] = f["score"] + f["attn_fwd"]
+        for name, fn, ref in (("score", score, r_sc), ("attn_fwd", attn, r_at), ("end_to_end", e2e, r_e2e)):
+            ts = []
+            with torch.no_grad():
+                fn()
+                for _ in range(5):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    fn()
+                    e1.record(stream)
+                    torch.cuda.synchronize()
+                    ts.append(e0.elapsed_time(e1))
+            row[f"{name}_ms"] = round(sorted(ts)[2], 4)
+            row[f"{name}_tflops"] = round(f[name] / sorted(ts)[2] / 1e9, 1)
+            row[f"{name}_reference_ms_rtx4090"] = ref
+        res.append(row)
+        del q, k, v, idx, raw, avg, merged, counts
+    return res
+
+
 class Pipeline:
     """One configuration's inputs, indices and stage launchers (C ABI calls on
     the current stream), for per-stage HIP-event timing."""
@@ -197,6 +257,9 @@ class Pipeline:
         self.ws_bwd = _lib.workspace(L.fta_sparse_attn_bwd_workspace_size(*geo), dev)
         self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
         self.streams_ok = b == 64 and D in (64, 128) and m_out <= 16
+        shp = (B, H, N, m_out)
+        self.sel_out = (torch.empty(shp, dtype=torch.int32, device=dev), torch.empty(shp, device=dev),
+                        torch.empty(shp, device=dev))
 
     # --- stage launchers
     def score(self):
@@ -209,6 +272,15 @@ class Pipeline:
                                          self.topk, self.ws_score.data_ptr(), self.ws_score.numel(),
                                          self.stream.cuda_stream)
         _lib.check(rc, "fta_topk_score_candidates")
+
+    def select_streams(self):
+        """The stream selector alone, over the streams the last scorer() call left."""
+        L, _lib = self.L, self._lib
+        rc = L.fta_topk_select_candidates(self.B, self.H, self.N, self.D, self.st, self.b, self.pad[0], self.pad[1],
+                                          self.topk, self.thr, self.sel_out[0].data_ptr(),
+                                          self.sel_out[1].data_ptr(), self.sel_out[2].data_ptr(),
+                                          self.ws_score.data_ptr(), self.ws_score.numel(), self.stream.cuda_stream)
+        _lib.check(rc, "fta_topk_select_candidates")
 
     def merge(self):
         self.fta.build_qblock_topk_indices(self.idx, self.g, self.qpad, self.avg, self.W)
@@ -288,13 +360,13 @@ class Pipeline:
         r["score"] = {"ms": t_score, "tflops": f_score / t_score / 1e9}
         if self.streams_ok:
             t_k = self.time(self.scorer, reps)
-            sel_ms = max(t_score - t_k, 1e-6)
+            sel_ms = self.time(self.select_streams, reps)
             r["score_kernel"] = {"ms": t_k, "bound": "mfma", "tflops": f_score / t_k / 1e9,
                                  "frac": f_score / t_k / 1e9 / PEAK_BF16_TFLOPS}
             sb = self.selector_bytes()
             r["topk_select"] = {"ms": sel_ms, "bound": "hbm", "gbs": sb / sel_ms / 1e6,
                                 "frac": sb / sel_ms / 1e6 / PEAK_HBM_GBS, "bytes": sb,
-                                "note": "score stage minus the scoring kernel alone"}
+                                "note": "fta_topk_select_candidates alone over the scorer's streams"}
         K = self.idx.shape[-1]
         mb = 2.0 * B * H * N * K * 4 + B * H * self.QM * (self.merged.shape[3] + 1) * 4
         t = self.time(self.merge, reps)
@@ -330,7 +402,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the C3-iid, C2, C4, C5 and V1 rows")
-    ap.add_argument("--cpu-rows", type=int, default=32768)
     ap.add_argument("--cpu-heads", type=int, default=2)
     ap.add_argument("--only", choices=["score", "scorer", "topk", "merge", "fwd", "bwd", "dq", "dkv", "copy", "v1"],
                     default=None, help="profiling aid: run one stage of the C3 step --steps times and exit")
@@ -362,10 +433,12 @@ def main():
         else:
             pl = Pipeline(dev, B, N, H, D, b, topk, thr, g, W, peaked=True, seed=2)
         big = torch.empty(256 << 20, device=dev, dtype=torch.uint8)
-        fn = {"score": pl.score, "scorer": pl.scorer, "topk": pl.score, "merge": pl.merge, "fwd": pl.fwd,
+        fn = {"score": pl.score, "scorer": pl.scorer, "topk": pl.select_streams, "merge": pl.merge, "fwd": pl.fwd,
               "dq": pl.dq_stage, "dkv": pl.dkv_stage,
               "bwd": lambda: (pl.delta_stage(), pl.dq_stage(), pl.dkv_stage()),
               "copy": lambda: big[: 128 << 20].copy_(big[128 << 20:])}[args.only]
+        if args.only == "topk":
+            pl.scorer()  # the streams the selector reads
         for _ in range(args.steps):
             fn()
         torch.cuda.synchronize()
@@ -479,9 +552,10 @@ def main():
         torch.cuda.empty_cache()
         out["configs"] = extra
         out["v1_score"] = bench_v1(dev, stream)
+        out["v2_reference_rows"] = bench_v2_rows(dev, stream)
 
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, args.cpu_rows, args.cpu_heads)
+        out["cpu_baseline"] = cpu_baseline(q, k, v, do, H, D, b, topk, thr, g, W, args.cpu_heads)
 
     print(json.dumps(out), flush=True)
 

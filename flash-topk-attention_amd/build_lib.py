@@ -31,6 +31,7 @@ COMMON = [
     f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", CSRC,
+    "-I", os.path.join(os.path.dirname(HERE), "include"),
 ]
 
 

@@ -212,11 +212,6 @@ __device__ __forceinline__ void fta_wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Status codes returned by every extern "C" entry point (see include/fta.h).
-#define FTA_OK 0
-#define FTA_ERR_ARG 1
-#define FTA_ERR_UNSUPPORTED 2
-#define FTA_ERR_HIP 3
-
-// Size of the device array behind fta_sparse_attn_bwd_noalloc (include/fta.h).
-#define FTA_NOALLOC_SCRATCH_BYTES (64u << 20)
+// Status codes (FTA_OK / FTA_ERR_*) and FTA_NOALLOC_SCRATCH_BYTES come from the
+// public header, so the library and its callers share one definition.
+#include "fta.h"

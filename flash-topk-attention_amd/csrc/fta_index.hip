@@ -429,7 +429,9 @@ __global__ __launch_bounds__(256) void fta_kv_order_kernel(const uint32_t* __res
                                                            int G, int32_t* __restrict__ order,
                                                            int32_t* __restrict__ head_work) {
     // WG (b, K/V head, slice): counts every block's selections (coalesced reads
-    // of the bitmap rows, LDS atomics), then ranks the blocks of its slice of 256
+    // of the bitmap rows, LDS atomics), then ranks the blocks of its slice of
+    // 1024 (four per thread).  Each slice reads the head's whole bitmap, so up to
+    // 1024 blocks one WG per head reads it once.
     __shared__ uint32_t key[4096];
     __shared__ int s_work;
     const int64_t rk = blockIdx.x;               // (b, K/V head)
@@ -455,15 +457,18 @@ __global__ __launch_bounds__(256) void fta_kv_order_kernel(const uint32_t* __res
     atomicAdd(&s_work, cw);
     __syncthreads();
     if (slice == 0 && threadIdx.x == 0) head_work[rk] = s_work;
-    const int i = slice * 256 + threadIdx.x;
-    if (i < M) {
-        const uint32_t ki = key[i];
-        int rank = 0;
-        for (int j = 0; j < M; ++j) {
-            const uint32_t kj = key[j];
-            rank += (kj < ki) || (kj == ki && j < i);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = slice * 1024 + u * 256 + threadIdx.x;
+        if (i < M) {
+            const uint32_t ki = key[i];
+            int rank = 0;
+            for (int j = 0; j < M; ++j) {
+                const uint32_t kj = key[j];
+                rank += (kj < ki) || (kj == ki && j < i);
+            }
+            order[rk * M + rank] = i;
         }
-        order[rk * M + rank] = i;
     }
 }
 
@@ -717,7 +722,7 @@ int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint3
 int launch_kv_order(const uint32_t* sel, int B, int H, int Hk, int M, int QW, int32_t* order, int32_t* head_work,
                     int32_t* head_perm, hipStream_t st) {
     if (M <= 0 || B * Hk == 0) return FTA_OK;
-    hipLaunchKernelGGL(fta_kv_order_kernel, dim3((unsigned)(B * Hk), (unsigned)((M + 255) / 256)), dim3(256), 0, st,
+    hipLaunchKernelGGL(fta_kv_order_kernel, dim3((unsigned)(B * Hk), (unsigned)((M + 1023) / 1024)), dim3(256), 0, st,
                        sel, M, QW, H, H / Hk, order, head_work);
     int rc = check_launch("fta_kv_order_kernel");
     if (rc != FTA_OK) return rc;

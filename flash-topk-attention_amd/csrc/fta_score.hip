@@ -1696,6 +1696,23 @@ StreamBufs stream_layout(void* workspace, int B, int H, int N, int M, int m_out,
     return sb;
 }
 
+// The selector over the candidate streams of stream_layout (fta_topk_stream_kernel).
+int launch_stream_select(const StreamBufs& sb, const float* row_lse, int B, int H, int N, int M, int m_out, int bsz,
+                         int pad_head, int pad_tail, float threshold, int32_t* idx, float* raw, float* avg,
+                         hipStream_t s) {
+    const int qtiles = (N + 255) / 256;
+#define FTA_LAUNCH_STREAM(KB)                                                                                     \
+    hipLaunchKernelGGL(fta_topk_stream_kernel<KB>, dim3((unsigned)(B * H * qtiles)), dim3(256), 0, s, sb.cand, \
+                       sb.count, sb.tau_key, row_lse, N, qtiles, M, m_out, bsz, pad_head, pad_tail, threshold, idx, \
+                       raw, avg)
+    if (m_out <= 8)
+        FTA_LAUNCH_STREAM(8);
+    else
+        FTA_LAUNCH_STREAM(16);
+#undef FTA_LAUNCH_STREAM
+    return fta::check_launch("fta_topk_stream_kernel");
+}
+
 // Shared checks of fta_topk_score and fta_topk_score_candidates; sets M and m_out.
 int topk_score_checks(int B, int H, int N, int D, int bsz, int pad_head, int pad_tail, int max_topk,
                       size_t workspace_bytes, int* M, int* m_out) {
@@ -1729,6 +1746,24 @@ int fta_topk_score_candidates(const void* q, const void* k, int dtype, int B, in
     FTA_TRY_END
 }
 
+int fta_topk_select_candidates(int B, int H, int N, int D, const int64_t* k_strides, int score_block_size,
+                               int pad_head, int pad_tail, int max_topk, float threshold, int32_t* topk_indices,
+                               float* topk_raw, float* topk_avg, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+    FTA_TRY_BEGIN
+    int M = 0, m_out = 0;
+    int st = topk_score_checks(B, H, N, D, score_block_size, pad_head, pad_tail, max_topk, workspace_bytes, &M, &m_out);
+    if (st != FTA_OK) return st;
+    if (!(m_out <= kStreamMaxTopk && score_pipe_ok(score_block_size, fta::kernel_head_dim(D), k_strides)))
+        return fta::unsupported("topk_select_candidates: needs b = 64, D <= 128 and at most 16 blocks per query");
+    if (!topk_indices || !topk_raw || !topk_avg) return fta::arg_error("topk_select_candidates: null pointer");
+    float* row_lse = nullptr;
+    const StreamBufs sb = stream_layout(workspace, B, H, N, M, m_out, &row_lse);
+    return launch_stream_select(sb, row_lse, B, H, N, M, m_out, score_block_size, pad_head, pad_tail, threshold,
+                                topk_indices, topk_raw, topk_avg, (hipStream_t)stream);
+    FTA_TRY_END
+}
+
 int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N, int D, const int64_t* q_strides,
                    const int64_t* k_strides, int score_block_size, int pad_head, int pad_tail, float scale,
                    int max_topk, float threshold, int32_t* topk_indices, float* topk_raw, float* topk_avg,
@@ -1745,17 +1780,8 @@ int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N,
         st = launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, pad_tail,
                               scale, nullptr, row_lse, 0, nullptr, s, sb);
         if (st != FTA_OK) return st;
-        const int qtiles = (N + 255) / 256;
-#define FTA_LAUNCH_STREAM(KB)                                                                                     \
-    hipLaunchKernelGGL(fta_topk_stream_kernel<KB>, dim3((unsigned)(B * H * qtiles)), dim3(256), 0, s, sb.cand, \
-                       sb.count, sb.tau_key, row_lse, N, qtiles, M, m_out, score_block_size, pad_head, pad_tail,  \
-                       threshold, topk_indices, topk_raw, topk_avg)
-        if (m_out <= 8)
-            FTA_LAUNCH_STREAM(8);
-        else
-            FTA_LAUNCH_STREAM(16);
-#undef FTA_LAUNCH_STREAM
-        return fta::check_launch("fta_topk_stream_kernel");
+        return launch_stream_select(sb, row_lse, B, H, N, M, m_out, score_block_size, pad_head, pad_tail, threshold,
+                                    topk_indices, topk_raw, topk_avg, s);
     }
     float* blk_lse = (float*)workspace;
     float* row_lse = (float*)((char*)workspace + fta::align_up((size_t)B * H * M * N * sizeof(float)));

@@ -73,7 +73,10 @@ def flash_topk_score(
     )
     _lib.check(rc, "flash_topk_score")
     # every id is < M <= 4096: build_qblock_topk_indices need not read the max back
-    # (recorded with the tensor's version counter, so an in-place change voids it)
+    # (recorded with the tensor's version counter, so an in-place change through a
+    # torch op voids it; writes that bypass the version counter -- through
+    # ``.data``, numpy or DLPack views -- are not seen, and ids >= M written that
+    # way would be dropped by the merge instead of raising as the reference does)
     idx._fta_id_bound = (M, idx._version)
     return idx, raw, avg
 

@@ -74,6 +74,25 @@ class _SparseAttnGQAFunc(torch.autograd.Function):
         return dq, dk, dv, None, None, None, None, None, None, None, None
 
 
+def _apply_counts(merged: torch.Tensor, counts: torch.Tensor) -> torch.Tensor:
+    """The list each q-block of the reference's kernel walks, with -1 after it.
+
+    The reference (csrc/sparse_attn_kernel.cu:57-86) sorts rows of at most 512
+    slots ascending with -1 mapped to INT_MAX and walks the first ``count``
+    sorted ids; wider rows are walked unsorted for ``count`` slots.  Positions
+    at or past ``count`` become -1 here; the kernels skip -1 entries, and a
+    row with ``count <= 0`` has no entries (o = 0, lse = -inf).
+    """
+    W = merged.shape[-1]
+    cnt = counts.to(device=merged.device, dtype=torch.int64).reshape(*merged.shape[:-1], 1)
+    if W <= 512:
+        key = torch.where(merged >= 0, merged, torch.full_like(merged, torch.iinfo(torch.int32).max))
+        merged = torch.sort(key, dim=-1).values
+        merged = torch.where(merged == torch.iinfo(torch.int32).max, torch.full_like(merged, -1), merged)
+    pos = torch.arange(W, device=merged.device, dtype=torch.int64)
+    return torch.where(pos < cnt, merged, torch.full_like(merged, -1)).contiguous()
+
+
 class FlashSparseAttnFunc(torch.autograd.Function):
     """Autograd function with the reference's call contract
     (flash_topk_attn_v2/sparse_attn.py:130-224):
@@ -88,15 +107,20 @@ class FlashSparseAttnFunc(torch.autograd.Function):
     reference's lse (sparse_attn.py:391).  The virtual tail paddings follow
     from the shapes, as in the reference's kernels: q tail =
     QM * q_block_size - q_pad_head - N_real, kv tail = num_kv_blocks *
-    kv_block_size - kv_pad_head - N_real.  ``counts`` and ``qblock_topk`` are
-    implied by ``merged_indices`` (-1 entries are skipped).  Gradients are
-    ``[B, N_phys, C]`` with zero rows past ``N_real``.
+    kv_block_size - kv_pad_head - N_real.  ``counts`` selects the blocks a
+    q-block attends to as the reference's kernel does
+    (csrc/sparse_attn_kernel.cu:39-86, :201): rows of at most 512 slots keep
+    the ``counts`` smallest valid ids (the row sorted ascending, -1 entries
+    last), wider rows their first ``counts`` slots; ``counts <= 0`` gives
+    o = 0 and lse = -inf.  Counts that equal the number of valid entries (what
+    ``build_qblock_topk_indices`` returns) keep every listed block.
+    Gradients are ``[B, N_phys, C]`` with zero rows past ``N_real``.
     """
 
     @staticmethod
     def forward(ctx, q, k, v, merged_indices, counts, num_heads, q_block_size, kv_block_size, qblock_topk,
                 softmax_scale, q_pad_head, kv_pad_head, N_real, num_kv_blocks):
-        del counts, qblock_topk
+        del qblock_topk
         B, N_phys, C = q.shape
         N = int(N_real)
         if N <= 0 or N > N_phys:
@@ -106,7 +130,7 @@ class FlashSparseAttnFunc(torch.autograd.Function):
         kv_padding = (int(kv_pad_head), int(num_kv_blocks) * kv_block_size - int(kv_pad_head) - N)
         if q_padding[1] < 0 or kv_padding[1] < 0:
             raise ValueError("merged_indices / num_kv_blocks do not cover N_real with the given head paddings")
-        merged = merged_indices.to(torch.int32).contiguous()
+        merged = _apply_counts(merged_indices.to(torch.int32), counts)
         qs, ks, vs = q[:, :N], k[:, :N], v[:, :N]
         o, lse = _sparse_attn_fwd(qs, ks, vs, merged, num_heads, q_block_size, kv_block_size,
                                   float(softmax_scale), q_padding, kv_padding, num_heads)

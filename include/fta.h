@@ -125,6 +125,21 @@ int fta_topk_score_candidates(const void* q, const void* k, int dtype, int B, in
                               int score_block_size, int pad_head, int pad_tail, float scale,
                               int max_topk, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Stage 2 of fta_topk_score alone: the top-k selection (with the threshold
+ * cut) over the candidate streams that fta_topk_score_candidates left in
+ * `workspace` for the same geometry and max_topk.  k_strides and D only decide
+ * (as in fta_topk_score) whether the stream path applies; FTA_ERR_UNSUPPORTED
+ * otherwise.  fta_topk_score_candidates followed by this call gives the same
+ * outputs as fta_topk_score.  Stands for the reference's top-k stage
+ * (topk_select_launch, flash_topk_attn_v2/csrc/topk_select.cpp, as called from
+ * flash_topk_attn_v2/topk_select.py:185-311).
+ */
+int fta_topk_select_candidates(int B, int H, int N, int D, const int64_t* k_strides, int score_block_size,
+                               int pad_head, int pad_tail, int max_topk, float threshold,
+                               int32_t* topk_indices, float* topk_raw, float* topk_avg, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- indices */
 
 /*
@@ -327,7 +342,10 @@ int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void*
  * the scratch (membership bitmap + lse in log2 units, the size that
  * fta_sparse_attn_bwd_workspace_size reports) lives in a device array of
  * FTA_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the
- * process ends.  A problem needing more returns FTA_ERR_UNSUPPORTED.  The call
+ * process ends.  The array belongs to the library's code object: every process
+ * that loads the library reserves it on each GPU where the library's kernels
+ * are loaded, whether or not it ever calls this entry point (64 MiB per GPU;
+ * change FTA_NOALLOC_SCRATCH_BYTES here and rebuild to resize it).  A problem needing more returns FTA_ERR_UNSUPPORTED.  The call
  * allocates nothing (no hipMalloc, no library allocator); it uses the current
  * device's array, so `stream` must belong to the current device.  Calls that
  * overlap on one GPU (different streams, or host threads) race on the array.

@@ -95,7 +95,9 @@ def test_config_full_size(name):
     rows_sum = scores.sum(-1)
     assert torch.allclose(rows_sum, torch.ones_like(rows_sum), rtol=1e-4, atol=1e-4)
 
-    heads = sorted({0, H - 1})
+    # the headline config (C3) samples four heads, the others the first and last
+    heads = sorted({0, 7, 19, H - 1}) if name == "C3" else sorted({0, H - 1})
+    scales = []  # largest |gradient| of each float64 check (reported)
     bs = sorted({0, B - 1})
     rows = np.sort(rng.choice(N, size=48, replace=False))
     rows = np.unique(np.concatenate([rows, [0, N - 1]]))
@@ -174,14 +176,14 @@ def test_config_full_size(name):
             rdq, _, _ = O.sparse_attn_bwd(qh, kh, vh, doh, mh, 1, g, b, None, qpad, pad, qblocks=trip, **kw)
             assert_within(np32(q.grad[bb, rws, h * D:(h + 1) * D]), rdq[0, rws], name="dq vs rounding oracle")
             rdq64, _, _ = O.sparse_attn_bwd(qh, kh, vh, doh, mh, 1, g, b, None, qpad, pad, qblocks=trip)
-            scl = max(1.0, np.abs(rdq64[0, rws]).max() / 4)
+            scales.append(("dq", h, np.abs(rdq64[0, rws]).max()))
             # on peaked data (C3) dS = P (dP - delta) is a small difference of large terms and
             # is rounded to 16 bits, so up to 0.1% of dQ elements exceed the soft float64 bound
             frac = 0.999 if data == "peaked" else 0.9995
-            assert_close_frac(np32(q.grad[bb, rws, h * D:(h + 1) * D]), rdq64[0, rws], atol=2e-3 * scl, rtol=1e-2,
-                              name="dq vs f64", min_frac=frac, hard_atol=1e-2 * scl)
+            assert_close_frac(np32(q.grad[bb, rws, h * D:(h + 1) * D]), rdq64[0, rws], atol=2e-3, rtol=1e-2,
+                              name="dq vs f64", min_frac=frac, hard_atol=1e-2)
             # dK / dV of one sampled KV block: every q-block that selected it contributes
-            for m in rng.choice(M, size=1, replace=False):
+            for m in rng.choice(M, size=2 if name == "C3" else 1, replace=False):
                 sel = [(0, 0, int(qm)) for qm in range(QM) if (mh[0, 0, qm] == m).any()]
                 if not sel:
                     continue
@@ -192,7 +194,10 @@ def test_config_full_size(name):
                     gg = np32(got[bb, t0:t1, h * D:(h + 1) * D])
                     assert_within(gg, ref[0, t0:t1], name=f"{nm} vs rounding oracle")
                     r = ref64[0, t0:t1]
-                    s2 = max(1.0, np.abs(r).max() / 4)
-                    assert_close_frac(gg, r, atol=2e-3 * s2, rtol=1e-2, name=f"{nm} vs f64", min_frac=frac,
-                                      hard_atol=1e-2 * s2)
+                    scales.append((nm, h, np.abs(r).max()))
+                    assert_close_frac(gg, r, atol=2e-3, rtol=1e-2, name=f"{nm} vs f64", min_frac=frac,
+                                      hard_atol=1e-2)
+    if scales:
+        say(f"[config {name}] float64 gradient checks (unscaled bound), max |ref|: {max(x[2] for x in scales):.3f} "
+            f"({[(a, b_, round(c, 3)) for a, b_, c in scales]})")
     say(f"[config {name}] ok: M={M} QM={QM} W={Wm} mean count {counts.float().mean().item():.1f}")

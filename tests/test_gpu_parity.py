@@ -395,6 +395,47 @@ def check_attn_vs_oracle(q, k, v, do, o, lse, merged, H, g, b, qpad, kvpad, dt, 
                           hard_atol=1e-2 * s2)
 
 
+def test_dkv_launch_order_many_blocks():
+    """More than 1024 KV blocks through the split dK/dV kernel: its launch order
+    (blocks ranked by selection count in slices of 1024) must still be a
+    permutation of the blocks.  dK / dV of sampled blocks on both sides of 1024
+    against the rounding oracle, and dV exactly zero for every block that no
+    q-block selected and nonzero for every selected one."""
+    from flash_topk_attn_v2.sparse_attn_bwd import preprocess_delta
+
+    B, H, D, g, b, W = 1, 1, 64, 64, 64, 3
+    N = 1100 * 64 - 40
+    kvpad, qpad = (0, 40), (0, 40)
+    say(f"[dkv order] N{N} M1100 D{D} g{g} W{W}")
+    QM = M = 1100
+    merged = _random_merged(B, H, QM, W, M, 21, empty_frac=0.0)
+    q, k, v = (rand((B, N, H * D), 90 + i, torch.bfloat16, "cuda").requires_grad_(True) for i in range(3))
+    tm = torch.from_numpy(merged).cuda()
+    o, lse = fta.flash_topk_attn(q, k, v, tm, (tm >= 0).sum(-1).int(), H, g, b, None, None, kvpad, qpad)
+    do = rand((B, N, H * D), 94, torch.bfloat16, "cuda")
+    o.backward(do)
+    torch.cuda.synchronize()
+    selected = np.zeros(M, dtype=bool)
+    selected[merged[merged >= 0]] = True
+    dv = np32(v.grad)[0]
+    for m in range(M):
+        t0, t1 = m * b, min(N, (m + 1) * b)
+        nz = bool(np.any(dv[t0:t1] != 0))
+        assert nz == selected[m], f"KV block {m}: selected={selected[m]} but dV nonzero={nz}"
+    l = lse.detach().cpu().numpy().astype(np.float64)
+    delta = preprocess_delta(o.detach(), do, H).cpu().numpy().astype(np.float64)
+    qn, kn, vn, dn = np32(q), np32(k), np32(v), np32(do)
+    picks = [int(x) for x in np.nonzero(selected)[0] if x in (0, 5, 700, 1023, 1024, 1050, 1099)]
+    picks += [int(x) for x in np.nonzero(selected[1025:])[0][:3] + 1025]
+    for m in sorted(set(picks)):
+        sel = [(0, 0, qm) for qm in range(QM) if (merged[0, 0, qm] == m).any()]
+        _, rdk, rdv = O.sparse_attn_bwd(qn, kn, vn, dn, merged, H, g, b, None, qpad, kvpad, qblocks=sel,
+                                        round_p="bf16", lse=l, delta=delta)
+        t0, t1 = m * b, min(N, (m + 1) * b)
+        assert_within(np32(k.grad)[0, t0:t1], rdk[0, t0:t1], name=f"dk block {m}")
+        assert_within(dv[t0:t1], rdv[0, t0:t1], name=f"dv block {m}")
+
+
 GQA_CASES = [
     # B, N, H, Hk, D, g, b, qpad, kvpad, W, dtype
     (1, 1000, 4, 2, 128, 32, 64, (0, 24), (0, 24), 8, torch.bfloat16),   # split dK/dV kernel
@@ -521,6 +562,48 @@ def test_flash_sparse_attn_func_reference_contract(N, Nphys, H, D, g, b, qph, kv
         assert a.grad.shape == (1, Nphys, H * D)
         assert torch.equal(a.grad[:, :N], c.grad)
         assert not a.grad[:, N:].any()
+
+
+def test_flash_sparse_attn_func_truncated_counts():
+    """counts below the number of valid entries: the reference's kernel
+    (csrc/sparse_attn_kernel.cu:57-86, :201) sorts each row (at most 512 slots)
+    ascending and walks the first `count` ids, and a row with count 0 gives
+    o = 0, lse = -inf.  The expected lists are built here in plain Python and
+    run through flash_topk_attn."""
+    from flash_topk_attn_v2 import FlashSparseAttnFunc
+
+    N, H, D, g, b, W = 1024, 2, 64, 32, 64, 10
+    say(f"[FlashSparseAttnFunc counts] N{N} H{H} D{D} g{g} b{b} W{W}")
+    QM, M = N // g, N // b
+    merged = _random_merged(1, H, QM, W, M, 11)
+    valid = (merged >= 0).sum(-1)
+    rs = np.random.RandomState(12)
+    counts = np.minimum(valid, rs.randint(0, W + 1, size=valid.shape)).astype(np.int32)
+    counts[0, 0, 3] = 0
+    counts[0, 1, 5] = -2
+    expect = np.full_like(merged, -1)
+    for h in range(H):
+        for qm in range(QM):
+            ids = sorted(int(x) for x in merged[0, h, qm] if x >= 0)[: max(int(counts[0, h, qm]), 0)]
+            expect[0, h, qm, : len(ids)] = ids
+    base = [rand((1, N, H * D), 80 + i, torch.bfloat16, "cuda") for i in range(3)]
+    do = rand((1, N, H * D), 84, torch.bfloat16, "cuda")
+    x1 = [t.clone().requires_grad_(True) for t in base]
+    o1, sm, sl = FlashSparseAttnFunc.apply(x1[0], x1[1], x1[2], torch.from_numpy(merged).cuda(),
+                                           torch.from_numpy(counts).cuda(), H, g, b, W, D ** -0.5, 0, 0, N, M)
+    o1.backward(do)
+    x2 = [t.clone().requires_grad_(True) for t in base]
+    ex = torch.from_numpy(expect).cuda()
+    o2, lse2 = fta.flash_topk_attn(x2[0], x2[1], x2[2], ex, (ex >= 0).sum(-1).int(), H, g, b)
+    o2.backward(do)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    assert torch.equal(sm + sl, lse2)
+    for a, c in zip(x1, x2):
+        assert torch.equal(a.grad, c.grad)
+    # the empty q-blocks: zero output rows, -inf lse
+    assert not o1[0, 3 * g:4 * g, :D].any() and torch.isneginf(sl[0, 0, 3 * g:4 * g]).all()
+    assert not o1[0, 5 * g:6 * g, D:].any() and torch.isneginf(sl[0, 1, 5 * g:6 * g]).all()
 
 
 def _pattern_qk(N, H, D, pattern, seed):

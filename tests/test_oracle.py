@@ -459,3 +459,39 @@ def test_check_topk_f64_rules():
     assert check_topk_f64(np.array([[0, 1, 2]]), raw2, raw2, 0.9, 3) == 0  # cum 0.9 - 1e-9: near the threshold
     raw3 = np.array([[0.4, 0.4 + 1e-9, 0.2]])
     assert check_topk_f64(np.array([[0, 1, 2]]), raw3, raw3, 1.0, 3) == 0  # near-tie swap
+
+
+def test_torch_cpu_baseline_matches_numpy_oracle():
+    """The PyTorch-CPU fp32 pipeline that bench.py times as the CPU baseline
+    (oracle/fta_torch_cpu.py) against the numpy oracle on the same inputs:
+    block scores within fp32 rounding of the float64 ones; the top-k, fed the
+    same fp32 scores, bit for bit; the merge, fed the same top-k, equal; o, lse
+    and the gradients, given the same merged lists, within fp32 rounding."""
+    import fta_torch_cpu as T
+
+    N, D, b, topk, thr, g, W = 512, 64, 64, 4, 0.9, 32, 8
+    gen = torch.Generator().manual_seed(5)
+    q, k, v, do = (torch.randn(N, D, generator=gen) for _ in range(4))
+    sc = T.block_score(q, k, b, chunk=128)
+    ref = O.block_score(q.numpy()[None], k.numpy()[None], 1, b)[0, 0]
+    np.testing.assert_allclose(sc.numpy(), ref, rtol=2e-5, atol=1e-7)
+    idx, raw, avg = T.topk_select(sc, thr, topk, b)
+    ri, rr, ra = O.topk_select(sc.numpy(), thr, topk, b)
+    np.testing.assert_array_equal(idx.numpy(), ri)
+    np.testing.assert_array_equal(avg.numpy(), ra)
+    np.testing.assert_array_equal(raw.numpy(), rr)
+    merged, counts = T.qblock_merge(idx, avg, g, W, N // b)
+    rm, _ = O.qblock_merge(idx.numpy()[None, None], avg.numpy()[None, None], g, W, N // b)
+    np.testing.assert_array_equal(merged.numpy(), rm[0, 0])
+    np.testing.assert_array_equal(counts.numpy(), (rm[0, 0] >= 0).sum(-1))
+    merged[3] = -1  # an empty q-block
+    o, lse, dq, dk, dv = T.sparse_attn_fwd_bwd(q, k, v, do, merged, g, b, group=5)
+    mm = merged.numpy()[None, None]
+    ro, rl = O.sparse_attn(q.numpy()[None], k.numpy()[None], v.numpy()[None], mm, 1, g, b)
+    np.testing.assert_allclose(o.numpy(), ro[0], rtol=1e-4, atol=1e-5)
+    assert np.array_equal(np.isneginf(lse.numpy()), np.isneginf(rl[0, 0]))
+    fin = np.isfinite(rl[0, 0])
+    np.testing.assert_allclose(lse.numpy()[fin], rl[0, 0][fin], rtol=1e-5, atol=1e-5)
+    grads = O.sparse_attn_bwd(q.numpy()[None], k.numpy()[None], v.numpy()[None], do.numpy()[None], mm, 1, g, b)
+    for got, r in zip((dq, dk, dv), grads):
+        np.testing.assert_allclose(got.numpy(), r[0], rtol=1e-4, atol=2e-5)
