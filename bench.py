@@ -252,11 +252,11 @@ class Pipeline:
         self.dt = _lib.dtype_code(self.dtype)
         m_out = topk if 0 < topk < self.M else self.M
         self.m_out = m_out
-        self.ws_score = _lib.workspace(L.fta_topk_score_workspace_size(B, H, N, self.M), dev)
+        self.ws_score = _lib.workspace(L.fta_topk_score_workspace_size_ex(B, H, N, D, b, pad[0], pad[1], topk), dev)
         geo = (B, H, N, D, g, b, qpad[0], qpad[1], pad[0], pad[1])
         self.ws_bwd = _lib.workspace(L.fta_sparse_attn_bwd_workspace_size(*geo), dev)
         self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
-        self.streams_ok = b == 64 and D in (64, 128) and m_out <= 16
+        self.streams_ok = b == 64 and D in (64, 128) and m_out <= 32
         shp = (B, H, N, m_out)
         self.sel_out = (torch.empty(shp, dtype=torch.int32, device=dev), torch.empty(shp, device=dev),
                         torch.empty(shp, device=dev))
@@ -276,7 +276,8 @@ class Pipeline:
     def select_streams(self):
         """The stream selector alone, over the streams the last scorer() call left."""
         L, _lib = self.L, self._lib
-        rc = L.fta_topk_select_candidates(self.B, self.H, self.N, self.D, self.st, self.b, self.pad[0], self.pad[1],
+        rc = L.fta_topk_select_candidates(self.q.data_ptr(), self.k.data_ptr(), self.dt, self.B, self.H, self.N,
+                                          self.D, self.st, self.st, self.b, self.pad[0], self.pad[1], self.D ** -0.5,
                                           self.topk, self.thr, self.sel_out[0].data_ptr(),
                                           self.sel_out[1].data_ptr(), self.sel_out[2].data_ptr(),
                                           self.ws_score.data_ptr(), self.ws_score.numel(), self.stream.cuda_stream)
@@ -346,9 +347,16 @@ class Pipeline:
         row total and start bound (8 B per row) and the three outputs."""
         rows = self.B * self.H * self.N
         waves = self.B * self.H * ((self.N + 255) // 256) * 4
-        off = -(-waves * 64 * self.M * 8 // 256) * 256
-        cnt = self.ws_score[off: off + waves * 4].view(self.torch.int32)
-        return float(cnt.sum().item()) * 8 + rows * 8 + rows * self.m_out * 12
+        cnt = self.ws_score[: waves * 4].view(self.torch.int32)  # per-wave entry counts lead the workspace
+        return float(cnt.clamp(min=0).sum().item()) * 8 + rows * 8 + rows * self.m_out * 12
+
+    def stream_stats(self):
+        """Entries per query of the scorer's candidate streams, tiles sent to the
+        fallback, and the stream workspace (after a scorer() + select_streams())."""
+        waves = self.B * self.H * ((self.N + 255) // 256) * 4
+        cnt = self.ws_score[: waves * 4].view(self.torch.int32)
+        return {"entries_per_query": round(float(cnt.clamp(min=0).sum().item()) / (self.B * self.H * self.N), 2),
+                "overflow_waves": int((cnt < 0).sum().item()), "workspace_bytes": int(self.ws_score.numel())}
 
     def stages(self, bwd=True, reps=5):
         """Per-stage ms and roofline fractions."""
@@ -367,6 +375,7 @@ class Pipeline:
             r["topk_select"] = {"ms": sel_ms, "bound": "hbm", "gbs": sb / sel_ms / 1e6,
                                 "frac": sb / sel_ms / 1e6 / PEAK_HBM_GBS, "bytes": sb,
                                 "note": "fta_topk_select_candidates alone over the scorer's streams"}
+            r["streams"] = self.stream_stats()
         K = self.idx.shape[-1]
         mb = 2.0 * B * H * N * K * 4 + B * H * self.QM * (self.merged.shape[3] + 1) * 4
         t = self.time(self.merge, reps)

@@ -520,18 +520,71 @@ struct ScorePipeShape {
 // pass, so the final selection over the streams equals the one over all
 // blocks.  tau_key[row] receives the final bound (at least m_out blocks rank
 // at or above it).
-constexpr int kStreamMaxTopk = 16;
+constexpr int kStreamMaxTopk = 32;
+// Entries per stream chunk (a multiple of the selector's 256-entry steps).
+constexpr int kStreamChunk = 1024;
 
 __device__ __forceinline__ float fta_stream_margin(float b) { return b - (0x1p-10f + fabsf(b) * 0x1p-18f); }
 
-template <int DT, int D, int NG>
-__global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh, int64_t k_sn,
-    int H, int N, int Dreal, int M, int bsz, int pad_head, int pad_tail, float c,
-    float* __restrict__ blk_lse, float* __restrict__ row_lse, int qtiles, int total, int kgroups,
-    int32_t* __restrict__ tau_idx, uint2* __restrict__ cand, int* __restrict__ cand_count,
-    float* __restrict__ tau_key) {
+// Arguments of the pipelined scoring kernel (one struct, passed by value).
+struct ScoreArgs {
+    const uint16_t* q;
+    const uint16_t* k;
+    int64_t q_sb, q_sh, q_sn, k_sb, k_sh, k_sn;
+    int H, N, Dreal, M, bsz, pad_head, pad_tail;
+    float c;
+    // NG = 0: per-block values.  blk_ld = 0 writes the [B*H][M][N] array at
+    // blk_lse; blk_ld > 0 writes the tile's own [M][blk_ld] slot at blk_lse
+    // (query qt * 256 + j at column j).
+    float* blk_lse;
+    int blk_ld;
+    float* row_lse;
+    int qtiles, total, kgroups;
+    int32_t* tau_idx;
+    // NG > 0: candidate streams in chunks of kStreamChunk entries.  Wave w's
+    // first chunk is chunk w of `pool`; further chunks are taken from the
+    // counter pool_ctr (chunk ids waves + counter value, below pool_chunks) and
+    // recorded in chunk_tab[w][1 ..].  count[w] = the wave's entry count, or -1
+    // when the pool ran out (the wave's tile is then scored again by the
+    // fallback kernel).
+    uint2* pool;
+    int* count;
+    float* tau_key;
+    int* chunk_tab;
+    int* pool_ctr;
+    int pool_chunks, maxch;
+};
+
+// Group state of the candidate-stream filter: per query and block group, the GT
+// largest ranking keys seen, descending, as fp32 (GH = false) or as fp16 (GH =
+// true: half the LDS; the stored values may exceed the keys by the fp16
+// rounding, 2^-11 relative, which the bound's margin covers).
+template <int GB>
+struct GroupRaw;
+template <>
+struct GroupRaw<8> {
+    using type = uint2;
+};
+template <>
+struct GroupRaw<16> {
+    using type = uint4;
+};
+__device__ __forceinline__ float fta_h2f(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu));
+}
+__device__ __forceinline__ uint32_t fta_f2h2(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
+
+template <int DT, int D, int NG, int GT = 2, bool GH = false>
+__device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg) {
+    const uint16_t* __restrict__ q = a.q;
+    const uint16_t* __restrict__ k = a.k;
+    const int64_t q_sb = a.q_sb, q_sh = a.q_sh, q_sn = a.q_sn, k_sb = a.k_sb, k_sh = a.k_sh, k_sn = a.k_sn;
+    const int H = a.H, N = a.N, Dreal = a.Dreal, M = a.M, bsz = a.bsz, pad_head = a.pad_head,
+              pad_tail = a.pad_tail, qtiles = a.qtiles, kgroups = a.kgroups;
+    const float c = a.c;
     // NG > 0: candidate streams with NG block groups (STREAM)
     constexpr bool STREAM = NG > 0;
     using E = Elem<DT>;
@@ -540,9 +593,12 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     constexpr int KS = D / 16;
     constexpr int QSEG = Sh::QSEG, LQ = Sh::LQ, NBUF = Sh::NBUF;
     __shared__ __align__(1024) unsigned char sK[NBUF][Sh::BUF_B];
-    __shared__ float2 sG[STREAM ? NG : 1][256];
+    static_assert(GT == 2 || GT == 4, "group top-2 or top-4");
+    static_assert(!GH || GT == 4, "fp16 group state holds four keys");
+    constexpr int GB = GT * (GH ? 2 : 4);  // bytes per (group, query)
+    using GRaw = typename GroupRaw<GB>::type;
+    __shared__ __align__(16) GRaw sG[STREAM ? NG : 1][256];
 
-    const int wg = fta_xcd_remap(blockIdx.x, total);
     const int bh = wg / qtiles;
     const int qt = wg - bh * qtiles;
     const int b = bh / H, h = bh - (bh / H) * H;
@@ -640,6 +696,7 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     // tiles; L: running total of the lane's own (tile lane >> 5, query lane & 31)
     float R[2] = {-FTA_INF, -FTA_INF}, L = 0.f;
     const bool own1 = lane >= 32;
+    float Rown = -FTA_INF;  // R of the lane's own tile (R[lane >> 5])
     // One pipeline stage, written in issue order: the MFMAs of half s of block mb
     // (into dst) interleaved with the exps of src, 32 / KS exps after each MFMA
     // pair.  The sums use the same 16-term tree as fta_sum_exp2<16>.
@@ -696,18 +753,65 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
     const float adj_head = (pad_head > 0) ? fta_log2((float)bsz / (float)(bsz - pad_head)) : 0.f;
     const float adj_tail = (pad_tail > 0) ? fta_log2((float)bsz / (float)(bsz - pad_tail)) : 0.f;
 
-    // candidate-stream state: this wave's key / mask streams, write position,
-    // current filter bound and group slot
+    // the GT keys of a group-state entry, descending
+    auto gdecode = [&](const GRaw& r, float (&t)[GT]) {
+        if constexpr (GH) {
+            const uint2 u = __builtin_bit_cast(uint2, r);
+            t[0] = fta_h2f(u.x);
+            t[1] = fta_h2f(u.x >> 16);
+            t[2] = fta_h2f(u.y);
+            t[3] = fta_h2f(u.y >> 16);
+        } else {
+            const auto f = __builtin_bit_cast(typename std::conditional<GT == 2, float2, float4>::type, r);
+            t[0] = f.x;
+            t[1] = f.y;
+            if constexpr (GT == 4) {
+                t[2] = f.z;
+                t[3] = f.w;
+            }
+        }
+    };
+    auto gencode = [&](const float (&t)[GT]) -> GRaw {
+        if constexpr (GH) {
+            return __builtin_bit_cast(GRaw, make_uint2(fta_f2h2(t[0], t[1]), fta_f2h2(t[2], t[3])));
+        } else if constexpr (GT == 2) {
+            return __builtin_bit_cast(GRaw, make_float2(t[0], t[1]));
+        } else {
+            return __builtin_bit_cast(GRaw, make_float4(t[0], t[1], t[2], t[3]));
+        }
+    };
+    // the smallest kept key of group j (the bound's operand)
+    auto glast = [&](int j) -> float {
+        const GRaw r = sG[j][tid];
+        if constexpr (GH) {
+            return fta_h2f(__builtin_bit_cast(uint2, r).y >> 16);
+        } else {
+            float t[GT];
+            gdecode(r, t);
+            return t[GT - 1];
+        }
+    };
+    // bound from a min over groups: fp16 keys may sit 2^-11 relative above the
+    // key they hold, so their bound is lowered by a further 2^-10 relative
+    auto gmargin = [&](float bnd) -> float {
+        return GH ? fta_stream_margin(bnd) - fabsf(bnd) * 0x1p-10f : fta_stream_margin(bnd);
+    };
+
+    // candidate-stream state: the wave's current chunk and position in it, its
+    // chunk count and entry count, and the current filter bound
     uint2* cst = nullptr;
-    int spos = 0;
+    int cpos = 0, nch = 1, spos = 0;
+    const int64_t sw = (int64_t)wg * 4 + wave;
     // lanes past N never pass: their bound is +inf
     const bool lane_ok = qbase + lane < N;
     float sbnd = lane_ok ? -FTA_INF : FTA_INF;
     if constexpr (STREAM) {
-        const int64_t sw = (int64_t)wg * 4 + wave;
-        cst = cand + sw * 64 * M;
+        cst = a.pool + sw * kStreamChunk;
+        float ninf[GT];
 #pragma unroll
-        for (int j = 0; j < NG; ++j) sG[j][tid] = make_float2(-FTA_INF, -FTA_INF);
+        for (int i = 0; i < GT; ++i) ninf[i] = -FTA_INF;
+#pragma unroll
+        for (int j = 0; j < NG; ++j) sG[j][tid] = gencode(ninf);
     }
 
 #pragma unroll
@@ -741,7 +845,7 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
         __syncthreads();  // block m + 1 visible; every wave is past block m - 1
         if (m + 3 < M) issue(m + 3);
         // this block's group top-2 entry, read now so its latency hides under the stages
-        float2 gtop = make_float2(0.f, 0.f);
+        GRaw gtop = {};
         if constexpr (STREAM) gtop = sG[gslot][tid];
 
         float e0[2], e1[2];
@@ -778,11 +882,12 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
             tot_own = a + b;
         }
         // every (tile, query) is owned by one lane, so wave votes on tot_own cover both
-        // tiles.  The rare cases (a total that overflows the reference or grows large)
-        // share one branch, so the common path keeps R and L in place.
-        float mine;
-        if (__ballot(!(tot_own < 0x1p100f) || tot_own > 0x1p40f) != 0ull) {
-            if (__ballot(!(tot_own < 0x1p100f)) != 0ull) {
+        // tiles.  The rare cases (a total that overflows the reference, or grows
+        // large) are handled around the common update, so R and L keep one
+        // definition on the common path (no register copies at the merges).
+        const bool rare = __ballot(!(tot_own <= 0x1p40f)) != 0ull;  // large, infinite or NaN
+        {
+            if (rare && __ballot(!(tot_own < 0x1p100f)) != 0ull) {
                 // exact path: reference = this block's max (scores recomputed from LDS)
                 f32x16 x0[2], x1[2];
                 mma_half(bm, 0, x0);
@@ -801,6 +906,7 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
                     R[t] = (mx == -FTA_INF) ? 0.f : mx * c;
                 }
                 const float R_new = own1 ? R[1] : R[0];
+                Rown = R_new;
                 L = (L > 0.f) ? L * fta_exp2(R_old - R_new) : 0.f;
                 float f0[2], f1[2];
                 sums16(x0, R, f0);
@@ -813,11 +919,12 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
                 }
                 tot_own = own1 ? tot[1] : tot[0];
             }
-            // only the lane's own block lse is stored
-            const float R_m = own1 ? R[1] : R[0];
-            mine = (tot_own > 0.f) ? R_m + fta_log2(tot_own) : -FTA_INF;
-            L += tot_own;
-            if (__ballot(tot_own > 0x1p40f) != 0ull) {
+        }
+        // only the lane's own block lse is stored (log2(0) = -inf)
+        const float mine = Rown + fta_log2(tot_own);
+        L += tot_own;
+        {
+            if (rare && __ballot(tot_own > 0x1p40f) != 0ull) {
                 // rebase a large row total on this block's lse (both tiles' references,
                 // so this lane's exps of the other tile stay in step with its owner)
                 float x = tot_own, y = tot_own;
@@ -831,11 +938,8 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
                         if ((t == 1) == own1) L *= fta_exp2(R[t] - Rn);
                         R[t] = Rn;
                     }
+                Rown = own1 ? R[1] : R[0];
             }
-        } else {
-            const float R_m = own1 ? R[1] : R[0];
-            mine = (tot_own > 0.f) ? R_m + fta_log2(tot_own) : -FTA_INF;
-            L += tot_own;
         }
         const int qi = qbase + lane;
         if constexpr (STREAM) {
@@ -847,27 +951,62 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
             const unsigned long long mk = __ballot(pass);
             const int rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32),
                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
-            if (pass) {  // wave-uniform base, 32-bit lane offset
-                uint2* dst = cst + spos;
-                dst[(uint32_t)rank] = make_uint2(__builtin_bit_cast(uint32_t, mine), ((uint32_t)lane << 16) | m);
+            const int nmk = __popcll(mk);
+            const uint2 entry = make_uint2(__builtin_bit_cast(uint32_t, mine), ((uint32_t)lane << 16) | m);
+            if (cpos + nmk <= kStreamChunk) {
+                if (pass) {  // wave-uniform base, 32-bit lane offset
+                    uint2* dst = cst + cpos;
+                    dst[(uint32_t)rank] = entry;
+                }
+                cpos += nmk;
+            } else {
+                // the chunk is full (or the pool ran out before: cpos is then past
+                // any chunk): continue in a new chunk from the pool
+                int id = 0;
+                if (lane == 0 && cpos <= kStreamChunk) id = atomicAdd(a.pool_ctr, 1);
+                id = __builtin_amdgcn_readfirstlane(id) + a.total * 4;
+                if (cpos > kStreamChunk || id >= a.pool_chunks || nch >= a.maxch) {
+                    cpos = 0x40000000;  // out of pool: no further entries are stored
+                } else {
+                    if (lane == 0) a.chunk_tab[sw * a.maxch + nch] = id;
+                    ++nch;
+                    uint2* nxt = a.pool + (int64_t)id * kStreamChunk;
+                    const int room = kStreamChunk - cpos;
+                    if (pass) {
+                        uint2* dst = (rank < room) ? cst + cpos + rank : nxt + (rank - room);
+                        *dst = entry;
+                    }
+                    cst = nxt;
+                    cpos += nmk - kStreamChunk;
+                }
             }
-            spos += __popcll(mk);
-            // group top-2 (t.y <= t.x): new second = med3(t.x, t.y, ak), new first =
-            // max(t.x, ak).  Written as instructions: the compiler's max / med3 first
-            // quiet every operand (three extra instructions), and no value here is a NaN.
-            float2 t = gtop;
-            float nx, ny;
-            asm("v_med3_f32 %0, %1, %2, %3" : "=v"(ny) : "v"(t.x), "v"(t.y), "v"(ak));
-            asm("v_max_f32 %0, %1, %2" : "=v"(nx) : "v"(t.x), "v"(ak));
-            sG[gslot][tid] = make_float2(nx, ny);
-            if (gslot == NG - 1) {
-                float bnd = sG[0][tid].y;
+            spos += nmk;
+            // group top-GT insertion (t descending): new t0 = max(t0, ak), new t_i =
+            // med3(t_{i-1}, t_i, ak).  Written as instructions: the compiler's max /
+            // med3 first quiet every operand, and no value here is a NaN.  fp16 state
+            // takes the key clamped to the largest finite half (below the key).
+            float t[GT], nt[GT];
+            gdecode(gtop, t);
+            float akg = ak;
+            if constexpr (GH) asm("v_min_f32 %0, %1, %2" : "=v"(akg) : "v"(ak), "v"(65504.f));
+            asm("v_max_f32 %0, %1, %2" : "=v"(nt[0]) : "v"(t[0]), "v"(akg));
 #pragma unroll
-                for (int j = 1; j < NG; ++j) bnd = __builtin_amdgcn_fmed3f(bnd, sG[j][tid].y, -FTA_INF);
-                sbnd = lane_ok ? fta_stream_margin(bnd) : FTA_INF;
+            for (int i = 1; i < GT; ++i)
+                asm("v_med3_f32 %0, %1, %2, %3" : "=v"(nt[i]) : "v"(t[i - 1]), "v"(t[i]), "v"(akg));
+            sG[gslot][tid] = gencode(nt);
+            if (gslot == NG - 1) {
+                float bnd = glast(0);
+#pragma unroll
+                for (int j = 1; j < NG; ++j) bnd = __builtin_amdgcn_fmed3f(bnd, glast(j), -FTA_INF);
+                sbnd = lane_ok ? gmargin(bnd) : FTA_INF;
             }
         } else {
-            if (qi < N) blk_lse[((int64_t)bh * M + m) * N + qi] = mine;
+            if (qi < N) {
+                if (a.blk_ld == 0)
+                    a.blk_lse[((int64_t)bh * M + m) * N + qi] = mine;
+                else
+                    a.blk_lse[(int64_t)m * a.blk_ld + (qi - qt * 256)] = mine;
+            }
         }
         if (!STREAM && kgroups > 0) {
             float key = mine;
@@ -911,21 +1050,26 @@ __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(
 
     const int qi = qbase + lane;
     if constexpr (STREAM) {
-        if (lane == 0) cand_count[(int64_t)wg * 4 + wave] = spos;
+        if (lane == 0) a.count[sw] = (cpos > kStreamChunk) ? -1 : spos;
     }
     if (qi < N) {
-        const float Rr = own1 ? R[1] : R[0];
-        row_lse[(int64_t)bh * N + qi] = (L > 0.f) ? Rr + fta_log2(L) : -FTA_INF;
+        a.row_lse[(int64_t)bh * N + qi] = (L > 0.f) ? Rown + fta_log2(L) : -FTA_INF;
         if constexpr (STREAM) {
-            float bnd = sG[0][tid].y;
+            float bnd = glast(0);
 #pragma unroll
-            for (int j = 1; j < NG; ++j) bnd = fminf(bnd, sG[j][tid].y);
-            tau_key[(int64_t)bh * N + qi] = bnd;
+            for (int j = 1; j < NG; ++j) bnd = fminf(bnd, glast(j));
+            if constexpr (GH) bnd = bnd - fabsf(bnd) * 0x1p-10f;  // the fp16 rounding, as in gmargin
+            a.tau_key[(int64_t)bh * N + qi] = bnd;
         } else if (kgroups > 0) {
             if (curg >= 0 && gkey < tkey) tidx = gidx;
-            tau_idx[(int64_t)bh * N + qi] = tidx;
+            a.tau_idx[(int64_t)bh * N + qi] = tidx;
         }
     }
+}
+
+template <int DT, int D, int NG, int GT, bool GH>
+__global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(const ScoreArgs a) {
+    fta_score_tile<DT, D, NG, GT, GH>(a, fta_xcd_remap(blockIdx.x, a.total));
 }
 
 // ----------------------------------------------------------------------------
@@ -1145,22 +1289,20 @@ __device__ __forceinline__ void fta_topk_emit(float (&lv)[KB], int (&li)[KB], in
     }
 }
 
+// Rows blk * 256 .. blk * 256 + 255 of the selection (one row per thread).
 template <int KB, int MODE>
-// Lists of <= 16 entries fit 4 waves per SIMD (<= 128 VGPRs), which keeps more
-// of the scan's loads in flight; longer lists run at 2 waves per SIMD (a
-// 64-entry list then spills a few registers, still 40% faster than 1 wave).
-__global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_select_kernel(
+__device__ __forceinline__ void fta_topk_rows(
     const float* __restrict__ in, int64_t stride_row, int64_t stride_m, const float* __restrict__ row_lse,
     int N, int rows, int M, int m_out, int bsz, int pad_head, int pad_tail, float threshold,
     int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg,
-    const int32_t* __restrict__ tau_idx) {
+    const int32_t* __restrict__ tau_idx, const int blk) {
     constexpr int LDB = 24;             // blocks loaded per batch
     constexpr int UNR = 8;              // blocks tested between candidate-list checks
     constexpr int CAP = 12 + UNR;       // a sub-batch starts with at most CAP - UNR parked candidates
     __shared__ __align__(16) float cand_v[4][CAP][64];
     __shared__ int cand_i[4][CAP][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int row = blockIdx.x * 256 + tid;
+    const int row = blk * 256 + tid;
     const bool active = row < rows;
 
     float lv[KB];
@@ -1273,11 +1415,24 @@ __global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_select_kerne
     flush();
 
     // the wave's rows are consecutive: rows wrow0 .. wrow0 + nrows - 1
-    const int64_t wrow0 = (int64_t)blockIdx.x * 256 + wave * 64;
+    const int64_t wrow0 = (int64_t)blk * 256 + wave * 64;
     const int nrows = (int)min((int64_t)64, (int64_t)rows - wrow0);
     if (nrows <= 0) return;
     fta_topk_emit<KB, CAP>(lv, li, m_out, M, bsz, pad_head, pad_tail, threshold, out_idx, out_raw, out_avg, wrow0,
                            nrows, lane, active, row, cand_v[wave]);
+}
+
+// Lists of <= 16 entries fit 4 waves per SIMD (<= 128 VGPRs), which keeps more
+// of the scan's loads in flight; longer lists run at 2 waves per SIMD (a
+// 64-entry list then spills a few registers, still 40% faster than 1 wave).
+template <int KB, int MODE>
+__global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_select_kernel(
+    const float* __restrict__ in, int64_t stride_row, int64_t stride_m, const float* __restrict__ row_lse,
+    int N, int rows, int M, int m_out, int bsz, int pad_head, int pad_tail, float threshold,
+    int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg,
+    const int32_t* __restrict__ tau_idx) {
+    fta_topk_rows<KB, MODE>(in, stride_row, stride_m, row_lse, N, rows, M, m_out, bsz, pad_head, pad_tail,
+                            threshold, out_idx, out_raw, out_avg, tau_idx, blockIdx.x);
 }
 
 // Top-k selection over the candidate streams of the pipelined scoring kernel
@@ -1291,11 +1446,17 @@ __global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_select_kerne
 // insertion network) and the entry is parked again.  Each owner's bound starts
 // from tau_key (at least m_out blocks rank at or above it) and tightens as its
 // list fills.
+//
+// The streams are chains of kStreamChunk-entry chunks (ScoreArgs).  A tile
+// (workgroup) with a wave whose stream ran out of pool (count -1) selects
+// nothing: it appends its tile index to ovf_list (count in *ovf_cnt) for the
+// fallback kernel, which scores and selects those tiles again.
 template <int KB>
-__global__ __launch_bounds__(256, 4) void fta_topk_stream_kernel(
-    const uint2* __restrict__ cand, const int* __restrict__ cand_count, const float* __restrict__ tau_key,
-    const float* __restrict__ row_lse, int N, int qtiles, int M, int m_out, int bsz, int pad_head, int pad_tail,
-    float threshold, int32_t* __restrict__ out_idx, float* __restrict__ out_raw, float* __restrict__ out_avg) {
+__global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_stream_kernel(
+    const uint2* __restrict__ pool, const int* __restrict__ cand_count, const int* __restrict__ chunk_tab, int maxch,
+    const float* __restrict__ tau_key, const float* __restrict__ row_lse, int N, int qtiles, int M, int m_out,
+    int bsz, int pad_head, int pad_tail, float threshold, int32_t* __restrict__ out_idx, float* __restrict__ out_raw,
+    float* __restrict__ out_avg, int* __restrict__ ovf_list, int* __restrict__ ovf_cnt) {
     constexpr int CAP = 16;
     __shared__ __align__(16) float cand_v[4][CAP][64];
     __shared__ int cand_i[4][CAP][64];
@@ -1309,7 +1470,14 @@ __global__ __launch_bounds__(256, 4) void fta_topk_stream_kernel(
     const bool active = n < N;
     const int64_t row = (int64_t)bh * N + (active ? n : 0);
     const int64_t sw = (int64_t)blockIdx.x * 4 + wave;
-    const uint2* ent = cand + sw * 64 * M;
+    {
+        const int* c4 = cand_count + (int64_t)blockIdx.x * 4;
+        if (min(min(c4[0], c4[1]), min(c4[2], c4[3])) < 0) {  // a stream of this tile is incomplete
+            if (tid == 0) ovf_list[atomicAdd(ovf_cnt, 1)] = blockIdx.x;
+            return;
+        }
+    }
+    const int* tab = chunk_tab + sw * maxch;
     const int total = __builtin_amdgcn_readfirstlane(cand_count[sw]);
 
     float lv[KB];
@@ -1360,12 +1528,14 @@ __global__ __launch_bounds__(256, 4) void fta_topk_stream_kernel(
     // are issued together, so their LDS latencies overlap.
     constexpr int NC = 4;
     auto load_step = [&] __attribute__((always_inline)) (int c0, uint2 (&e)[NC]) {
+        if (c0 >= total) return;
+        // the step's 256 entries lie in one chunk; entries past the end (still
+        // inside the chunk) are masked where they are used
+        const int j = c0 / kStreamChunk;
+        const int id = (j == 0) ? (int)sw : tab[j];
+        const uint2* ent = pool + (int64_t)id * kStreamChunk + (c0 - j * kStreamChunk);
 #pragma unroll
-        for (int i = 0; i < NC; ++i) {
-            // unconditional (clamped) loads keep the next step's loads in flight;
-            // entries past the end are masked where they are used
-            e[i] = ent[min(c0 + i * 64 + lane, 64 * M - 1)];
-        }
+        for (int i = 0; i < NC; ++i) e[i] = ent[i * 64 + lane];
     };
     uint2 ea[NC], eb[NC];
     load_step(0, ea);
@@ -1410,6 +1580,48 @@ __global__ __launch_bounds__(256, 4) void fta_topk_stream_kernel(
     if (nrows <= 0) return;
     fta_topk_emit<KB, CAP>(lv, li, m_out, M, bsz, pad_head, pad_tail, threshold, out_idx, out_raw, out_avg,
                            (int64_t)bh * N + n0, nrows, lane, active, row, cand_v[wave]);
+}
+
+// Zeroes the stream pool's chunk counter and the fallback tile count (ctrs[0],
+// ctrs[1]) before a scoring launch.
+__global__ void fta_stream_reset_kernel(int* __restrict__ ctrs) {
+    if (threadIdx.x < 2) ctrs[threadIdx.x] = 0;
+}
+
+// Fallback for the tiles whose candidate streams ran out of pool (listed by
+// fta_topk_stream_kernel): each workgroup takes listed tiles in turn, scores
+// the tile's 256 queries into its own [M][256] slot of per-block values (the
+// scoring kernel's code with the stream filter replaced by the value store, so
+// every value is the same fp32 number the stream carried) and selects their
+// top-k from the slot with the selector of the per-block-value path.  The
+// results equal the stream path's (both selectors are exact); only the time
+// differs.
+template <int DT, int D, int KB>
+__global__ __launch_bounds__(256, 1) void fta_stream_fallback_kernel(ScoreArgs a, const int* __restrict__ ovf_list,
+                                                                    const int* __restrict__ ovf_cnt,
+                                                                    float* __restrict__ slots, int m_out,
+                                                                    float threshold, int32_t* __restrict__ out_idx,
+                                                                    float* __restrict__ out_raw,
+                                                                    float* __restrict__ out_avg) {
+    const int n = __builtin_amdgcn_readfirstlane(*ovf_cnt);
+    if ((int)blockIdx.x >= n) return;
+    float* slot = slots + (int64_t)blockIdx.x * 256 * a.M;
+    a.blk_lse = slot;
+    a.blk_ld = 256;
+    a.kgroups = 0;
+    a.tau_idx = nullptr;
+    for (int r = blockIdx.x; r < n; r += gridDim.x) {
+        const int tile = __builtin_amdgcn_readfirstlane(ovf_list[r]);
+        fta_score_tile<DT, D, 0>(a, tile);
+        __syncthreads();  // the slot is complete
+        const int bh = tile / a.qtiles, qt = tile - bh * a.qtiles;
+        const int64_t r0 = (int64_t)bh * a.N + qt * 256;
+        const int rows = min(256, a.N - qt * 256);
+        fta_topk_rows<KB, 1>(slot, 0, 0, a.row_lse + r0, 256, rows, a.M, m_out, a.bsz, a.pad_head, a.pad_tail,
+                             threshold, out_idx + r0 * m_out, out_raw + r0 * m_out, out_avg + r0 * m_out, nullptr,
+                             0);
+        __syncthreads();  // the slot is free for the next tile
+    }
 }
 
 // Slow general path for m_out > 64: one workgroup per row, bitonic sort of the
@@ -1497,6 +1709,8 @@ __global__ __launch_bounds__(256) void fta_topk_select_sort_kernel(
 // ----------------------------------------------------------------------------
 #include "fta_host.h"
 
+#include <cmath>
+
 namespace {
 
 // The pipelined scoring kernel serves b = 64 with D <= 128 rounded to 64 or 128
@@ -1505,17 +1719,65 @@ bool score_pipe_ok(int bsz, int Dk, const int64_t* ks) {
     return bsz == 64 && (Dk == 64 || Dk == 128) && ks[2] >= 0 && ks[2] <= (1 << 24);
 }
 
-// Candidate streams of the pipelined kernel (STREAM = true): entries
-// [waves][64 * M] (value, lane << 16 | m), counts [waves], tau keys [B*H][N];
-// waves = B * H * ceil(N / 256) * 4.
+// Candidate streams of the pipelined kernel (STREAM = true), laid out in the
+// workspace by stream_layout: per-wave entry counts, chunk tables, the two
+// counters (pool chunks taken, fallback tiles), the fallback tile list, row
+// totals, tau keys, the fallback slots and the chunk pool (the rest of the
+// workspace).  waves = B * H * ceil(N / 256) * 4.
 struct StreamBufs {
-    uint2* cand = nullptr;
+    uint2* pool = nullptr;
     int* count = nullptr;
+    int* tab = nullptr;
+    int* ctrs = nullptr;
+    int* ovf_list = nullptr;
     float* tau_key = nullptr;
-    int ngroups = 0;
+    float* slots = nullptr;
+    int m_out = 0;
+    int maxch = 0;
+    int pool_chunks = 0;
 };
 
+// Fallback slots ([M][256] fp32 each): the fallback kernel's workgroups.
+constexpr int kStreamSlots = 64;
+
 int64_t stream_waves(int B, int H, int N) { return (int64_t)B * H * ((N + 255) / 256) * 4; }
+
+ScoreArgs score_args(const void* q, const void* k, int B, int H, int N, int D, const int64_t* qs, const int64_t* ks,
+                     int M, int bsz, int pad_head, int pad_tail, float scale, float* blk_lse, float* row_lse,
+                     int kgroups, int32_t* tau, const StreamBufs& sb) {
+    ScoreArgs a;
+    a.q = (const uint16_t*)q;
+    a.k = (const uint16_t*)k;
+    a.q_sb = qs[0];
+    a.q_sh = qs[1];
+    a.q_sn = qs[2];
+    a.k_sb = ks[0];
+    a.k_sh = ks[1];
+    a.k_sn = ks[2];
+    a.H = H;
+    a.N = N;
+    a.Dreal = D;
+    a.M = M;
+    a.bsz = bsz;
+    a.pad_head = pad_head;
+    a.pad_tail = pad_tail;
+    a.c = scale * 1.4426950408889634f;
+    a.blk_lse = blk_lse;
+    a.blk_ld = 0;
+    a.row_lse = row_lse;
+    a.qtiles = (N + 255) / 256;
+    a.total = a.qtiles * B * H;
+    a.kgroups = kgroups;
+    a.tau_idx = tau;
+    a.pool = sb.pool;
+    a.count = sb.count;
+    a.tau_key = sb.tau_key;
+    a.chunk_tab = sb.tab;
+    a.pool_ctr = sb.ctrs;
+    a.pool_chunks = sb.pool_chunks;
+    a.maxch = sb.maxch;
+    return a;
+}
 
 template <int DT>
 int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D, int Dk, const int64_t* qs,
@@ -1526,19 +1788,26 @@ int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D
     const int total = qtiles * B * H;
     const float c = scale * 1.4426950408889634f;
     const bool pipe = score_pipe_ok(bsz, Dk, ks);
-    if (sb.cand != nullptr && !pipe) return fta::arg_error("block_score: candidate streams need the pipelined kernel");
-#define FTA_LAUNCH_PIPE(DK, NG, CAND, CNT, TAU, KG, TI)                                                   \
-    hipLaunchKernelGGL((fta_block_score_lse_pipe_kernel<DT, (DK == 64) ? 64 : 128, NG>), dim3(total),       \
-                       dim3(256), 0, st, (const uint16_t*)q, (const uint16_t*)k, qs[0], qs[1], qs[2], ks[0],  \
-                       ks[1], ks[2], H, N, D, M, bsz, pad_head, pad_tail, c, blk_lse, row_lse, qtiles, total, KG, \
-                       TI, CAND, CNT, TAU)
+    if (sb.pool != nullptr && !pipe) return fta::arg_error("block_score: candidate streams need the pipelined kernel");
+    if (sb.pool != nullptr) {
+        hipLaunchKernelGGL(fta_stream_reset_kernel, dim3(1), dim3(64), 0, st, sb.ctrs);
+        int rc = fta::check_launch("fta_stream_reset_kernel");
+        if (rc != FTA_OK) return rc;
+    }
+    const ScoreArgs sa = score_args(q, k, B, H, N, D, qs, ks, M, bsz, pad_head, pad_tail, scale, blk_lse, row_lse,
+                                    kgroups, tau, sb);
+#define FTA_LAUNCH_PIPE(DK, NG, GT, GH)                                                                    \
+    hipLaunchKernelGGL((fta_block_score_lse_pipe_kernel<DT, (DK == 64) ? 64 : 128, NG, GT, GH>), dim3(total), \
+                       dim3(256), 0, st, sa)
 #define FTA_LAUNCH_SCORE(DK)                                                                               \
-    if (pipe && sb.cand != nullptr && sb.ngroups <= 4)                                                     \
-        FTA_LAUNCH_PIPE(DK, 4, sb.cand, sb.count, sb.tau_key, 0, nullptr);                                 \
-    else if (pipe && sb.cand != nullptr)                                                                   \
-        FTA_LAUNCH_PIPE(DK, 8, sb.cand, sb.count, sb.tau_key, 0, nullptr);                                 \
+    if (pipe && sb.pool != nullptr && sb.m_out <= 8)                                                       \
+        FTA_LAUNCH_PIPE(DK, 4, 2, false);                                                                  \
+    else if (pipe && sb.pool != nullptr && sb.m_out <= 16)                                                 \
+        FTA_LAUNCH_PIPE(DK, 4, 4, false);                                                                  \
+    else if (pipe && sb.pool != nullptr)                                                                   \
+        FTA_LAUNCH_PIPE(DK, 8, 4, true);                                                                   \
     else if (pipe)                                                                                         \
-        FTA_LAUNCH_PIPE(DK, 0, nullptr, nullptr, nullptr, kgroups, tau);                                   \
+        FTA_LAUNCH_PIPE(DK, 0, 2, false);                                                                  \
     else if (bsz <= 64)                                                                                    \
         hipLaunchKernelGGL((fta_block_score_lse_fast_kernel<DT, DK, (DK > 128) ? 1 : 2>), dim3(total),    \
                            dim3(256 * (2 / ((DK > 128) ? 1 : 2))), 0, st,                                \
@@ -1666,64 +1935,185 @@ int fta_topk_select(const float* block_scores, int64_t rows, int M, int64_t stri
     FTA_TRY_END
 }
 
-// Either path's workspace: [BH][M][N] block values + row totals + tau ids, or
-// the candidate streams + row totals + tau keys.
+}  // extern "C"
+
+namespace {
+// Candidate-stream workspace geometry (stream_layout): everything but the
+// chunk pool has a fixed size; the pool takes the rest of the workspace.
+struct StreamGeo {
+    int64_t waves, tiles;
+    int maxch;
+    size_t fixed;
+};
+StreamGeo stream_geo(int B, int H, int N, int M) {
+    StreamGeo g;
+    g.waves = stream_waves(B, H, N);
+    g.tiles = g.waves / 4;
+    g.maxch = (64 * M + kStreamChunk - 1) / kStreamChunk + 1;  // a wave never needs more chunks
+    const size_t rows = (size_t)B * H * N;
+    g.fixed = fta::align_up(g.waves * sizeof(int)) + fta::align_up(g.waves * g.maxch * sizeof(int)) +
+              fta::align_up(4 * sizeof(int)) + fta::align_up(g.tiles * sizeof(int)) +
+              2 * fta::align_up(rows * sizeof(float)) +
+              fta::align_up((size_t)kStreamSlots * 256 * M * sizeof(float));
+    return g;
+}
+constexpr size_t kChunkBytes = (size_t)kStreamChunk * sizeof(uint2);
+// The least workspace of the stream path: one chunk per wave.
+size_t stream_min_bytes(int B, int H, int N, int M) {
+    const StreamGeo g = stream_geo(B, H, N, M);
+    return g.fixed + (size_t)g.waves * kChunkBytes;
+}
+// The recommended workspace of the stream path: a pool for the expected number
+// of stream entries, E = m_out (1 + 2 ln(M / m_out)) per query (at most M; a
+// block enters a query's stream when it may still be in its top m_out, which
+// for blocks in random order happens about m_out ln(M / m_out) times beyond
+// the first m_out; the filter's bound is looser than the exact m_out-th key,
+// hence the factor 2), plus half a chunk per wave for partly filled chunks.
+// Inputs that need more run their overflowing tiles through the fallback kernel.
+size_t stream_rec_bytes(int B, int H, int N, int M, int m_out) {
+    const StreamGeo g = stream_geo(B, H, N, M);
+    double e = (m_out >= M) ? (double)M : (double)m_out * (1.0 + 2.0 * std::log((double)M / (double)m_out));
+    if (e > (double)M) e = (double)M;
+    const double entries = (double)B * H * N * std::ceil(e) + (double)g.waves * (kStreamChunk / 2);
+    int64_t chunks = (int64_t)std::ceil(entries / kStreamChunk);
+    if (chunks < g.waves) chunks = g.waves;
+    if (chunks > g.waves * g.maxch) chunks = g.waves * g.maxch;
+    return g.fixed + (size_t)chunks * kChunkBytes;
+}
+// The per-block value path: [BH][M][N] values + row totals + tau ids.
+size_t full_bytes(int B, int H, int N, int M) {
+    return fta_block_score_workspace_size(B, H, N, M) + fta::align_up((size_t)B * H * N * sizeof(int32_t));
+}
+}  // namespace
+
+extern "C" {
+
 size_t fta_topk_score_workspace_size(int B, int H, int N, int M) {
-    const size_t full = fta_block_score_workspace_size(B, H, N, M) + fta::align_up((size_t)B * H * N * sizeof(int32_t));
-    const size_t w = (size_t)stream_waves(B, H, N);
-    const size_t strm = fta::align_up(w * 64 * M * sizeof(uint2)) + fta::align_up(w * sizeof(int)) +
-                        2 * fta::align_up((size_t)B * H * N * sizeof(float));
+    if (B <= 0 || H <= 0 || N <= 0 || M <= 0) return 0;
+    const size_t full = full_bytes(B, H, N, M);
+    const size_t strm = stream_rec_bytes(B, H, N, M, M < kStreamMaxTopk ? M : kStreamMaxTopk);
     return full > strm ? full : strm;
+}
+
+size_t fta_topk_score_workspace_size_ex(int B, int H, int N, int D, int score_block_size, int pad_head,
+                                        int pad_tail, int max_topk) {
+    int M = 0;
+    if (fta::check_score_args(B, H, N, D, score_block_size, pad_head, pad_tail, &M) != FTA_OK || max_topk < 0)
+        return 0;
+    const int m_out = (max_topk > 0 && max_topk < M) ? max_topk : M;
+    const int64_t ks[3] = {0, 0, 0};  // a token stride within the pipelined kernel's range
+    if (m_out <= kStreamMaxTopk && score_pipe_ok(score_block_size, fta::kernel_head_dim(D), ks))
+        return stream_rec_bytes(B, H, N, M, m_out);
+    return full_bytes(B, H, N, M);
+}
+
+size_t fta_topk_score_workspace_min(int B, int H, int N, int D, int score_block_size, int pad_head, int pad_tail,
+                                    int max_topk) {
+    int M = 0;
+    if (fta::check_score_args(B, H, N, D, score_block_size, pad_head, pad_tail, &M) != FTA_OK || max_topk < 0)
+        return 0;
+    const int m_out = (max_topk > 0 && max_topk < M) ? max_topk : M;
+    const int64_t ks[3] = {0, 0, 0};
+    if (m_out <= kStreamMaxTopk && score_pipe_ok(score_block_size, fta::kernel_head_dim(D), ks))
+        return stream_min_bytes(B, H, N, M);
+    return full_bytes(B, H, N, M);
 }
 
 }  // extern "C"
 
 namespace {
-// fta_topk_score's workspace as candidate streams: entries, per-wave counts,
-// row totals, tau keys (in that order).
-StreamBufs stream_layout(void* workspace, int B, int H, int N, int M, int m_out, float** row_lse) {
-    const size_t w = (size_t)stream_waves(B, H, N);
+// fta_topk_score's workspace as candidate streams (StreamBufs), in this order:
+// per-wave counts, chunk tables, counters, fallback tile list, row totals, tau
+// keys, fallback slots, chunk pool (the rest of the workspace).
+StreamBufs stream_layout(void* workspace, size_t workspace_bytes, int B, int H, int N, int M, int m_out,
+                         float** row_lse) {
+    const StreamGeo g = stream_geo(B, H, N, M);
+    const size_t rows = (size_t)B * H * N;
     char* p = (char*)workspace;
     StreamBufs sb;
-    sb.cand = (uint2*)p;
-    p += fta::align_up(w * 64 * M * sizeof(uint2));
     sb.count = (int*)p;
-    p += fta::align_up(w * sizeof(int));
+    p += fta::align_up(g.waves * sizeof(int));
+    sb.tab = (int*)p;
+    p += fta::align_up(g.waves * g.maxch * sizeof(int));
+    sb.ctrs = (int*)p;
+    p += fta::align_up(4 * sizeof(int));
+    sb.ovf_list = (int*)p;
+    p += fta::align_up(g.tiles * sizeof(int));
     *row_lse = (float*)p;
-    p += fta::align_up((size_t)B * H * N * sizeof(float));
+    p += fta::align_up(rows * sizeof(float));
     sb.tau_key = (float*)p;
-    sb.ngroups = (m_out + 1) / 2;
+    p += fta::align_up(rows * sizeof(float));
+    sb.slots = (float*)p;
+    p += fta::align_up((size_t)kStreamSlots * 256 * M * sizeof(float));
+    sb.pool = (uint2*)p;
+    const size_t pool_bytes = workspace_bytes - (size_t)(p - (char*)workspace);
+    const int64_t chunks = (int64_t)(pool_bytes / kChunkBytes);
+    sb.pool_chunks = (int)(chunks < (int64_t)0x7fffffff ? chunks : (int64_t)0x7fffffff);
+    sb.maxch = g.maxch;
+    sb.m_out = m_out;
     return sb;
 }
 
-// The selector over the candidate streams of stream_layout (fta_topk_stream_kernel).
-int launch_stream_select(const StreamBufs& sb, const float* row_lse, int B, int H, int N, int M, int m_out, int bsz,
-                         int pad_head, int pad_tail, float threshold, int32_t* idx, float* raw, float* avg,
-                         hipStream_t s) {
-    const int qtiles = (N + 255) / 256;
+// The selector over the candidate streams (fta_topk_stream_kernel), then the
+// fallback kernel for tiles whose streams ran out of pool (it returns at once
+// when there are none).
+template <int DT>
+int launch_stream_select_dt(const ScoreArgs& sa, int Dk, const StreamBufs& sb, int m_out, float threshold,
+                            int32_t* idx, float* raw, float* avg, hipStream_t s) {
+    const int qtiles = sa.qtiles;
 #define FTA_LAUNCH_STREAM(KB)                                                                                     \
-    hipLaunchKernelGGL(fta_topk_stream_kernel<KB>, dim3((unsigned)(B * H * qtiles)), dim3(256), 0, s, sb.cand, \
-                       sb.count, sb.tau_key, row_lse, N, qtiles, M, m_out, bsz, pad_head, pad_tail, threshold, idx, \
-                       raw, avg)
+    hipLaunchKernelGGL(fta_topk_stream_kernel<KB>, dim3((unsigned)sa.total), dim3(256), 0, s, sb.pool, sb.count, \
+                       sb.tab, sb.maxch, sb.tau_key, sa.row_lse, sa.N, qtiles, sa.M, m_out, sa.bsz, sa.pad_head,  \
+                       sa.pad_tail, threshold, idx, raw, avg, sb.ovf_list, sb.ctrs + 1)
     if (m_out <= 8)
         FTA_LAUNCH_STREAM(8);
-    else
+    else if (m_out <= 16)
         FTA_LAUNCH_STREAM(16);
+    else
+        FTA_LAUNCH_STREAM(32);
 #undef FTA_LAUNCH_STREAM
-    return fta::check_launch("fta_topk_stream_kernel");
+    int rc = fta::check_launch("fta_topk_stream_kernel");
+    if (rc != FTA_OK) return rc;
+    const int grid = sa.total < kStreamSlots ? sa.total : kStreamSlots;
+    if (Dk == 64)
+        hipLaunchKernelGGL((fta_stream_fallback_kernel<DT, 64, 32>), dim3(grid), dim3(256), 0, s, sa, sb.ovf_list,
+                           sb.ctrs + 1, sb.slots, m_out, threshold, idx, raw, avg);
+    else
+        hipLaunchKernelGGL((fta_stream_fallback_kernel<DT, 128, 32>), dim3(grid), dim3(256), 0, s, sa, sb.ovf_list,
+                           sb.ctrs + 1, sb.slots, m_out, threshold, idx, raw, avg);
+    return fta::check_launch("fta_stream_fallback_kernel");
 }
 
-// Shared checks of fta_topk_score and fta_topk_score_candidates; sets M and m_out.
+// Shared checks of the fta_topk_score entry points; sets M, m_out and whether
+// the candidate-stream path applies, and checks the workspace for that path.
 int topk_score_checks(int B, int H, int N, int D, int bsz, int pad_head, int pad_tail, int max_topk,
-                      size_t workspace_bytes, int* M, int* m_out) {
+                      const int64_t* k_strides, size_t workspace_bytes, int* M, int* m_out, bool* streams) {
     int st = fta::check_score_args(B, H, N, D, bsz, pad_head, pad_tail, M);
     if (st != FTA_OK) return st;
     if (*M > 4096) return fta::unsupported("topk_score: M exceeds 4096");
     if (max_topk < 0) return fta::arg_error("topk_score: max_topk must be >= 0");
-    if (workspace_bytes < fta_topk_score_workspace_size(B, H, N, *M))
-        return fta::arg_error("topk_score: workspace too small");
     *m_out = (max_topk > 0 && max_topk < *M) ? max_topk : *M;
+    *streams = *m_out <= kStreamMaxTopk && score_pipe_ok(bsz, fta::kernel_head_dim(D), k_strides);
+    const size_t need = *streams ? stream_min_bytes(B, H, N, *M) : full_bytes(B, H, N, *M);
+    if (workspace_bytes < need)
+        return fta::arg_error("topk_score: workspace too small (see fta_topk_score_workspace_size_ex)");
     return FTA_OK;
+}
+
+int stream_select(const void* q, const void* k, int dtype, int B, int H, int N, int D, const int64_t* qs,
+                  const int64_t* ks, int bsz, int pad_head, int pad_tail, float scale, int M, int m_out,
+                  float threshold, int32_t* idx, float* raw, float* avg, void* workspace, size_t workspace_bytes,
+                  hipStream_t s) {
+    float* row_lse = nullptr;
+    const StreamBufs sb = stream_layout(workspace, workspace_bytes, B, H, N, M, m_out, &row_lse);
+    const ScoreArgs sa =
+        score_args(q, k, B, H, N, D, qs, ks, M, bsz, pad_head, pad_tail, scale, nullptr, row_lse, 0, nullptr, sb);
+    const int Dk = fta::kernel_head_dim(D);
+    if (dtype == FTA_DTYPE_BF16)
+        return launch_stream_select_dt<FTA_DTYPE_BF16>(sa, Dk, sb, m_out, threshold, idx, raw, avg, s);
+    if (dtype == FTA_DTYPE_F16)
+        return launch_stream_select_dt<FTA_DTYPE_F16>(sa, Dk, sb, m_out, threshold, idx, raw, avg, s);
+    return fta::arg_error("topk_score: dtype must be bf16 or fp16");
 }
 }  // namespace
 
@@ -1735,32 +2125,36 @@ int fta_topk_score_candidates(const void* q, const void* k, int dtype, int B, in
                               void* stream) {
     FTA_TRY_BEGIN
     int M = 0, m_out = 0;
-    int st = topk_score_checks(B, H, N, D, score_block_size, pad_head, pad_tail, max_topk, workspace_bytes, &M, &m_out);
+    bool streams = false;
+    int st = topk_score_checks(B, H, N, D, score_block_size, pad_head, pad_tail, max_topk, k_strides,
+                               workspace_bytes, &M, &m_out, &streams);
     if (st != FTA_OK) return st;
-    if (!(m_out <= kStreamMaxTopk && score_pipe_ok(score_block_size, fta::kernel_head_dim(D), k_strides)))
-        return fta::unsupported("topk_score_candidates: needs b = 64, D <= 128 and at most 16 blocks per query");
+    if (!streams)
+        return fta::unsupported("topk_score_candidates: needs b = 64, D <= 128 and at most 32 blocks per query");
     float* row_lse = nullptr;
-    const StreamBufs sb = stream_layout(workspace, B, H, N, M, m_out, &row_lse);
+    const StreamBufs sb = stream_layout(workspace, workspace_bytes, B, H, N, M, m_out, &row_lse);
     return launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, pad_tail,
                             scale, nullptr, row_lse, 0, nullptr, (hipStream_t)stream, sb);
     FTA_TRY_END
 }
 
-int fta_topk_select_candidates(int B, int H, int N, int D, const int64_t* k_strides, int score_block_size,
-                               int pad_head, int pad_tail, int max_topk, float threshold, int32_t* topk_indices,
-                               float* topk_raw, float* topk_avg, void* workspace, size_t workspace_bytes,
-                               void* stream) {
+int fta_topk_select_candidates(const void* q, const void* k, int dtype, int B, int H, int N, int D,
+                               const int64_t* q_strides, const int64_t* k_strides, int score_block_size,
+                               int pad_head, int pad_tail, float scale, int max_topk, float threshold,
+                               int32_t* topk_indices, float* topk_raw, float* topk_avg, void* workspace,
+                               size_t workspace_bytes, void* stream) {
     FTA_TRY_BEGIN
     int M = 0, m_out = 0;
-    int st = topk_score_checks(B, H, N, D, score_block_size, pad_head, pad_tail, max_topk, workspace_bytes, &M, &m_out);
+    bool streams = false;
+    int st = topk_score_checks(B, H, N, D, score_block_size, pad_head, pad_tail, max_topk, k_strides,
+                               workspace_bytes, &M, &m_out, &streams);
     if (st != FTA_OK) return st;
-    if (!(m_out <= kStreamMaxTopk && score_pipe_ok(score_block_size, fta::kernel_head_dim(D), k_strides)))
-        return fta::unsupported("topk_select_candidates: needs b = 64, D <= 128 and at most 16 blocks per query");
+    if (!streams)
+        return fta::unsupported("topk_select_candidates: needs b = 64, D <= 128 and at most 32 blocks per query");
     if (!topk_indices || !topk_raw || !topk_avg) return fta::arg_error("topk_select_candidates: null pointer");
-    float* row_lse = nullptr;
-    const StreamBufs sb = stream_layout(workspace, B, H, N, M, m_out, &row_lse);
-    return launch_stream_select(sb, row_lse, B, H, N, M, m_out, score_block_size, pad_head, pad_tail, threshold,
-                                topk_indices, topk_raw, topk_avg, (hipStream_t)stream);
+    return stream_select(q, k, dtype, B, H, N, D, q_strides, k_strides, score_block_size, pad_head, pad_tail, scale,
+                         M, m_out, threshold, topk_indices, topk_raw, topk_avg, workspace, workspace_bytes,
+                         (hipStream_t)stream);
     FTA_TRY_END
 }
 
@@ -1770,18 +2164,21 @@ int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N,
                    void* workspace, size_t workspace_bytes, void* stream) {
     FTA_TRY_BEGIN
     int M = 0, m_out = 0;
-    int st = topk_score_checks(B, H, N, D, score_block_size, pad_head, pad_tail, max_topk, workspace_bytes, &M, &m_out);
+    bool streams = false;
+    int st = topk_score_checks(B, H, N, D, score_block_size, pad_head, pad_tail, max_topk, k_strides,
+                               workspace_bytes, &M, &m_out, &streams);
     if (st != FTA_OK) return st;
     hipStream_t s = (hipStream_t)stream;
-    if (m_out <= kStreamMaxTopk && score_pipe_ok(score_block_size, fta::kernel_head_dim(D), k_strides)) {
+    if (streams) {
         // candidate streams: no [BH][M][N] intermediate
         float* row_lse = nullptr;
-        const StreamBufs sb = stream_layout(workspace, B, H, N, M, m_out, &row_lse);
+        const StreamBufs sb = stream_layout(workspace, workspace_bytes, B, H, N, M, m_out, &row_lse);
         st = launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, pad_tail,
                               scale, nullptr, row_lse, 0, nullptr, s, sb);
         if (st != FTA_OK) return st;
-        return launch_stream_select(sb, row_lse, B, H, N, M, m_out, score_block_size, pad_head, pad_tail, threshold,
-                                    topk_indices, topk_raw, topk_avg, s);
+        return stream_select(q, k, dtype, B, H, N, D, q_strides, k_strides, score_block_size, pad_head, pad_tail,
+                             scale, M, m_out, threshold, topk_indices, topk_raw, topk_avg, workspace, workspace_bytes,
+                             s);
     }
     float* blk_lse = (float*)workspace;
     float* row_lse = (float*)((char*)workspace + fta::align_up((size_t)B * H * M * N * sizeof(float)));

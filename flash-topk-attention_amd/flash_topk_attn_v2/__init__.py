@@ -36,8 +36,9 @@ def flash_topk_score(
     Returns ``(topk_indices int32, topk_raw_scores f32, topk_avg_scores f32)``,
     each ``[B, H, N, min(topk, M)]`` (``M`` when ``topk == 0``).  Scoring and
     selection run in one C call: the normalised ``[B, H, N, M]`` scores are
-    never formed; the selector reads the scorer's per-block log2-sums from a
-    workspace.
+    never formed; for b = 64, D <= 128 and topk <= 32 the selector reads the
+    scorer's candidate streams (bounded workspace), otherwise its per-block
+    log2-sums.
     """
     input_4d = q.ndim == 4
     if input_4d:
@@ -65,7 +66,8 @@ def flash_topk_score(
     raw = torch.empty(B, H, N, m_out, device=dev, dtype=torch.float32)
     avg = torch.empty(B, H, N, m_out, device=dev, dtype=torch.float32)
     L = _lib.lib()
-    ws = _lib.workspace(L.fta_topk_score_workspace_size(B, H, N, M), dev)
+    ws = _lib.workspace(L.fta_topk_score_workspace_size_ex(B, H, N, Dp, score_block_size, pad_head, pad_tail, topk),
+                        dev)
     rc = L.fta_topk_score(
         _lib.ptr(qq), _lib.ptr(kk), _lib.dtype_code(qq.dtype), B, H, N, Dp, _lib.i64arr(qs), _lib.i64arr(ks),
         score_block_size, pad_head, pad_tail, float(D ** -0.5), topk, float(threshold),

@@ -41,7 +41,10 @@ _SIGNATURES = {
     "fta_topk_score": (_i, [_p, _p, _i, _i, _i, _i, _i, _i64p, _i64p, _i, _i, _i, _f, _i, _f, _p, _p, _p, _p,
                             _sz, _p]),
     "fta_topk_score_candidates": (_i, [_p, _p, _i, _i, _i, _i, _i, _i64p, _i64p, _i, _i, _i, _f, _i, _p, _sz, _p]),
-    "fta_topk_select_candidates": (_i, [_i, _i, _i, _i, _i64p, _i, _i, _i, _i, _f, _p, _p, _p, _p, _sz, _p]),
+    "fta_topk_select_candidates": (_i, [_p, _p, _i, _i, _i, _i, _i, _i64p, _i64p, _i, _i, _i, _f, _i, _f, _p, _p,
+                                        _p, _p, _sz, _p]),
+    "fta_topk_score_workspace_size_ex": (_sz, [_i] * 8),
+    "fta_topk_score_workspace_min": (_sz, [_i] * 8),
     "fta_qblock_merge": (_i, [_p, _p, _i64, _i, _i, _i, _i, _p, _p, _p, _p]),
     "fta_qblock_merge_maxid": (_i, [_p, _p, _i64, _i, _i, _p, _i, _p, _p, _p, _p]),
     "fta_qblock_union": (_i, [_p, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p]),

@@ -94,7 +94,30 @@ int fta_topk_select(const float* block_scores, int64_t rows, int M, int64_t stri
                     float threshold, int32_t* topk_indices, float* topk_raw, float* topk_avg,
                     void* stream);
 
+/*
+ * Workspace of fta_topk_score.  fta_topk_score_workspace_size covers every
+ * path (any head dim, block size and max_topk); fta_topk_score_workspace_size_ex
+ * returns the recommended size for one call's geometry (0 for an invalid one),
+ * assuming a K token stride of at most 2^24 elements.
+ *
+ * b = 64, D <= 128 (rounded to 64 / 128) and at most 32 blocks per query run
+ * on candidate streams: chunks of 1024 entries taken from a pool in the
+ * workspace, one chunk per 64 queries plus a shared remainder, sized for the
+ * expected number of entries (m_out (1 + 2 ln(M / m_out)) per query; 1.17e9
+ * bytes at B1 H32 N32768 b64 top-16, against 2.15e9 for the per-block values
+ * and 4.3e9 before the pool).  Any workspace of at least
+ * fta_topk_score_workspace_min bytes (one chunk per 64 queries plus the fixed
+ * parts) is accepted: the 256-query tiles whose streams do not fit are scored
+ * and selected again by a fallback kernel (same results, more time).  Other
+ * geometries store the [B][H][M][N] per-block values.
+ */
 size_t fta_topk_score_workspace_size(int B, int H, int N, int M);
+size_t fta_topk_score_workspace_size_ex(int B, int H, int N, int D, int score_block_size, int pad_head,
+                                        int pad_tail, int max_topk);
+/* The least workspace fta_topk_score accepts for that geometry (the stream
+ * path then holds one chunk per 64 queries and scores the rest again). */
+size_t fta_topk_score_workspace_min(int B, int H, int N, int D, int score_block_size, int pad_head, int pad_tail,
+                                    int max_topk);
 
 /*
  * Fused scoring + selection: the result of fta_block_score followed by
@@ -110,7 +133,7 @@ int fta_topk_score(const void* q, const void* k, int dtype, int B, int H, int N,
 
 /*
  * Stage 1 of fta_topk_score alone, on its candidate-stream path (b = 64,
- * D <= 128, at most 16 blocks per query; FTA_ERR_UNSUPPORTED otherwise): the
+ * D <= 128, at most 32 blocks per query; FTA_ERR_UNSUPPORTED otherwise): the
  * scoring kernel writes, into the workspace, per-wave candidate streams of the
  * blocks that can still be in a query's top-k, the row totals and the bound
  * the selector starts from.  Exposed so that the scoring kernel can be timed
@@ -128,15 +151,18 @@ int fta_topk_score_candidates(const void* q, const void* k, int dtype, int B, in
 /*
  * Stage 2 of fta_topk_score alone: the top-k selection (with the threshold
  * cut) over the candidate streams that fta_topk_score_candidates left in
- * `workspace` for the same geometry and max_topk.  k_strides and D only decide
- * (as in fta_topk_score) whether the stream path applies; FTA_ERR_UNSUPPORTED
- * otherwise.  fta_topk_score_candidates followed by this call gives the same
- * outputs as fta_topk_score.  Stands for the reference's top-k stage
- * (topk_select_launch, flash_topk_attn_v2/csrc/topk_select.cpp, as called from
+ * `workspace` for the same inputs, geometry and max_topk, including the
+ * fallback for tiles whose streams ran out of pool (which scores those tiles
+ * again, so q and k are needed).  Same arguments as fta_topk_score;
+ * FTA_ERR_UNSUPPORTED where fta_topk_score_candidates is.
+ * fta_topk_score_candidates followed by this call gives the same outputs as
+ * fta_topk_score.  Stands for the reference's top-k stage (topk_select_launch,
+ * flash_topk_attn_v2/csrc/topk_select.cpp, as called from
  * flash_topk_attn_v2/topk_select.py:185-311).
  */
-int fta_topk_select_candidates(int B, int H, int N, int D, const int64_t* k_strides, int score_block_size,
-                               int pad_head, int pad_tail, int max_topk, float threshold,
+int fta_topk_select_candidates(const void* q, const void* k, int dtype, int B, int H, int N, int D,
+                               const int64_t* q_strides, const int64_t* k_strides, int score_block_size,
+                               int pad_head, int pad_tail, float scale, int max_topk, float threshold,
                                int32_t* topk_indices, float* topk_raw, float* topk_avg, void* workspace,
                                size_t workspace_bytes, void* stream);
 

@@ -644,12 +644,18 @@ STREAM_CASES = [
     (8192, 2, 128, (0, 0), 1, 1.0, "peaked"),
     (8192, 2, 64, (0, 0), 16, 0.9, "peaked"),
     (8160, 2, 128, (10, 22), 12, 0.8, "increasing"),
+    # 17 to 32 blocks per query: eight groups of four fp16 keys
+    (4096, 2, 128, (0, 0), 32, 1.0, "increasing"),
+    (4096, 1, 64, (0, 0), 24, 0.9, "ties"),
+    (8192, 2, 128, (0, 0), 32, 0.9, "peaked"),
+    (1000, 2, 64, (30, 58), 20, 1.0, "iid"),
+    (4096, 2, 64, (0, 0), 17, 1.0, "decreasing"),
 ]
 
 
 @pytest.mark.parametrize("case", STREAM_CASES, ids=lambda c: f"N{c[0]}D{c[2]}k{c[4]}{c[6]}p{c[3][0]}")
 def test_topk_candidate_streams_exact(case):
-    """The pipelined scorer's candidate streams (b = 64, top-k <= 16) drop a
+    """The pipelined scorer's candidate streams (b = 64, top-k <= 32) drop a
     block only when enough earlier blocks rank above it: the fused result
     equals the selection over the full score tensor bit for bit, including
     adversarial block orders (every block a new maximum), exact ties and
@@ -667,6 +673,58 @@ def test_topk_candidate_streams_exact(case):
     if pattern == "increasing" and pad == (0, 0):
         M = N // 64
         assert (ri[..., 0] == M - 1).all()
+
+
+@pytest.mark.parametrize("pattern,topk,D,extra_chunks", [
+    ("increasing", 16, 128, 0),     # every block enters every stream: all tiles overflow
+    ("increasing", 16, 128, 300),   # spare chunks for part of the waves: some tiles fit, others overflow
+    ("iid", 32, 64, 0),
+    ("ties", 8, 128, 5),
+])
+def test_topk_stream_pool_overflow_fallback(pattern, topk, D, extra_chunks):
+    """Candidate streams share a pool sized by the workspace; tiles whose
+    streams do not fit are scored and selected again by the fallback kernel.
+    With the least workspace the library accepts (one 1024-entry chunk per 64
+    queries, plus `extra_chunks`) the adversarial orders overflow, and the
+    results must still equal the selection over the full score tensor bit for
+    bit, through fta_topk_score and through the two-stage entry points."""
+    from flash_topk_attn_v2 import _lib
+
+    N, H, pad, thr = 4096, 2, (0, 0), 1.0 if pattern != "iid" else 0.9
+    say(f"[stream overflow] {pattern} topk{topk} D{D} extra{extra_chunks}")
+    q, k = _pattern_qk(N, H, D, pattern, 33)
+    scores = fta.flash_block_score(q, k, H, 64, pad)
+    ri, rr, ra = O.topk_select(scores.cpu().numpy(), thr, topk, 64, pad)
+    L = _lib.lib()
+    nmin = L.fta_topk_score_workspace_min(1, H, N, D, 64, 0, 0, topk)
+    assert 0 < nmin < L.fta_topk_score_workspace_size_ex(1, H, N, D, 64, 0, 0, topk)
+    ws = torch.empty(nmin + extra_chunks * 8192, dtype=torch.uint8, device="cuda")
+    st = _lib.i64arr([N * H * D, D, H * D])
+    stream = torch.cuda.current_stream().cuda_stream
+    for two_stage in (False, True):
+        out = [torch.full((1, H, N, topk), 7, dtype=torch.int32, device="cuda"),
+               torch.zeros(1, H, N, topk, device="cuda"), torch.zeros(1, H, N, topk, device="cuda")]
+        optr = [o.data_ptr() for o in out]
+        if two_stage:
+            rc = L.fta_topk_score_candidates(q.data_ptr(), k.data_ptr(), 0, 1, H, N, D, st, st, 64, 0, 0,
+                                             D ** -0.5, topk, ws.data_ptr(), ws.numel(), stream)
+            _lib.check(rc, "fta_topk_score_candidates")
+            counts = ws[: (N // 256) * 4 * H * 4].view(torch.int32).clone()
+            rc = L.fta_topk_select_candidates(q.data_ptr(), k.data_ptr(), 0, 1, H, N, D, st, st, 64, 0, 0,
+                                              D ** -0.5, topk, thr, *optr, ws.data_ptr(), ws.numel(), stream)
+            _lib.check(rc, "fta_topk_select_candidates")
+        else:
+            rc = L.fta_topk_score(q.data_ptr(), k.data_ptr(), 0, 1, H, N, D, st, st, 64, 0, 0, D ** -0.5, topk,
+                                  thr, *optr, ws.data_ptr(), ws.numel(), stream)
+            _lib.check(rc, "fta_topk_score")
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out[0].cpu().numpy(), ri)
+        np.testing.assert_array_equal(out[1].cpu().numpy(), rr)
+        np.testing.assert_array_equal(out[2].cpu().numpy(), ra)
+    if pattern == "increasing":
+        assert (counts < 0).any(), "the least workspace should overflow on this input"
+        if extra_chunks:
+            assert (counts >= 0).any(), "spare chunks should let some waves finish"
 
 
 @pytest.mark.parametrize("D", [64, 128])
