@@ -126,21 +126,29 @@ __device__ __forceinline__ uint4 fta_tr_frag(const uint16_t* tile, int row, int 
 // be padded.  Rows of QSEG 16-byte slots are stored unpadded with slot j of
 // row r at position j ^ x(r); the loading lane picks its global source from its
 // physical position, the reading lane swizzles its address.
-// x(r) is chosen from measured gfx950 LDS bank behaviour (SQ_LDS_BANK_CONFLICT):
-//  * 16-byte reads (MFMA operand rows) are served 8 lanes at a time over 128
-//    bytes: 8 consecutive rows reading one logical slot need distinct x mod 8;
+// x(r) is chosen from measured gfx950 LDS bank behaviour (64 banks of 4 bytes,
+// SQ_LDS_BANK_CONFLICT):
+//  * 16-byte reads (MFMA operand rows, lane = row) are served 16 lanes at a
+//    time over 256 bytes: 16 consecutive rows reading one logical slot need
+//    16 distinct bank positions, i.e. x bijective on r & 15 for rows of 256
+//    bytes or more (an x built from r & 7 alone left rows r and r + 8 on the
+//    same banks: a 2-way conflict on every operand read, 6.8e8 conflict cycles
+//    per C3-iid sparse forward, 5.5e8 per C3 scoring launch);
 //  * ds_read_b64_tr_b16 is served 32 lanes at a time over 256 bytes: 4
 //    consecutive rows x 64 bytes, so bits 2..3 of x must differ across them.
-// Both hold for the x below with 16 or more slots per row (conflict-free),
-// and for 8 slots with the row-pair form; 4 slots need none.  12 and 20 slots
-// use r & 3 (not tuned).
+// x(r) = (r & 3) << 2 | (r >> 2) & 3 meets both for 16 or more slots per row
+// (V = 1 keeps the earlier 8-row form, which one kernel measured faster with);
+// 8 slots (128-byte rows, two rows per bank line) use the row-pair form; 4
+// slots need none.  12 and 20 slots use r & 3 (not tuned).
 // ---------------------------------------------------------------------------
-template <int QSEG>
+template <int QSEG, int V = 0>
 struct FtaSwz {
     static_assert(QSEG % 4 == 0, "rows must be a multiple of 4 slots");
     __device__ static __forceinline__ int x(int r) {
-        if constexpr (QSEG % 16 == 0) {
+        if constexpr (QSEG % 16 == 0 && V == 1) {
             return ((r & 1) << 2) | (((r >> 1) & 1) * 10) | ((r >> 2) & 1);
+        } else if constexpr (QSEG % 16 == 0) {
+            return ((r & 3) << 2) | ((r >> 2) & 3);
         } else if constexpr (QSEG == 8) {
             const int h = (r >> 1) & 7;
             return ((h & 1) << 2) | (h >> 1);
@@ -157,13 +165,13 @@ struct FtaSwz {
 };
 
 // fta_tr_frag over a swizzled tile of QSEG slots per row.
-template <int QSEG>
+template <int QSEG, int V = 0>
 __device__ __forceinline__ uint4 fta_tr_frag_sw(const uint16_t* tile, int k0, int n0, int lane) {
     const int g = lane >> 4, i = lane & 15;
     const int r = k0 + 4 * (g >> 1) + (i >> 2);
     const int col = n0 + 16 * (g & 1) + 4 * (i & 3);
-    const uint16_t* p0 = tile + FtaSwz<QSEG>::off(r, col >> 3) + (col & 7);
-    const uint16_t* p1 = tile + FtaSwz<QSEG>::off(r + 8, col >> 3) + (col & 7);
+    const uint16_t* p0 = tile + FtaSwz<QSEG, V>::off(r, col >> 3) + (col & 7);
+    const uint16_t* p1 = tile + FtaSwz<QSEG, V>::off(r + 8, col >> 3) + (col & 7);
     const fta_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (fta_lds_s16x4*)(__attribute__((address_space(3))) uint16_t*)p0);
     const fta_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
