@@ -33,7 +33,7 @@ PEAK_HBM_GBS = 8000.0
 # device copy (`--only copy`: FETCH_SIZE x2.0, WRITE_SIZE x1.0).  A PMC pass
 # cannot run inside this process, so this is the last measured figure; it is
 # refreshed whenever the kernel changes.
-SCORE_FETCH_KIB, SCORE_WRITE_KIB = 6.533e5, 9.585e5
+SCORE_FETCH_KIB, SCORE_WRITE_KIB = 6.517e5, 7.793e5
 SCORE_TRAFFIC_BYTES = int((2.0 * SCORE_FETCH_KIB + 1.0 * SCORE_WRITE_KIB) * 1024)
 
 

@@ -426,12 +426,14 @@ __global__ __launch_bounds__(256) void fta_argsort_desc_rows_kernel(const int32_
 // receives the head's total (selections plus one setup step per block) for
 // fta_head_balance_kernel.
 __global__ __launch_bounds__(256) void fta_kv_order_kernel(const uint32_t* __restrict__ sel, int M, int QW, int H,
-                                                           int G, int32_t* __restrict__ order,
+                                                           int G, int slice_blocks, int32_t* __restrict__ order,
                                                            int32_t* __restrict__ head_work) {
     // WG (b, K/V head, slice): counts every block's selections (coalesced reads
     // of the bitmap rows, LDS atomics), then ranks the blocks of its slice of
-    // 1024 (four per thread).  Each slice reads the head's whole bitmap, so up to
-    // 1024 blocks one WG per head reads it once.
+    // slice_blocks (256 or 1024: one to four per thread).  Each slice reads the
+    // head's whole bitmap: small heads rank in slices of 256 (the ranking, O(M)
+    // per block, dominates), heads of more than 1024 blocks in slices of 1024
+    // (four times fewer bitmap re-reads).
     __shared__ uint32_t key[4096];
     __shared__ int s_work;
     const int64_t rk = blockIdx.x;               // (b, K/V head)
@@ -457,9 +459,8 @@ __global__ __launch_bounds__(256) void fta_kv_order_kernel(const uint32_t* __res
     atomicAdd(&s_work, cw);
     __syncthreads();
     if (slice == 0 && threadIdx.x == 0) head_work[rk] = s_work;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = slice * 1024 + u * 256 + threadIdx.x;
+    for (int u = 0; u < slice_blocks / 256; ++u) {
+        const int i = slice * slice_blocks + u * 256 + threadIdx.x;
         if (i < M) {
             const uint32_t ki = key[i];
             int rank = 0;
@@ -722,8 +723,9 @@ int launch_sel_bitmap(const int32_t* merged, int BH, int QM, int W, int M, uint3
 int launch_kv_order(const uint32_t* sel, int B, int H, int Hk, int M, int QW, int32_t* order, int32_t* head_work,
                     int32_t* head_perm, hipStream_t st) {
     if (M <= 0 || B * Hk == 0) return FTA_OK;
-    hipLaunchKernelGGL(fta_kv_order_kernel, dim3((unsigned)(B * Hk), (unsigned)((M + 1023) / 1024)), dim3(256), 0, st,
-                       sel, M, QW, H, H / Hk, order, head_work);
+    const int slice = (M > 1024) ? 1024 : 256;
+    hipLaunchKernelGGL(fta_kv_order_kernel, dim3((unsigned)(B * Hk), (unsigned)((M + slice - 1) / slice)), dim3(256), 0,
+                       st, sel, M, QW, H, H / Hk, slice, order, head_work);
     int rc = check_launch("fta_kv_order_kernel");
     if (rc != FTA_OK) return rc;
     hipLaunchKernelGGL(fta_head_balance_kernel, dim3(1), dim3(256), 0, st, head_work, nullptr, 0, 0, 1, B * Hk,
