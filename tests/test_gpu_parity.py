@@ -610,7 +610,10 @@ def _pattern_qk(N, H, D, pattern, seed):
     """q, k [1, N, H*D] bf16 whose block scores follow `pattern` over the blocks:
     'increasing' / 'decreasing' (every block beats / loses to all earlier ones),
     'ties' (all 64-key blocks identical, so every block score is exactly equal),
-    'peaked' (config 3's block-centred data) or 'iid'."""
+    'peaked' (config 3's block-centred data), 'iid', or 'jump' (blocks 5 and
+    M - 3 score 130+ log2 units above everything before them, so their exp sums
+    overflow the scorer's running reference: in the candidate-stream scorer the
+    tile is scored again by the fallback kernel's exact path)."""
     g = torch.Generator(device="cpu").manual_seed(seed)
     C = H * D
     if pattern == "peaked":
@@ -621,6 +624,13 @@ def _pattern_qk(N, H, D, pattern, seed):
         q = 0.3 * torch.randn(1, N, C, generator=g) + torch.gather(cent, 1, pick.unsqueeze(-1).expand(1, N, C))
     elif pattern == "iid":
         q, k = torch.randn(1, N, C, generator=g), torch.randn(1, N, C, generator=g)
+    elif pattern == "jump":
+        u = torch.randn(1, 1, C, generator=g)
+        q = u + 0.1 * torch.randn(1, N, C, generator=g)
+        k = 0.5 * torch.randn(1, N, C, generator=g)
+        M = N // 64
+        for j in (5, M - 3):
+            k[:, j * 64:(j + 1) * 64] = 12.0 * u + 0.1 * torch.randn(1, 64, C, generator=g)
     else:
         u = torch.randn(1, 1, C, generator=g)
         q = u + 0.1 * torch.randn(1, N, C, generator=g)
@@ -650,6 +660,9 @@ STREAM_CASES = [
     (8192, 2, 128, (0, 0), 32, 0.9, "peaked"),
     (1000, 2, 64, (30, 58), 20, 1.0, "iid"),
     (4096, 2, 64, (0, 0), 17, 1.0, "decreasing"),
+    # reference overflow inside the unrolled block loop: the tile goes through the fallback
+    (4096, 2, 128, (0, 0), 16, 1.0, "jump"),
+    (4096, 1, 64, (0, 0), 32, 0.9, "jump"),
 ]
 
 
