@@ -256,7 +256,7 @@ class Pipeline:
         geo = (B, H, N, D, g, b, qpad[0], qpad[1], pad[0], pad[1])
         self.ws_bwd = _lib.workspace(L.fta_sparse_attn_bwd_workspace_size(*geo), dev)
         self.dq, self.dk, self.dv = (torch.empty_like(self.q) for _ in range(3))
-        self.streams_ok = b == 64 and D in (64, 128) and m_out <= 32
+        self.streams_ok = b in (64, 128) and D in (64, 128) and m_out <= 32
         shp = (B, H, N, m_out)
         self.sel_out = (torch.empty(shp, dtype=torch.int32, device=dev), torch.empty(shp, device=dev),
                         torch.empty(shp, device=dev))

@@ -506,16 +506,17 @@ struct ScorePipeShape {
     static_assert(SLOTS % 256 == 0, "whole DMA instructions per wave");
 };
 
-// Candidate streams (template NG > 0, top-k lists of at most 16 blocks):
+// Candidate streams (template NG > 0, top-k lists of at most 32 blocks):
 // instead of the [BH][M][N] per-block values, each wave appends, per block, an
 // entry (value, lane << 16 | m) for every query of the wave for which the block
-// can still be in the top-k, compacted in lane order (cand[wave][...]); the
-// wave's entry count goes to cand_count[wave].  A block is dropped for a query
-// when at least m_out earlier blocks rank strictly above it: each query keeps,
-// in LDS, the two largest ranking keys (block value + log2(b / valid count)) of
-// NG interleaved block groups (m mod NG, NG = 4 for m_out <= 8, else 8); the
-// smallest second largest over the groups bounds 2 NG >= m_out earlier blocks
-// from below.  The bound is refreshed once per NG blocks and lowered by a
+// can still be in the top-k, compacted in lane order into the wave's chunks of
+// the pool; the wave's entry count goes to count[wave].  A block is dropped for
+// a query when at least m_out earlier blocks rank strictly above it: each query
+// keeps, in LDS, the GT largest ranking keys (block value + log2(b / valid
+// count)) of NG interleaved block groups (m mod NG; NG x GT = 4 x 2 for m_out
+// <= 8, 4 x 4 for <= 16, 8 x 4 in fp16 for <= 32); the smallest kept key over
+// the groups bounds NG GT >= m_out earlier blocks from below.  The bound is
+// refreshed once per NG blocks and lowered by a
 // margin far above fp32 exp2 / log2 rounding, and partial edge blocks always
 // pass, so the final selection over the streams equals the one over all
 // blocks.  tau_key[row] receives the final bound (at least m_out blocks rank
@@ -577,7 +578,12 @@ __device__ __forceinline__ uint32_t fta_f2h2(float lo, float hi) {
            ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
 }
 
-template <int DT, int D, int NG, int GT = 2, bool GH = false>
+// SB = 64-key LDS chunks per score block: 1 (b = 64) or 2 (b = 128).  The
+// pipeline runs over chunks u (keys u * 64 - pad_head ...); a block's value is
+// formed at its last chunk from the chunk totals, all taken against the row's
+// running reference R (an exact-path re-reference inside a block rescales the
+// block's earlier chunks, as it rescales the row total).
+template <int DT, int D, int NG, int GT = 2, bool GH = false, int SB = 1>
 __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg) {
     const uint16_t* __restrict__ q = a.q;
     const uint16_t* __restrict__ k = a.k;
@@ -595,6 +601,7 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
     __shared__ __align__(1024) unsigned char sK[NBUF][Sh::BUF_B];
     static_assert(GT == 2 || GT == 4, "group top-2 or top-4");
     static_assert(!GH || GT == 4, "fp16 group state holds four keys");
+    static_assert(SB == 1 || SB == 2, "blocks of 64 or 128 keys");
     constexpr int GB = GT * (GH ? 2 : 4);  // bytes per (group, query)
     using GRaw = typename GroupRaw<GB>::type;
     __shared__ __align__(16) GRaw sG[STREAM ? NG : 1][256];
@@ -635,9 +642,10 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
         roff[i] = (uint32_t)(row * (int)k_sn + j * 8) * 2u;
     }
     const uint32_t lds0 = fta_lds_addr(&sK[0][0]);
-    auto issue = [&](int m) {
-        const uint32_t sb = lds0 + (m & (NBUF - 1)) * Sh::BUF_B;
-        const int kb = m * 64 - pad_head;
+    const int U = M * SB;  // 64-key chunks
+    auto issue = [&](int u) {
+        const uint32_t sb = lds0 + (u & (NBUF - 1)) * Sh::BUF_B;
+        const int kb = u * 64 - pad_head;
         if (kb >= 0 && kb + 64 <= N) {
             const uint16_t* base = kp + (int64_t)kb * k_sn;
 #pragma unroll
@@ -657,7 +665,7 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
             }
         }
     };
-    // scores of keys 32 s .. 32 s + 31 of block m for both query tiles
+    // scores of keys 32 s .. 32 s + 31 of a chunk for both query tiles
     auto mma_half = [&](int bi, int s, f32x16 (&acc)[2]) {
         const uint16_t* base = reinterpret_cast<const uint16_t*>(&sK[bi][0]) + s * 32 * QSEG * 8;
         const f32x16 zacc = {};
@@ -670,8 +678,8 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
             acc[1] = E::mma(a[ks], qf[1][ks], ks ? acc[1] : zacc);
         }
     };
-    auto edge_mask = [&](int m, int s, f32x16 (&acc)[2]) {
-        const int kb = m * 64 - pad_head;
+    auto edge_mask = [&](int u, int s, f32x16 (&acc)[2]) {
+        const int kb = u * 64 - pad_head;
         if (kb < 0 || kb + 64 > N) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
@@ -816,10 +824,10 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
 
 #pragma unroll
     for (int j = 0; j < NBUF - 1; ++j)
-        if (j < M) issue(j);
-    if (M >= 3)
+        if (j < U) issue(j);
+    if (U >= 3)
         fta_wait_vmcnt<2 * LQ>();
-    else if (M == 2)
+    else if (U == 2)
         fta_wait_vmcnt<LQ>();
     else
         fta_wait_vmcnt<0>();
@@ -827,52 +835,59 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
     f32x16 h0[2], h1[2];
     mma_half(0, 0, h0);
 
-    // Block m; jm = m mod 8, a compile-time constant in the unrolled main loop, so
-    // the K buffer (m mod 4) and the group slot (m mod NG) become immediate LDS
-    // offsets instead of per-read address arithmetic.
-    // `interior`: 0 < m < M - 1 (no head / tail adjustment, a next block exists).
-    auto block = [&](int m, auto jm, auto interior) {
+    // Chunk u of block m = u / SB; ju = u mod 4 (a compile-time constant in the
+    // unrolled main loop, so the K buffer (u mod 4), the sub-chunk (u mod SB) and,
+    // for SB = 1, the group slot (m mod NG) become immediates instead of per-read
+    // address arithmetic).  bsum carries the block's earlier chunk totals (SB = 2).
+    // `interior`: chunk u lies inside the sequence, its block is neither the first
+    // nor the last (no head / tail adjustment) and a next chunk exists.
+    float bsum = 0.f;
+    auto block = [&](int u, auto ju, auto interior) {
         constexpr bool IN = decltype(interior)::value;
-        const int bm = int(jm) & (NBUF - 1), bn = (int(jm) + 1) & (NBUF - 1);  // buffers of m, m + 1
+        const int bm = int(ju) & (NBUF - 1), bn = (int(ju) + 1) & (NBUF - 1);  // buffers of u, u + 1
+        const int m = (SB == 1) ? u : (u >> 1);
+        const int sub = (SB == 1) ? 0 : (int(ju) & 1);
+        const bool blast = sub == SB - 1;  // the block's last chunk: its value is formed here
         const int gslot = m & (NG > 0 ? NG - 1 : 0);
-        // block m + 1 resident: blocks issued so far = min(M, m + 3)
-        if (IN || m + 1 < M) {
-            if (m + 3 <= M)
+        // chunk u + 1 resident: chunks issued so far = min(U, u + 3)
+        if (IN || u + 1 < U) {
+            if (u + 3 <= U)
                 fta_wait_vmcnt<LQ>();
             else
                 fta_wait_vmcnt<0>();
         }
-        __syncthreads();  // block m + 1 visible; every wave is past block m - 1
-        if (m + 3 < M) issue(m + 3);
+        __syncthreads();  // chunk u + 1 visible; every wave is past chunk u - 1
+        if (u + 3 < U) issue(u + 3);
         // this block's group top-2 entry, read now so its latency hides under the stages
         GRaw gtop = {};
-        if constexpr (STREAM) gtop = sG[gslot][tid];
+        if constexpr (STREAM)
+            if (blast) gtop = sG[gslot][tid];
 
         float e0[2], e1[2];
-        const int kb = m * 64 - pad_head;
-        if (IN || m + 1 < M) {
+        const int kb = u * 64 - pad_head;
+        if (IN || u + 1 < U) {
             // Every block but the last runs the same two stages; a block at a
             // sequence edge first masks its scores in place (uniform branches),
             // so the loop-carried accumulators have one definition and keep
             // their registers.  Masked scores are -inf: their exps are 0.
             // pad_head, pad_tail < b and b | pad_head + N + pad_tail (checked on the host):
-            // only the first and the last block can reach past the sequence
+            // only the chunks of the first and the last block can reach past the sequence
             const bool edge = !IN && (kb < 0 || kb + 64 > N);
-            if (edge) edge_mask(m, 0, h0);
-            stage(bm, 1, h1, h0, e0);     // MFMAs of half 1 of block m, exps of half 0
-            if (edge) edge_mask(m, 1, h1);
-            stage(bn, 0, h0, h1, e1);     // MFMAs of half 0 of block m + 1, exps of half 1
+            if (edge) edge_mask(u, 0, h0);
+            stage(bm, 1, h1, h0, e0);     // MFMAs of half 1 of chunk u, exps of half 0
+            if (edge) edge_mask(u, 1, h1);
+            stage(bn, 0, h0, h1, e1);     // MFMAs of half 0 of chunk u + 1, exps of half 1
         } else {
-            edge_mask(m, 0, h0);
+            edge_mask(u, 0, h0);
             mma_half(bm, 1, h1);
             sums16(h0, R, e0);
-            edge_mask(m, 1, h1);
-            if (m + 1 < M) {
+            edge_mask(u, 1, h1);
+            if (u + 1 < U) {
                 mma_half(bn, 0, h0);
             }
             sums16(h1, R, e1);
         }
-        // block total of the lane's own (tile, query): lanes l and l ^ 32 hold halves
+        // chunk total of the lane's own (tile, query): lanes l and l ^ 32 hold halves
         // of each query's sum; one lane-half swap adds them (the same operand pairs as
         // part + part[l ^ 32], so the results are identical)
         float tot_own;
@@ -892,8 +907,8 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
                 f32x16 x0[2], x1[2];
                 mma_half(bm, 0, x0);
                 mma_half(bm, 1, x1);
-                edge_mask(m, 0, x0);
-                edge_mask(m, 1, x1);
+                edge_mask(u, 0, x0);
+                edge_mask(u, 1, x1);
                 const float R_old = own1 ? R[1] : R[0];
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
@@ -908,6 +923,7 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
                 const float R_new = own1 ? R[1] : R[0];
                 Rown = R_new;
                 L = (L > 0.f) ? L * fta_exp2(R_old - R_new) : 0.f;
+                if constexpr (SB > 1) bsum = (bsum > 0.f) ? bsum * fta_exp2(R_old - R_new) : 0.f;
                 float f0[2], f1[2];
                 sums16(x0, R, f0);
                 sums16(x1, R, f1);
@@ -920,27 +936,36 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
                 tot_own = own1 ? tot[1] : tot[0];
             }
         }
+        // block total so far (the chunks before this one were rescaled with R)
+        float bs = tot_own;
+        if constexpr (SB > 1) bs = sub ? bsum + tot_own : tot_own;
         // only the lane's own block lse is stored (log2(0) = -inf)
-        const float mine = Rown + fta_log2(tot_own);
+        const float mine = Rown + fta_log2(bs);
         L += tot_own;
         {
-            if (rare && __ballot(tot_own > 0x1p40f) != 0ull) {
-                // rebase a large row total on this block's lse (both tiles' references,
+            if (rare && __ballot(bs > 0x1p40f) != 0ull) {
+                // rebase a large total on this block's lse (both tiles' references,
                 // so this lane's exps of the other tile stay in step with its owner)
-                float x = tot_own, y = tot_own;
+                float x = bs, y = bs;
                 fta_swap32(x, y);
                 const float other = own1 ? x : y;
-                const float tot[2] = {own1 ? other : tot_own, own1 ? tot_own : other};
+                const float tot[2] = {own1 ? other : bs, own1 ? bs : other};
 #pragma unroll
                 for (int t = 0; t < 2; ++t)
                     if (tot[t] > 0x1p40f) {
                         const float Rn = R[t] + fta_log2(tot[t]);
-                        if ((t == 1) == own1) L *= fta_exp2(R[t] - Rn);
+                        if ((t == 1) == own1) {
+                            const float f = fta_exp2(R[t] - Rn);
+                            L *= f;
+                            if constexpr (SB > 1) bs *= f;
+                        }
                         R[t] = Rn;
                     }
                 Rown = own1 ? R[1] : R[0];
             }
         }
+        if constexpr (SB > 1) bsum = bs;
+        if (!blast) return;
         const int qi = qbase + lane;
         if constexpr (STREAM) {
             // wave-uniform adjustment and edge flag (partial edge blocks always pass)
@@ -1027,25 +1052,43 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
             }
         }
     };
-    // every block but the last always produces the next block's half 0
+    // every chunk but the last always produces the next chunk's half 0
     {
         using I0 = std::integral_constant<int, 0>;
         using I1 = std::integral_constant<int, 1>;
         using I2 = std::integral_constant<int, 2>;
         using I3 = std::integral_constant<int, 3>;
-        int m = 0;
-        if (M > 1) {
+        if constexpr (SB == 1) {
+            int m = 0;
+            if (M > 1) {
+                block(0, I0{}, std::false_type{});
+                m = 1;
+            }
+            for (; m + 4 < M; m += 4) {  // m = 1 mod 4
+                block(m, I1{}, std::true_type{});
+                block(m + 1, I2{}, std::true_type{});
+                block(m + 2, I3{}, std::true_type{});
+                block(m + 3, I0{}, std::true_type{});
+            }
+            for (; m + 1 < M; ++m) block(m, m & 3, std::true_type{});
+            block(M - 1, (M - 1) & 3, std::false_type{});
+        } else {
+            // the two chunks of the first and of the last block run as edge chunks
             block(0, I0{}, std::false_type{});
-            m = 1;
+            block(1, I1{}, std::false_type{});
+            int u = 2;
+            for (; u + 4 <= U - 2; u += 4) {  // u = 2 mod 4
+                block(u, I2{}, std::true_type{});
+                block(u + 1, I3{}, std::true_type{});
+                block(u + 2, I0{}, std::true_type{});
+                block(u + 3, I1{}, std::true_type{});
+            }
+            for (; u < U - 2; ++u) block(u, u & 3, std::true_type{});
+            if (U > 2) {
+                block(U - 2, (U - 2) & 3, std::false_type{});
+                block(U - 1, (U - 1) & 3, std::false_type{});
+            }
         }
-        for (; m + 4 < M; m += 4) {  // m = 1 mod 4
-            block(m, I1{}, std::true_type{});
-            block(m + 1, I2{}, std::true_type{});
-            block(m + 2, I3{}, std::true_type{});
-            block(m + 3, I0{}, std::true_type{});
-        }
-        for (; m + 1 < M; ++m) block(m, m & 3, std::true_type{});
-        block(M - 1, (M - 1) & 3, std::false_type{});
     }
 
     const int qi = qbase + lane;
@@ -1067,9 +1110,9 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
     }
 }
 
-template <int DT, int D, int NG, int GT, bool GH>
+template <int DT, int D, int NG, int GT, bool GH, int SB>
 __global__ __launch_bounds__(256, 2) void fta_block_score_lse_pipe_kernel(const ScoreArgs a) {
-    fta_score_tile<DT, D, NG, GT, GH>(a, fta_xcd_remap(blockIdx.x, a.total));
+    fta_score_tile<DT, D, NG, GT, GH, SB>(a, fta_xcd_remap(blockIdx.x, a.total));
 }
 
 // ----------------------------------------------------------------------------
@@ -1596,7 +1639,7 @@ __global__ void fta_stream_reset_kernel(int* __restrict__ ctrs) {
 // top-k from the slot with the selector of the per-block-value path.  The
 // results equal the stream path's (both selectors are exact); only the time
 // differs.
-template <int DT, int D, int KB>
+template <int DT, int D, int KB, int SB>
 __global__ __launch_bounds__(256, 1) void fta_stream_fallback_kernel(ScoreArgs a, const int* __restrict__ ovf_list,
                                                                     const int* __restrict__ ovf_cnt,
                                                                     float* __restrict__ slots, int m_out,
@@ -1612,7 +1655,7 @@ __global__ __launch_bounds__(256, 1) void fta_stream_fallback_kernel(ScoreArgs a
     a.tau_idx = nullptr;
     for (int r = blockIdx.x; r < n; r += gridDim.x) {
         const int tile = __builtin_amdgcn_readfirstlane(ovf_list[r]);
-        fta_score_tile<DT, D, 0>(a, tile);
+        fta_score_tile<DT, D, 0, 2, false, SB>(a, tile);
         __syncthreads();  // the slot is complete
         const int bh = tile / a.qtiles, qt = tile - bh * a.qtiles;
         const int64_t r0 = (int64_t)bh * a.N + qt * 256;
@@ -1713,10 +1756,10 @@ __global__ __launch_bounds__(256) void fta_topk_select_sort_kernel(
 
 namespace {
 
-// The pipelined scoring kernel serves b = 64 with D <= 128 rounded to 64 or 128
-// and a K token stride whose 64-row offsets fit 32 bits.
+// The pipelined scoring kernel serves b = 64 and b = 128 with D <= 128 rounded to
+// 64 or 128 and a K token stride whose 64-row offsets fit 32 bits.
 bool score_pipe_ok(int bsz, int Dk, const int64_t* ks) {
-    return bsz == 64 && (Dk == 64 || Dk == 128) && ks[2] >= 0 && ks[2] <= (1 << 24);
+    return (bsz == 64 || bsz == 128) && (Dk == 64 || Dk == 128) && ks[2] >= 0 && ks[2] <= (1 << 24);
 }
 
 // Candidate streams of the pipelined kernel (STREAM = true), laid out in the
@@ -1796,9 +1839,16 @@ int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D
     }
     const ScoreArgs sa = score_args(q, k, B, H, N, D, qs, ks, M, bsz, pad_head, pad_tail, scale, blk_lse, row_lse,
                                     kgroups, tau, sb);
+#define FTA_LAUNCH_PIPE_SB(DK, NG, GT, GH, SB)                                                             \
+    hipLaunchKernelGGL((fta_block_score_lse_pipe_kernel<DT, (DK == 64) ? 64 : 128, NG, GT, GH, SB>),        \
+                       dim3(total), dim3(256), 0, st, sa)
 #define FTA_LAUNCH_PIPE(DK, NG, GT, GH)                                                                    \
-    hipLaunchKernelGGL((fta_block_score_lse_pipe_kernel<DT, (DK == 64) ? 64 : 128, NG, GT, GH>), dim3(total), \
-                       dim3(256), 0, st, sa)
+    do {                                                                                                   \
+        if (bsz == 64)                                                                                     \
+            FTA_LAUNCH_PIPE_SB(DK, NG, GT, GH, 1);                                                         \
+        else                                                                                               \
+            FTA_LAUNCH_PIPE_SB(DK, NG, GT, GH, 2);                                                         \
+    } while (0)
 #define FTA_LAUNCH_SCORE(DK)                                                                               \
     if (pipe && sb.pool != nullptr && sb.m_out <= 8)                                                       \
         FTA_LAUNCH_PIPE(DK, 4, 2, false);                                                                  \
@@ -1828,6 +1878,7 @@ int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D
     }
 #undef FTA_LAUNCH_SCORE
 #undef FTA_LAUNCH_PIPE
+#undef FTA_LAUNCH_PIPE_SB
     return fta::check_launch("fta_block_score_lse_kernel");
 }
 
@@ -2075,12 +2126,18 @@ int launch_stream_select_dt(const ScoreArgs& sa, int Dk, const StreamBufs& sb, i
     int rc = fta::check_launch("fta_topk_stream_kernel");
     if (rc != FTA_OK) return rc;
     const int grid = sa.total < kStreamSlots ? sa.total : kStreamSlots;
-    if (Dk == 64)
-        hipLaunchKernelGGL((fta_stream_fallback_kernel<DT, 64, 32>), dim3(grid), dim3(256), 0, s, sa, sb.ovf_list,
-                           sb.ctrs + 1, sb.slots, m_out, threshold, idx, raw, avg);
+#define FTA_LAUNCH_FALLBACK(DK, SB)                                                                             \
+    hipLaunchKernelGGL((fta_stream_fallback_kernel<DT, DK, 32, SB>), dim3(grid), dim3(256), 0, s, sa, sb.ovf_list, \
+                       sb.ctrs + 1, sb.slots, m_out, threshold, idx, raw, avg)
+    if (Dk == 64 && sa.bsz == 64)
+        FTA_LAUNCH_FALLBACK(64, 1);
+    else if (Dk == 64)
+        FTA_LAUNCH_FALLBACK(64, 2);
+    else if (sa.bsz == 64)
+        FTA_LAUNCH_FALLBACK(128, 1);
     else
-        hipLaunchKernelGGL((fta_stream_fallback_kernel<DT, 128, 32>), dim3(grid), dim3(256), 0, s, sa, sb.ovf_list,
-                           sb.ctrs + 1, sb.slots, m_out, threshold, idx, raw, avg);
+        FTA_LAUNCH_FALLBACK(128, 2);
+#undef FTA_LAUNCH_FALLBACK
     return fta::check_launch("fta_stream_fallback_kernel");
 }
 
@@ -2130,7 +2187,7 @@ int fta_topk_score_candidates(const void* q, const void* k, int dtype, int B, in
                                workspace_bytes, &M, &m_out, &streams);
     if (st != FTA_OK) return st;
     if (!streams)
-        return fta::unsupported("topk_score_candidates: needs b = 64, D <= 128 and at most 32 blocks per query");
+        return fta::unsupported("topk_score_candidates: needs b = 64 or 128, D <= 128 and at most 32 blocks per query");
     float* row_lse = nullptr;
     const StreamBufs sb = stream_layout(workspace, workspace_bytes, B, H, N, M, m_out, &row_lse);
     return launch_score_lse(q, k, dtype, B, H, N, D, q_strides, k_strides, M, score_block_size, pad_head, pad_tail,
@@ -2150,7 +2207,7 @@ int fta_topk_select_candidates(const void* q, const void* k, int dtype, int B, i
                                workspace_bytes, &M, &m_out, &streams);
     if (st != FTA_OK) return st;
     if (!streams)
-        return fta::unsupported("topk_select_candidates: needs b = 64, D <= 128 and at most 32 blocks per query");
+        return fta::unsupported("topk_select_candidates: needs b = 64 or 128, D <= 128 and at most 32 blocks per query");
     if (!topk_indices || !topk_raw || !topk_avg) return fta::arg_error("topk_select_candidates: null pointer");
     return stream_select(q, k, dtype, B, H, N, D, q_strides, k_strides, score_block_size, pad_head, pad_tail, scale,
                          M, m_out, threshold, topk_indices, topk_raw, topk_avg, workspace, workspace_bytes,

@@ -36,7 +36,7 @@ def flash_topk_score(
     Returns ``(topk_indices int32, topk_raw_scores f32, topk_avg_scores f32)``,
     each ``[B, H, N, min(topk, M)]`` (``M`` when ``topk == 0``).  Scoring and
     selection run in one C call: the normalised ``[B, H, N, M]`` scores are
-    never formed; for b = 64, D <= 128 and topk <= 32 the selector reads the
+    never formed; for b = 64 or 128, D <= 128 and topk <= 32 the selector reads the
     scorer's candidate streams (bounded workspace), otherwise its per-block
     log2-sums.
     """

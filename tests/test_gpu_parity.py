@@ -34,6 +34,10 @@ SCORE_CASES = [
     (1, 256, 2, 40, 64, (0, 0), torch.float32, "bnc"),
     (1, 200, 2, 256, 64, (30, 26), torch.bfloat16, "bnc"),
     (1, 40, 2, 80, 64, (0, 24), torch.bfloat16, "bnc"),
+    # b = 128 through the pipelined kernel (two 64-key chunks per block); a head /
+    # tail pad above 64 leaves a whole chunk of the edge block outside the sequence
+    (1, 1000, 2, 128, 128, (24, 0), torch.bfloat16, "bnc"),
+    (1, 700, 2, 64, 128, (100, 96), torch.float16, "bnc"),
 ]
 
 
@@ -97,10 +101,17 @@ SHORT_CASES = [
     (1, 320, 2, 64, 64, (0, 0), torch.bfloat16, "bnc"),    # M = 5: one unrolled pass
     (1, 560, 2, 128, 64, (30, 50), torch.bfloat16, "bnc"), # M = 10, partial edges
     (1, 576, 1, 64, 64, (0, 0), torch.float16, "bnc"),     # M = 9: unrolled twice, no remainder
+    # b = 128: 2 M chunks, the first and last two peeled, 2 M - 4 in the loop of four
+    (1, 128, 2, 128, 128, (0, 0), torch.bfloat16, "bnc"),    # M = 1
+    (1, 200, 2, 64, 128, (40, 16), torch.bfloat16, "bnc"),   # M = 2, both blocks partial
+    (1, 300, 1, 128, 128, (0, 84), torch.float16, "bnc"),    # M = 3, last chunk outside
+    (1, 512, 2, 64, 128, (0, 0), torch.bfloat16, "bnc"),     # M = 4: one unrolled pass
+    (1, 600, 2, 128, 128, (100, 68), torch.bfloat16, "bnc"), # M = 6: pass + remainder
+    (1, 896, 1, 64, 128, (0, 0), torch.float16, "bnc"),      # M = 7
 ]
 
 
-@pytest.mark.parametrize("case", SHORT_CASES, ids=lambda c: f"N{c[1]}D{c[3]}p{c[5]}")
+@pytest.mark.parametrize("case", SHORT_CASES, ids=lambda c: f"N{c[1]}D{c[3]}b{c[4]}p{c[5]}")
 def test_score_short_sequences(case):
     B, N, H, D, b, pad, dt, layout = case
     say(f"[short score] {case}")
@@ -606,20 +617,21 @@ def test_flash_sparse_attn_func_truncated_counts():
     assert not o1[0, 5 * g:6 * g, D:].any() and torch.isneginf(sl[0, 1, 5 * g:6 * g]).all()
 
 
-def _pattern_qk(N, H, D, pattern, seed):
-    """q, k [1, N, H*D] bf16 whose block scores follow `pattern` over the blocks:
+def _pattern_qk(N, H, D, pattern, seed, b=64):
+    """q, k [1, N, H*D] bf16 whose block scores follow `pattern` over the
+    b-key blocks:
     'increasing' / 'decreasing' (every block beats / loses to all earlier ones),
-    'ties' (all 64-key blocks identical, so every block score is exactly equal),
+    'ties' (all blocks identical, so every block score is exactly equal),
     'peaked' (config 3's block-centred data), 'iid', or 'jump' (blocks 5 and
     M - 3 score 130+ log2 units above everything before them, so their exp sums
-    overflow the scorer's running reference: in the candidate-stream scorer the
-    tile is scored again by the fallback kernel's exact path)."""
+    overflow the scorer's running reference: the scorer re-scores those blocks
+    on its exact path, here inside the unrolled block loop)."""
     g = torch.Generator(device="cpu").manual_seed(seed)
     C = H * D
     if pattern == "peaked":
-        M = N // 64
+        M = N // b
         cent = torch.randn(1, M, C, generator=g)
-        k = 0.3 * torch.randn(1, N, C, generator=g) + cent.repeat_interleave(64, dim=1)
+        k = 0.3 * torch.randn(1, N, C, generator=g) + cent.repeat_interleave(b, dim=1)
         pick = torch.randint(0, M, (1, N), generator=g)
         q = 0.3 * torch.randn(1, N, C, generator=g) + torch.gather(cent, 1, pick.unsqueeze(-1).expand(1, N, C))
     elif pattern == "iid":
@@ -628,16 +640,16 @@ def _pattern_qk(N, H, D, pattern, seed):
         u = torch.randn(1, 1, C, generator=g)
         q = u + 0.1 * torch.randn(1, N, C, generator=g)
         k = 0.5 * torch.randn(1, N, C, generator=g)
-        M = N // 64
+        M = N // b
         for j in (5, M - 3):
-            k[:, j * 64:(j + 1) * 64] = 12.0 * u + 0.1 * torch.randn(1, 64, C, generator=g)
+            k[:, j * b:(j + 1) * b] = 12.0 * u + 0.1 * torch.randn(1, b, C, generator=g)
     else:
         u = torch.randn(1, 1, C, generator=g)
         q = u + 0.1 * torch.randn(1, N, C, generator=g)
-        w = 0.5 * torch.randn(1, 64, C, generator=g)
-        k = w.repeat(1, (N + 63) // 64, 1)[:, :N]
+        w = 0.5 * torch.randn(1, b, C, generator=g)
+        k = w.repeat(1, (N + b - 1) // b, 1)[:, :N]
         if pattern != "ties":
-            j = torch.arange(N).div(64, rounding_mode="floor").float() / max(1, (N - 1) // 64)
+            j = torch.arange(N).div(b, rounding_mode="floor").float() / max(1, (N - 1) // b)
             ramp = j if pattern == "increasing" else 1.0 - j
             k = k + (1.5 * ramp).view(1, N, 1) * u
     return q.to(torch.bfloat16).cuda(), k.to(torch.bfloat16).cuda()
@@ -660,41 +672,55 @@ STREAM_CASES = [
     (8192, 2, 128, (0, 0), 32, 0.9, "peaked"),
     (1000, 2, 64, (30, 58), 20, 1.0, "iid"),
     (4096, 2, 64, (0, 0), 17, 1.0, "decreasing"),
-    # reference overflow inside the unrolled block loop: the tile goes through the fallback
+    # reference overflow inside the unrolled block loop: the exact path re-scores the block
     (4096, 2, 128, (0, 0), 16, 1.0, "jump"),
     (4096, 1, 64, (0, 0), 32, 0.9, "jump"),
+    # b = 128 (two 64-key chunks per block; the reference's published b = 128 shape
+    # is N 4096, H 32, D 128, top-16)
+    (8192, 2, 128, (0, 0), 16, 1.0, "increasing", 128),
+    (4096, 2, 64, (0, 0), 8, 0.9, "decreasing", 128),
+    (4096, 1, 128, (0, 0), 16, 1.0, "ties", 128),
+    (1000, 2, 64, (100, 52), 20, 1.0, "iid", 128),
+    (8192, 2, 128, (0, 0), 32, 0.9, "peaked", 128),
+    (8192, 2, 128, (0, 0), 16, 1.0, "jump", 128),
+    (4096, 4, 128, (0, 0), 16, 0.9, "iid", 128),
 ]
 
 
-@pytest.mark.parametrize("case", STREAM_CASES, ids=lambda c: f"N{c[0]}D{c[2]}k{c[4]}{c[6]}p{c[3][0]}")
+@pytest.mark.parametrize("case", STREAM_CASES,
+                         ids=lambda c: f"N{c[0]}D{c[2]}k{c[4]}{c[6]}p{c[3][0]}b{c[7] if len(c) > 7 else 64}")
 def test_topk_candidate_streams_exact(case):
-    """The pipelined scorer's candidate streams (b = 64, top-k <= 32) drop a
-    block only when enough earlier blocks rank above it: the fused result
-    equals the selection over the full score tensor bit for bit, including
-    adversarial block orders (every block a new maximum), exact ties and
-    partial edge blocks."""
-    N, H, D, pad, topk, thr, pattern = case
+    """The pipelined scorer's candidate streams (b = 64 or 128, top-k <= 32)
+    drop a block only when enough earlier blocks rank above it: the fused
+    result equals the selection over the full score tensor bit for bit,
+    including adversarial block orders (every block a new maximum), exact ties
+    and partial edge blocks."""
+    N, H, D, pad, topk, thr, pattern = case[:7]
+    b = case[7] if len(case) > 7 else 64
     say(f"[topk streams] {case}")
-    q, k = _pattern_qk(N, H, D, pattern, 31)
-    scores = fta.flash_block_score(q, k, H, 64, pad)
-    fi, fr, fa = fta.flash_topk_score(q, k, H, 64, topk, pad, thr)
+    q, k = _pattern_qk(N, H, D, pattern, 31, b)
+    scores = fta.flash_block_score(q, k, H, b, pad)
+    fi, fr, fa = fta.flash_topk_score(q, k, H, b, topk, pad, thr)
     torch.cuda.synchronize()
-    ri, rr, ra = O.topk_select(scores.cpu().numpy(), thr, topk, 64, pad)
+    ri, rr, ra = O.topk_select(scores.cpu().numpy(), thr, topk, b, pad)
     np.testing.assert_array_equal(fi.cpu().numpy(), ri)
     np.testing.assert_array_equal(fr.cpu().numpy(), rr)
     np.testing.assert_array_equal(fa.cpu().numpy(), ra)
     if pattern == "increasing" and pad == (0, 0):
-        M = N // 64
+        M = N // b
         assert (ri[..., 0] == M - 1).all()
 
 
-@pytest.mark.parametrize("pattern,topk,D,extra_chunks", [
-    ("increasing", 16, 128, 0),     # every block enters every stream: all tiles overflow
-    ("increasing", 16, 128, 300),   # spare chunks for part of the waves: some tiles fit, others overflow
-    ("iid", 32, 64, 0),
-    ("ties", 8, 128, 5),
+@pytest.mark.parametrize("pattern,topk,D,extra_chunks,b", [
+    ("increasing", 16, 128, 0, 64),     # every block enters every stream: all tiles overflow
+    ("increasing", 16, 128, 300, 64),   # spare chunks for part of the waves: some tiles fit, others overflow
+    ("iid", 32, 64, 0, 64),
+    ("ties", 8, 128, 5, 64),
+    ("increasing", 16, 64, 0, 128),
+    ("increasing", 32, 128, 60, 128),
+    ("jump", 16, 128, 0, 128),
 ])
-def test_topk_stream_pool_overflow_fallback(pattern, topk, D, extra_chunks):
+def test_topk_stream_pool_overflow_fallback(pattern, topk, D, extra_chunks, b):
     """Candidate streams share a pool sized by the workspace; tiles whose
     streams do not fit are scored and selected again by the fallback kernel.
     With the least workspace the library accepts (one 1024-entry chunk per 64
@@ -704,13 +730,13 @@ def test_topk_stream_pool_overflow_fallback(pattern, topk, D, extra_chunks):
     from flash_topk_attn_v2 import _lib
 
     N, H, pad, thr = 4096, 2, (0, 0), 1.0 if pattern != "iid" else 0.9
-    say(f"[stream overflow] {pattern} topk{topk} D{D} extra{extra_chunks}")
-    q, k = _pattern_qk(N, H, D, pattern, 33)
-    scores = fta.flash_block_score(q, k, H, 64, pad)
-    ri, rr, ra = O.topk_select(scores.cpu().numpy(), thr, topk, 64, pad)
+    say(f"[stream overflow] {pattern} topk{topk} D{D} extra{extra_chunks} b{b}")
+    q, k = _pattern_qk(N, H, D, pattern, 33, b)
+    scores = fta.flash_block_score(q, k, H, b, pad)
+    ri, rr, ra = O.topk_select(scores.cpu().numpy(), thr, topk, b, pad)
     L = _lib.lib()
-    nmin = L.fta_topk_score_workspace_min(1, H, N, D, 64, 0, 0, topk)
-    assert 0 < nmin < L.fta_topk_score_workspace_size_ex(1, H, N, D, 64, 0, 0, topk)
+    nmin = L.fta_topk_score_workspace_min(1, H, N, D, b, 0, 0, topk)
+    assert 0 < nmin < L.fta_topk_score_workspace_size_ex(1, H, N, D, b, 0, 0, topk)
     ws = torch.empty(nmin + extra_chunks * 8192, dtype=torch.uint8, device="cuda")
     st = _lib.i64arr([N * H * D, D, H * D])
     stream = torch.cuda.current_stream().cuda_stream
@@ -719,15 +745,15 @@ def test_topk_stream_pool_overflow_fallback(pattern, topk, D, extra_chunks):
                torch.zeros(1, H, N, topk, device="cuda"), torch.zeros(1, H, N, topk, device="cuda")]
         optr = [o.data_ptr() for o in out]
         if two_stage:
-            rc = L.fta_topk_score_candidates(q.data_ptr(), k.data_ptr(), 0, 1, H, N, D, st, st, 64, 0, 0,
+            rc = L.fta_topk_score_candidates(q.data_ptr(), k.data_ptr(), 0, 1, H, N, D, st, st, b, 0, 0,
                                              D ** -0.5, topk, ws.data_ptr(), ws.numel(), stream)
             _lib.check(rc, "fta_topk_score_candidates")
             counts = ws[: (N // 256) * 4 * H * 4].view(torch.int32).clone()
-            rc = L.fta_topk_select_candidates(q.data_ptr(), k.data_ptr(), 0, 1, H, N, D, st, st, 64, 0, 0,
+            rc = L.fta_topk_select_candidates(q.data_ptr(), k.data_ptr(), 0, 1, H, N, D, st, st, b, 0, 0,
                                               D ** -0.5, topk, thr, *optr, ws.data_ptr(), ws.numel(), stream)
             _lib.check(rc, "fta_topk_select_candidates")
         else:
-            rc = L.fta_topk_score(q.data_ptr(), k.data_ptr(), 0, 1, H, N, D, st, st, 64, 0, 0, D ** -0.5, topk,
+            rc = L.fta_topk_score(q.data_ptr(), k.data_ptr(), 0, 1, H, N, D, st, st, b, 0, 0, D ** -0.5, topk,
                                   thr, *optr, ws.data_ptr(), ws.numel(), stream)
             _lib.check(rc, "fta_topk_score")
         torch.cuda.synchronize()
