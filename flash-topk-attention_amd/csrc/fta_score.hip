@@ -525,7 +525,15 @@ constexpr int kStreamMaxTopk = 32;
 // Entries per stream chunk (a multiple of the selector's 256-entry steps).
 constexpr int kStreamChunk = 1024;
 
-__device__ __forceinline__ float fta_stream_margin(float b) { return b - (0x1p-10f + fabsf(b) * 0x1p-18f); }
+// Filter margin in log2 units.  A block is dropped only when its key is below
+// the bound by more than this, while at least m_out blocks have keys at or above
+// the bound; the selector ranks blocks by avg = 2^(fl(value - rl)) / b.  With
+// |value - rl| <= ~101 log2 units (the range that matters, see the end-of-tile
+// check), fl(value - rl) is off by at most 2^-24 * 128 = 2^-17 and v_exp_f32 by
+// about 1 ulp (2^-23 relative), so keys 2^-14 apart give strictly ordered
+// normal averages (8x slack); the relative term covers the rounding of the
+// subtraction below for large keys.
+__device__ __forceinline__ float fta_stream_margin(float b) { return b - (0x1p-14f + fabsf(b) * 0x1p-20f); }
 
 // Arguments of the pipelined scoring kernel (one struct, passed by value).
 struct ScoreArgs {
@@ -558,8 +566,9 @@ struct ScoreArgs {
 
 // Group state of the candidate-stream filter: per query and block group, the GT
 // largest ranking keys seen, descending, as fp32 (GH = false) or as fp16 (GH =
-// true: half the LDS; the stored values may exceed the keys by the fp16
-// rounding, 2^-11 relative, which the bound's margin covers).
+// true: half the LDS; keys relative to the query's first block key, and the
+// stored values may exceed them by the fp16 rounding, 2^-11 relative, which
+// the bound's margin covers).
 template <int GB>
 struct GroupRaw;
 template <>
@@ -799,11 +808,17 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
             return t[GT - 1];
         }
     };
-    // bound from a min over groups: fp16 keys may sit 2^-11 relative above the
-    // key they hold, so their bound is lowered by a further 2^-10 relative
-    auto gmargin = [&](float bnd) -> float {
-        return GH ? fta_stream_margin(bnd) - fabsf(bnd) * 0x1p-10f : fta_stream_margin(bnd);
+    // fp16 group state holds keys relative to the query's first block key gref,
+    // so its 2^-11 relative rounding scales with key differences, not with key
+    // magnitudes (near-uniform rows would otherwise pass every block).
+    float gref = 0.f;
+    // absolute bound from a min over the groups' keys: fp16 keys may sit 2^-11
+    // relative above the key they hold, so their bound is lowered by a further
+    // 2^-10 relative, and by 2^-22 |gref| for the fp32 add of the reference
+    auto gabs = [&](float bnd) -> float {
+        return GH ? gref + bnd - (fabsf(bnd) * 0x1p-10f + fabsf(gref) * 0x1p-22f) : bnd;
     };
+    auto gmargin = [&](float bnd) -> float { return fta_stream_margin(gabs(bnd)); };
 
     // candidate-stream state: the wave's current chunk and position in it, its
     // chunk count and entry count, and the current filter bound
@@ -1009,11 +1024,14 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
             // group top-GT insertion (t descending): new t0 = max(t0, ak), new t_i =
             // med3(t_{i-1}, t_i, ak).  Written as instructions: the compiler's max /
             // med3 first quiet every operand, and no value here is a NaN.  fp16 state
-            // takes the key clamped to the largest finite half (below the key).
+            // takes ak - gref clamped to the largest finite half (below the key).
             float t[GT], nt[GT];
             gdecode(gtop, t);
             float akg = ak;
-            if constexpr (GH) asm("v_min_f32 %0, %1, %2" : "=v"(akg) : "v"(ak), "v"(65504.f));
+            if constexpr (GH) {
+                if (!IN && m == 0) gref = (fabsf(ak) < FTA_INF) ? ak : 0.f;
+                asm("v_min_f32 %0, %1, %2" : "=v"(akg) : "v"(ak - gref), "v"(65504.f));
+            }
             asm("v_max_f32 %0, %1, %2" : "=v"(nt[0]) : "v"(t[0]), "v"(akg));
 #pragma unroll
             for (int i = 1; i < GT; ++i)
@@ -1092,16 +1110,25 @@ __device__ __forceinline__ void fta_score_tile(const ScoreArgs& a, const int wg)
     }
 
     const int qi = qbase + lane;
+    const float rlf = (L > 0.f) ? Rown + fta_log2(L) : -FTA_INF;
+    float bnd = -FTA_INF;
     if constexpr (STREAM) {
-        if (lane == 0) a.count[sw] = (cpos > kStreamChunk) ? -1 : spos;
+        bnd = glast(0);
+#pragma unroll
+        for (int j = 1; j < NG; ++j) bnd = fminf(bnd, glast(j));
+        bnd = gabs(bnd);  // fp16 state: relative to gref, lowered by its rounding
+        // The filter's margin orders the selector's averages 2^(key - rl) / b only
+        // while they are normal fp32 numbers: a final bound more than 100 log2
+        // units below the row total (averages that may be subnormal or zero, whose
+        // ties fall to the block index) sends the tile to the exact fallback, as
+        // an exhausted pool does.
+        const bool risky = lane_ok && bnd > -FTA_INF && !(bnd - rlf >= -100.f);
+        const bool redo = (cpos > kStreamChunk) || __ballot(risky) != 0ull;
+        if (lane == 0) a.count[sw] = redo ? -1 : spos;
     }
     if (qi < N) {
-        a.row_lse[(int64_t)bh * N + qi] = (L > 0.f) ? Rown + fta_log2(L) : -FTA_INF;
+        a.row_lse[(int64_t)bh * N + qi] = rlf;
         if constexpr (STREAM) {
-            float bnd = glast(0);
-#pragma unroll
-            for (int j = 1; j < NG; ++j) bnd = fminf(bnd, glast(j));
-            if constexpr (GH) bnd = bnd - fabsf(bnd) * 0x1p-10f;  // the fp16 rounding, as in gmargin
             a.tau_key[(int64_t)bh * N + qi] = bnd;
         } else if (kgroups > 0) {
             if (curg >= 0 && gkey < tkey) tidx = gidx;

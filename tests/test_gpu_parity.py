@@ -625,7 +625,11 @@ def _pattern_qk(N, H, D, pattern, seed, b=64):
     'peaked' (config 3's block-centred data), 'iid', or 'jump' (blocks 5 and
     M - 3 score 130+ log2 units above everything before them, so their exp sums
     overflow the scorer's running reference: the scorer re-scores those blocks
-    on its exact path, here inside the unrolled block loop)."""
+    on its exact path, here inside the unrolled block loop), 'cliff' (the last
+    block ~200+ log2 units above all others, whose averages underflow to zero,
+    so the top-k continues with the lowest block indices), 'step' (block M / 2
+    ~60 log2 units above the rest: small but normal averages) or 'uniform'
+    (q, k ~ N(0, 1) / sqrt(D): block values within ~1e-3 of each other)."""
     g = torch.Generator(device="cpu").manual_seed(seed)
     C = H * D
     if pattern == "peaked":
@@ -636,6 +640,15 @@ def _pattern_qk(N, H, D, pattern, seed, b=64):
         q = 0.3 * torch.randn(1, N, C, generator=g) + torch.gather(cent, 1, pick.unsqueeze(-1).expand(1, N, C))
     elif pattern == "iid":
         q, k = torch.randn(1, N, C, generator=g), torch.randn(1, N, C, generator=g)
+    elif pattern == "uniform":
+        q, k = (torch.randn(1, N, C, generator=g) / D ** 0.5 for _ in range(2))
+    elif pattern in ("cliff", "step"):
+        u = torch.randn(1, 1, C, generator=g)
+        q = u + 0.1 * torch.randn(1, N, C, generator=g)
+        k = 0.5 * torch.randn(1, N, C, generator=g)
+        M = N // b
+        j, sc = (M - 1, 16.0) if pattern == "cliff" else (M // 2, 60.0 / (1.4427 * D ** 0.5))
+        k[:, j * b:(j + 1) * b] = sc * u + 0.1 * torch.randn(1, b, C, generator=g)
     elif pattern == "jump":
         u = torch.randn(1, 1, C, generator=g)
         q = u + 0.1 * torch.randn(1, N, C, generator=g)
@@ -684,6 +697,15 @@ STREAM_CASES = [
     (8192, 2, 128, (0, 0), 32, 0.9, "peaked", 128),
     (8192, 2, 128, (0, 0), 16, 1.0, "jump", 128),
     (4096, 4, 128, (0, 0), 16, 0.9, "iid", 128),
+    # averages that underflow (ties at zero fall to the block index: exact fallback),
+    # small normal averages (kept on the stream path) and near-uniform scores
+    (4096, 2, 128, (0, 0), 16, 2.0, "cliff"),
+    (4096, 1, 64, (0, 0), 24, 2.0, "cliff", 128),
+    (4096, 2, 128, (0, 0), 16, 2.0, "step"),
+    (4096, 2, 64, (0, 0), 32, 2.0, "step"),
+    (8192, 2, 128, (0, 0), 16, 1.0, "uniform"),
+    (8192, 2, 64, (0, 0), 8, 0.9, "uniform"),
+    (4096, 2, 128, (0, 0), 32, 0.95, "uniform", 128),
 ]
 
 
@@ -709,6 +731,9 @@ def test_topk_candidate_streams_exact(case):
     if pattern == "increasing" and pad == (0, 0):
         M = N // b
         assert (ri[..., 0] == M - 1).all()
+    if pattern == "cliff":
+        # the case is live: the lists continue with zero averages at blocks 0, 1, ...
+        assert (ra[..., 1] == 0).mean() > 0.9 and (ri[..., 1] == 0).mean() > 0.9
 
 
 @pytest.mark.parametrize("pattern,topk,D,extra_chunks,b", [
