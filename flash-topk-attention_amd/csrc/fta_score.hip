@@ -1783,10 +1783,11 @@ __global__ __launch_bounds__(256) void fta_topk_select_sort_kernel(
 
 namespace {
 
-// The pipelined scoring kernel serves b = 64 and b = 128 with D <= 128 rounded to
-// 64 or 128 and a K token stride whose 64-row offsets fit 32 bits.
+// The pipelined scoring kernel serves b = 64 and b = 128 with D <= 128 (run as 64
+// or 128 columns, the columns past D multiplied by zero q columns) and a K token
+// stride whose 64-row offsets fit 32 bits.
 bool score_pipe_ok(int bsz, int Dk, const int64_t* ks) {
-    return (bsz == 64 || bsz == 128) && (Dk == 64 || Dk == 128) && ks[2] >= 0 && ks[2] <= (1 << 24);
+    return (bsz == 64 || bsz == 128) && Dk <= 128 && ks[2] >= 0 && ks[2] <= (1 << 24);
 }
 
 // Candidate streams of the pipelined kernel (STREAM = true), laid out in the
@@ -1867,7 +1868,7 @@ int launch_score_lse_dt(const void* q, const void* k, int B, int H, int N, int D
     const ScoreArgs sa = score_args(q, k, B, H, N, D, qs, ks, M, bsz, pad_head, pad_tail, scale, blk_lse, row_lse,
                                     kgroups, tau, sb);
 #define FTA_LAUNCH_PIPE_SB(DK, NG, GT, GH, SB)                                                             \
-    hipLaunchKernelGGL((fta_block_score_lse_pipe_kernel<DT, (DK == 64) ? 64 : 128, NG, GT, GH, SB>),        \
+    hipLaunchKernelGGL((fta_block_score_lse_pipe_kernel<DT, (DK <= 64) ? 64 : 128, NG, GT, GH, SB>),        \
                        dim3(total), dim3(256), 0, st, sa)
 #define FTA_LAUNCH_PIPE(DK, NG, GT, GH)                                                                    \
     do {                                                                                                   \
@@ -2156,9 +2157,9 @@ int launch_stream_select_dt(const ScoreArgs& sa, int Dk, const StreamBufs& sb, i
 #define FTA_LAUNCH_FALLBACK(DK, SB)                                                                             \
     hipLaunchKernelGGL((fta_stream_fallback_kernel<DT, DK, 32, SB>), dim3(grid), dim3(256), 0, s, sa, sb.ovf_list, \
                        sb.ctrs + 1, sb.slots, m_out, threshold, idx, raw, avg)
-    if (Dk == 64 && sa.bsz == 64)
+    if (Dk <= 64 && sa.bsz == 64)
         FTA_LAUNCH_FALLBACK(64, 1);
-    else if (Dk == 64)
+    else if (Dk <= 64)
         FTA_LAUNCH_FALLBACK(64, 2);
     else if (sa.bsz == 64)
         FTA_LAUNCH_FALLBACK(128, 1);

@@ -100,7 +100,7 @@ int fta_topk_select(const float* block_scores, int64_t rows, int M, int64_t stri
  * returns the recommended size for one call's geometry (0 for an invalid one),
  * assuming a K token stride of at most 2^24 elements.
  *
- * b = 64 or 128, D <= 128 (rounded to 64 / 128) and at most 32 blocks per query run
+ * b = 64 or 128, D <= 128 and at most 32 blocks per query run
  * on candidate streams: chunks of 1024 entries taken from a pool in the
  * workspace, one chunk per 64 queries plus a shared remainder, sized for the
  * expected number of entries (m_out (1 + 2 ln(M / m_out)) per query; 1.17e9

@@ -706,6 +706,11 @@ STREAM_CASES = [
     (8192, 2, 128, (0, 0), 16, 1.0, "uniform"),
     (8192, 2, 64, (0, 0), 8, 0.9, "uniform"),
     (4096, 2, 128, (0, 0), 32, 0.95, "uniform", 128),
+    # head dims run on the 64- or 128-column kernel with zero columns past D
+    (2048, 2, 96, (0, 0), 16, 0.9, "iid"),
+    (2048, 2, 32, (0, 0), 8, 1.0, "increasing"),
+    (1000, 2, 80, (24, 0), 12, 0.95, "iid"),
+    (2048, 1, 48, (0, 0), 24, 0.9, "ties", 128),
 ]
 
 
@@ -744,6 +749,7 @@ def test_topk_candidate_streams_exact(case):
     ("increasing", 16, 64, 0, 128),
     ("increasing", 32, 128, 60, 128),
     ("jump", 16, 128, 0, 128),
+    ("increasing", 16, 96, 0, 64),
 ])
 def test_topk_stream_pool_overflow_fallback(pattern, topk, D, extra_chunks, b):
     """Candidate streams share a pool sized by the workspace; tiles whose
