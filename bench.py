@@ -152,69 +152,129 @@ def bench_v1(dev, stream):
     return res
 
 
-# Rows of the reference's V2_BENCHMARK.md (RTX 4090, bf16, q_block_size =
-# score_block_size, threshold 1.0, qblock_topk = q_block_size * K): (B, N, H, D,
-# b, K, published V2 scoring ms, sparse attention ms, end-to-end ms, lines)
-V2_ROWS = [
-    (1, 4096, 32, 128, 64, 16, 2.67, 4.44, 7.26, "12,31,62"),
-    (1, 8192, 32, 128, 64, 16, 10.56, 17.37, 28.15, "13,32,63"),
-    (1, 4096, 32, 128, 128, 16, 2.42, 4.48, None, "14,33"),
-    (1, 4096, 32, 128, 64, 32, 2.69, 4.53, 7.37, "15,34,64"),
-    (2, 4096, 32, 128, 64, 16, 5.28, 8.95, 14.42, "16,35,65"),
+# The reference's published V2 numbers (V2_BENCHMARK.md; bf16, threshold 1.0,
+# q_block_size = score_block_size, qblock_topk = q_block_size * K).
+# Forward rows, RTX 4090: (B, N, H, D, b, K, {stage: (published ms, line)}).
+V2_FWD_ROWS = [
+    (1, 2048, 32, 128, 64, 16, {"score": (0.68, 11), "attn_fwd": (1.24, 30)}),
+    (1, 4096, 32, 128, 64, 16, {"score": (2.67, 12), "attn_fwd": (4.44, 31), "end_to_end": (7.26, 62)}),
+    (1, 8192, 32, 128, 64, 16, {"score": (10.56, 13), "attn_fwd": (17.37, 32), "end_to_end": (28.15, 63)}),
+    (1, 4096, 32, 128, 128, 16, {"score": (2.42, 14), "attn_fwd": (4.48, 33)}),
+    (1, 4096, 32, 128, 64, 32, {"score": (2.69, 15), "attn_fwd": (4.53, 34), "end_to_end": (7.37, 64)}),
+    (2, 4096, 32, 128, 64, 16, {"score": (5.28, 16), "attn_fwd": (8.95, 35), "end_to_end": (14.42, 65)}),
+    (1, 2016, 32, 128, 48, 16, {"score": (0.98, 17), "attn_fwd": (1.98, 36)}),
+    (1, 4032, 32, 128, 48, 16, {"score": (3.82, 18), "attn_fwd": (7.42, 37), "end_to_end": (11.25, 66)}),
+    (1, 3008, 32, 128, 64, 16, {"score": (1.57, 19), "attn_fwd": (2.55, 38)}),
+    (1, 5056, 32, 128, 64, 16, {"score": (4.63, 20), "attn_fwd": (6.70, 39), "end_to_end": (11.42, 67)}),
+    (1, 4096, 4, 64, 64, 16, {"score": (0.28, 21), "attn_fwd": (0.38, 40)}),
+    (1, 4096, 32, 64, 64, 16, {"score": (2.10, 22), "attn_fwd": (2.28, 41), "end_to_end": (4.47, 68)}),
 ]
+# Sparse attention forward over D, RTX 3090: B1 H8 N2048 b64 K8: (D, published ms, line).
+V2_ATTN_D_ROWS = [(32, 0.065, 49), (48, 0.140, 50), (64, 0.108, 51), (80, 0.203, 52), (96, 0.154, 53),
+                  (128, 0.182, 54)]
+# Backward (fwd + bwd minus fwd), RTX 3090, q and KV blocks of 64:
+# (N, H, D, K, dtype, published ms, line).
+V2_BWD_ROWS = (
+    [(n, h, 128, 8, "bf16", ms, ln) for n, h, ms, ln in
+     ((256, 8, 2.09, 78), (512, 8, 2.06, 79), (1024, 8, 1.93, 80), (2048, 8, 1.73, 81), (4096, 4, 1.96, 82),
+      (8192, 2, 1.47, 83))]
+    + [(2048, 8, 128, kk, "bf16", ms, ln) for kk, ms, ln in
+       ((1, 1.99, 89), (2, 2.01, 90), (4, 1.95, 91), (8, 1.94, 92), (16, 1.91, 93), (32, 1.56, 94))]
+    + [(2048, 8, d, 8, "bf16", ms, ln) for d, ms, ln in
+       ((32, 2.03, 100), (48, 2.97, 101), (64, 2.04, 102), (80, 2.95, 103), (96, 1.20, 104), (128, 1.94, 105),
+        (160, 1.88, 106), (256, 1.57, 107))]
+    + [(2048, 8, 128, 8, dt, ms, ln) for dt, ms, ln in (("bf16", 1.76, 113), ("fp16", 1.95, 114))]
+)
+
+
+def _median_ms(fn, stream, reps=5):
+    import torch
+
+    fn()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    return sorted(ts)[len(ts) // 2]
 
 
 def bench_v2_rows(dev, stream):
-    """The reference's published V2 shapes: flash_topk_score (scoring + top-k),
-    flash_topk_attn forward given the merged indices, and the end-to-end
-    forward pipeline (score + merge + attention), HIP events, median of 5."""
+    """Every shape of the reference's V2_BENCHMARK.md: flash_topk_score (scoring
+    + top-k), flash_topk_attn forward given the merged indices, the end-to-end
+    forward (score + merge + attention) and the backward (forward + backward
+    minus forward, as the reference measures it); synthetic N(0, 1) inputs,
+    HIP events, median of 5.  One entry per (shape, stage) with the published
+    time and the GPU it was measured on."""
     import torch
 
     import flash_topk_attn_v2 as fta
 
     res = []
-    for B, N, H, D, b, K, r_sc, r_at, r_e2e, lines in V2_ROWS:
-        q, k, v = make_inputs(B, N, H, D, False, 11, dev)
-        # q_block_size = score_block_size as the reference's table states; its
+
+    def prepare(B, N, H, D, b, K, dtype=None):
+        q, k, v = make_inputs(B, N, H, D, False, 11, dev, dtype=dtype)
+        # q_block_size = score_block_size as the reference's tables state; its
         # flash_sparse_attn accepts q blocks of at most 64 (sparse_attn.py:279),
         # so the 128-token row uses 64
         g = min(b, 64)
         W = g * K
-
-        def score():
-            return fta.flash_topk_score(q, k, H, b, K, (0, 0), 1.0)
-
-        idx, raw, avg = score()
+        idx, _, avg = fta.flash_topk_score(q, k, H, b, K, (0, 0), 1.0)
         merged, counts, _ = fta.build_qblock_topk_indices(idx, g, (0, 0), avg, W)
+        return q, k, v, g, W, merged, counts
 
-        def attn():
-            return fta.flash_topk_attn(q, k, v, merged, counts, H, g, b)
+    def entry(cfg, stage, ms, flop, ref, hw):
+        res.append({"config": cfg, "stage": stage, "ms": round(ms, 4),
+                    "tflops": round(flop / ms / 1e9, 1) if flop else None, "reference_ms": ref[0],
+                    "reference_hw": hw, "reference_source": f"V2_BENCHMARK.md:{ref[1]}"})
 
-        def e2e():
-            i, _, a = score()
-            m, c, _ = fta.build_qblock_topk_indices(i, g, (0, 0), a, W)
-            return fta.flash_topk_attn(q, k, v, m, c, H, g, b)
+    with torch.no_grad():
+        for B, N, H, D, b, K, refs in V2_FWD_ROWS:
+            q, k, v, g, W, merged, counts = prepare(B, N, H, D, b, K)
+            P = float(g * b * counts.sum().item())  # (query, key) pairs of the merged lists
+            cfg = f"B{B} N{N} H{H} D{D} b{b} K{K} g{g} bf16"
+            fns = {
+                "score": (lambda: fta.flash_topk_score(q, k, H, b, K, (0, 0), 1.0), 2.0 * B * H * N * N * D),
+                "attn_fwd": (lambda: fta.flash_topk_attn(q, k, v, merged, counts, H, g, b), 4.0 * D * P),
+            }
 
-        row = {"config": f"B{B} N{N} H{H} D{D} b{b} K{K} g{g} bf16", "reference_source": f"V2_BENCHMARK.md:{lines}"}
-        P = float(g * b * counts.sum().item())  # valid (query, key) pairs of the merged lists
-        f = {"score": 2.0 * B * H * N * N * D, "attn_fwd": 4.0 * D * P}
-        f["end_to_end"] = f["score"] + f["attn_fwd"]
-        for name, fn, ref in (("score", score, r_sc), ("attn_fwd", attn, r_at), ("end_to_end", e2e, r_e2e)):
-            ts = []
+            def e2e():
+                i, _, a = fta.flash_topk_score(q, k, H, b, K, (0, 0), 1.0)
+                m, c, _ = fta.build_qblock_topk_indices(i, g, (0, 0), a, W)
+                return fta.flash_topk_attn(q, k, v, m, c, H, g, b)
+
+            fns["end_to_end"] = (e2e, fns["score"][1] + fns["attn_fwd"][1])
+            for stage, ref in refs.items():
+                fn, flop = fns[stage]
+                entry(cfg, stage, _median_ms(fn, stream), flop, ref, "RTX 4090")
+            del q, k, v, merged, counts
+        for D, ref_ms, line in V2_ATTN_D_ROWS:
+            q, k, v, g, W, merged, counts = prepare(1, 2048, 8, D, 64, 8)
+            P = float(g * 64 * counts.sum().item())
+            ms = _median_ms(lambda: fta.flash_topk_attn(q, k, v, merged, counts, 8, g, 64), stream)
+            entry(f"B1 N2048 H8 D{D} b64 K8 g64 bf16", "attn_fwd", ms, 4.0 * D * P, (ref_ms, line), "RTX 3090")
+            del q, k, v, merged, counts
+    for N, H, D, K, dt, ref_ms, line in V2_BWD_ROWS:
+        dtype = torch.float16 if dt == "fp16" else torch.bfloat16
+        q, k, v, g, W, merged, counts = prepare(1, N, H, D, 64, K, dtype)
+        P = float(g * 64 * counts.sum().item())
+        ql, kl, vl = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        do = torch.randn_like(q)
+
+        def fwd():
             with torch.no_grad():
-                fn()
-                for _ in range(5):
-                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    e0.record(stream)
-                    fn()
-                    e1.record(stream)
-                    torch.cuda.synchronize()
-                    ts.append(e0.elapsed_time(e1))
-            row[f"{name}_ms"] = round(sorted(ts)[2], 4)
-            row[f"{name}_tflops"] = round(f[name] / sorted(ts)[2] / 1e9, 1)
-            row[f"{name}_reference_ms_rtx4090"] = ref
-        res.append(row)
-        del q, k, v, idx, raw, avg, merged, counts
+                return fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, 64)
+
+        def fwd_bwd():
+            o, _ = fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, 64)
+            o.backward(do)
+
+        ms = _median_ms(fwd_bwd, stream) - _median_ms(fwd, stream)
+        entry(f"B1 N{N} H{H} D{D} b64 K{K} g64 {dt}", "attn_bwd", ms, 10.0 * D * P, (ref_ms, line), "RTX 3090")
+        del q, k, v, ql, kl, vl, do, merged, counts
     return res
 
 
@@ -412,7 +472,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the C3-iid, C2, C4, C5 and V1 rows")
     ap.add_argument("--cpu-heads", type=int, default=2)
-    ap.add_argument("--only", choices=["score", "scorer", "topk", "merge", "fwd", "bwd", "dq", "dkv", "copy", "v1"],
+    ap.add_argument("--only", choices=["score", "scorer", "topk", "merge", "fwd", "bwd", "dq", "dkv", "copy", "v1",
+                                       "v2"],
                     default=None, help="profiling aid: run one stage of the C3 step --steps times and exit")
     ap.add_argument("--iid", action="store_true",
                     help="with --only: the C3-iid variant (iid q/k/v, threshold 1.0, qblock_topk 512)")
@@ -432,6 +493,9 @@ def main():
             bench_v1(dev, torch.cuda.current_stream(dev))
         torch.cuda.synchronize()
         print(json.dumps({"only": "v1", "steps": args.steps}), flush=True)
+        return
+    if args.only == "v2":  # the reference's V2 shapes alone
+        print(json.dumps({"only": "v2", "rows": bench_v2_rows(dev, torch.cuda.current_stream(dev))}), flush=True)
         return
     B, N, H, D, b, topk, thr, g, W = 1, 32768, 32, 128, 64, 16, 0.9, 32, 256
     stream = torch.cuda.current_stream(dev)

@@ -64,6 +64,12 @@ struct AttnArgs {
     int Hk, G;  // K/V heads and query heads per K/V head (G = H / Hk; 1 without GQA)
     float c, scale;
     int wg_per_bh, total;
+    // forward split over the union walk (nsplit > 1, small grids): partial
+    // unnormalised O [nsplit][nbh][npq][Dk] and (m, L) [nsplit][nbh][npq], by
+    // padded query position, merged by fta_fwd_combine_kernel
+    int nsplit, nbh, npq;
+    float* part_o;
+    float2* part_ml;
 };
 
 // Bits [lo, hi) of a 32-bit mask; lo and hi may lie anywhere (they are clamped
@@ -406,7 +412,10 @@ __device__ __forceinline__ void fta_pin_frags(uint4 (&f)[2][KS]) {
         }
 }
 
-template <int DT, int D, int NW>
+// SPLIT: workgroup (tiles, part sp) walks union positions [sp U / nsplit,
+// (sp + 1) U / nsplit) of each mask segment and writes its unnormalised partial
+// output, running max and sum instead of o and lse.
+template <int DT, int D, int NW, bool SPLIT>
 __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArgs a) {
     using E = Elem<DT>;
     using Sh = FwdPipeShape<D, NW>;
@@ -421,9 +430,18 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
     __shared__ int s_tmp[8];
 
     const int wgi = fta_xcd_remap(blockIdx.x, a.total);
-    const int hp = wgi / a.wg_per_bh;                     // head position
+    int hp, wq, sp = 0;  // head position, tile group, part
+    if constexpr (SPLIT) {
+        const int per = a.wg_per_bh * a.nsplit;
+        hp = wgi / per;
+        const int r = wgi - hp * per;
+        wq = r / a.nsplit;
+        sp = r - wq * a.nsplit;
+    } else {
+        hp = wgi / a.wg_per_bh;
+        wq = wgi - hp * a.wg_per_bh;
+    }
     const int bh = a.head_perm ? a.head_perm[hp] : hp;  // (b, h)
-    const int wq = wgi - hp * a.wg_per_bh;
     const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -472,13 +490,19 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
     for (int seg0 = 0; seg0 < a.Mkv; seg0 += kSeg) {
         const int segn = min(kSeg, a.Mkv - seg0);
         const int U = fta_build_q_masks<T>(a, bh, p0, seg0, segn, sMask, sList, s_tmp);
-        if (U == 0) continue;
-        const int iters = U * nch;
+        int u_lo = 0, u_n = U;  // this part's union positions (workgroup-uniform)
+        if constexpr (SPLIT) {
+            u_lo = (U * sp) / a.nsplit;
+            u_n = (U * (sp + 1)) / a.nsplit - u_lo;
+        }
+        // no wave reads sMask / sList below when the part is empty
+        if (u_n == 0) continue;
+        const int iters = u_n * nch;
 
         // gather chunk `it` (64 keys of union block it / nch) into stage buffer st
         auto issue = [&](int st, int it) {
             const uint32_t sb = lds0 + st * Sh::STAGE_B;
-            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int u = u_lo + it / nch, ch = it - (it / nch) * nch;
             const int m = __builtin_amdgcn_readfirstlane(seg0 + sList[u]);
             const int kb = m * a.kvb - a.kv_pad + ch * 64;
             const int rem = a.kvb - ch * 64;
@@ -517,7 +541,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
             __syncthreads();  // chunk it visible; every wave is past chunk it - 1
             if (it + NST - 1 < iters) issue(cur == 0 ? NST - 1 : cur - 1, it + NST - 1);
 
-            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int u = u_lo + it / nch, ch = it - (it / nch) * nch;
             const int ml = sList[u];
             const int m = seg0 + ml;
             const int kb = m * a.kvb - a.kv_pad + ch * 64;
@@ -613,6 +637,21 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
 
     // finalize: O = O^T / L, lse = ln(sum) + max
     const float L = l_run + fta_xor32(l_run);
+    if constexpr (SPLIT) {
+        // the part's unnormalised O, its running max and sum, by padded position
+        const int p = p0 + 32 * wave + (lane & 31);
+        if (p >= a.npq) return;
+        const int64_t row = ((int64_t)sp * a.nbh + bh) * a.npq + p;
+        if (lane < 32) a.part_ml[row] = make_float2(m_run, L);
+        float* po = a.part_o + row * D;
+#pragma unroll
+        for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; i += 4)
+                *reinterpret_cast<float4*>(po + dt * 32 + c_row(i, lane)) =
+                    make_float4(oacc[dt][i], oacc[dt][i + 1], oacc[dt][i + 2], oacc[dt][i + 3]);
+        return;
+    }
     const float inv = (L > 0.f) ? 1.f / L : 0.f;
     const int t = p0 + 32 * wave + (lane & 31) - a.q_pad;
     if (t < 0 || t >= a.N) return;
@@ -631,6 +670,55 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_fwd_pipe_kernel(AttnArg
                 *reinterpret_cast<uint2*>(op + d) = w;
             }
         }
+}
+
+// Merge of the forward's split parts: one thread per (b·h, query, 8 columns).
+// m = max over the parts with a positive sum; O = sum_p O_p 2^{c (m_p - m)} / L,
+// L = sum_p L_p 2^{c (m_p - m)}, lse = (c m + log2 L) ln 2 (-inf, O = 0 for a
+// query with no selected key, as in the unsplit kernel).
+template <int DT, int D>
+__global__ __launch_bounds__(256) void fta_fwd_combine_kernel(AttnArgs a) {
+    using E = Elem<DT>;
+    constexpr int DC = D / 8;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)a.nbh * a.N * DC) return;
+    const int dc = (int)(idx % DC);
+    const int64_t rest = idx / DC;
+    const int t = (int)(rest % a.N), bh = (int)(rest / a.N);
+    const int d0 = dc * 8;
+    if (d0 >= a.Dreal && dc != 0) return;
+    const int p = t + a.q_pad;
+    float m = -FTA_INF;
+    for (int sp = 0; sp < a.nsplit; ++sp) {
+        const float2 ml = a.part_ml[((int64_t)sp * a.nbh + bh) * a.npq + p];
+        if (ml.y > 0.f) m = fmaxf(m, ml.x);
+    }
+    float L = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < a.nsplit; ++sp) {
+        const int64_t row = ((int64_t)sp * a.nbh + bh) * a.npq + p;
+        const float2 ml = a.part_ml[row];
+        if (!(ml.y > 0.f)) continue;
+        const float w = fta_exp2((ml.x - m) * a.c);
+        L = fmaf(ml.y, w, L);
+        const float4 x0 = *reinterpret_cast<const float4*>(a.part_o + row * D + d0);
+        const float4 x1 = *reinterpret_cast<const float4*>(a.part_o + row * D + d0 + 4);
+        o[0] = fmaf(x0.x, w, o[0]);
+        o[1] = fmaf(x0.y, w, o[1]);
+        o[2] = fmaf(x0.z, w, o[2]);
+        o[3] = fmaf(x0.w, w, o[3]);
+        o[4] = fmaf(x1.x, w, o[4]);
+        o[5] = fmaf(x1.y, w, o[5]);
+        o[6] = fmaf(x1.z, w, o[6]);
+        o[7] = fmaf(x1.w, w, o[7]);
+    }
+    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    if (dc == 0)
+        a.lse[(int64_t)bh * a.N + t] = (L > 0.f) ? fmaf(m, a.c, fta_log2(L)) * 0.69314718055994531f : -FTA_INF;
+    if (d0 >= a.Dreal) return;
+    const float inv = (L > 0.f) ? 1.f / L : 0.f;
+    uint16_t* op = a.out0 + b * a.o0_sb + h * a.o0_sh + (int64_t)t * a.o0_sn + d0;
+    *reinterpret_cast<uint2*>(op) = make_uint2(E::pack2(o[0] * inv, o[1] * inv), E::pack2(o[2] * inv, o[3] * inv));
+    *reinterpret_cast<uint2*>(op + 4) = make_uint2(E::pack2(o[4] * inv, o[5] * inv), E::pack2(o[6] * inv, o[7] * inv));
 }
 
 // ----------------------------------------------------------------------------
@@ -1797,7 +1885,9 @@ int geometry(int B, int H, int N, int D, int g, int kvb, int qph, int qpt, int k
     if (nq % g) return fta::arg_error("sparse_attn: q_pad_head + N + q_pad_tail must be divisible by q_block_size");
     if (nk % kvb) return fta::arg_error("sparse_attn: kv_pad_head + N + kv_pad_tail must be divisible by kv_block_size");
     if (nq / g != QM) return fta::arg_error("sparse_attn: merged_indices dim 2 must equal QM");
-    o->Dk = fta::kernel_head_dim(D);
+    // D <= 128 runs on the 64- or 128-column kernels (columns past D meet zero
+    // Q / dO columns and are never stored)
+    o->Dk = (D <= 64) ? 64 : (D <= 128) ? 128 : fta::kernel_head_dim(D);
     o->Mkv = (int)(nk / kvb);
     o->QM = QM;
     o->nch = (kvb + 63) / 64;
@@ -1837,15 +1927,19 @@ int launch_fwd_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
         break;
         FTA_FWD(32, 1, 8)
         case 64:
-            if (pipe_ok)
-                hipLaunchKernelGGL((fta_sparse_fwd_pipe_kernel<DT, 64, 8>), dim3(grid), dim3(512), 0, st, a);
+            if (pipe_ok && a.nsplit > 1)
+                hipLaunchKernelGGL((fta_sparse_fwd_pipe_kernel<DT, 64, 8, true>), dim3(grid), dim3(512), 0, st, a);
+            else if (pipe_ok)
+                hipLaunchKernelGGL((fta_sparse_fwd_pipe_kernel<DT, 64, 8, false>), dim3(grid), dim3(512), 0, st, a);
             else
                 hipLaunchKernelGGL((fta_sparse_fwd_kernel<DT, 64, 1, 8>), dim3(grid), dim3(512), 0, st, a);
             break;
         FTA_FWD(96, 1, 8)
         case 128:
-            if (pipe_ok)
-                hipLaunchKernelGGL((fta_sparse_fwd_pipe_kernel<DT, 128, 8>), dim3(grid), dim3(512), 0, st, a);
+            if (pipe_ok && a.nsplit > 1)
+                hipLaunchKernelGGL((fta_sparse_fwd_pipe_kernel<DT, 128, 8, true>), dim3(grid), dim3(512), 0, st, a);
+            else if (pipe_ok)
+                hipLaunchKernelGGL((fta_sparse_fwd_pipe_kernel<DT, 128, 8, false>), dim3(grid), dim3(512), 0, st, a);
             else
                 hipLaunchKernelGGL((fta_sparse_fwd_kernel<DT, 128, 1, 8>), dim3(grid), dim3(512), 0, st, a);
             break;
@@ -1855,7 +1949,15 @@ int launch_fwd_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
         default:
             return fta::arg_error("sparse_attn: unsupported head dim");
     }
-    return fta::check_launch("fta_sparse_fwd_kernel");
+    int rc = fta::check_launch("fta_sparse_fwd_kernel");
+    if (rc != FTA_OK || !(pipe_ok && a.nsplit > 1)) return rc;
+    const int64_t threads = (int64_t)a.nbh * a.N * (Dk / 8);
+    const unsigned blocks = (unsigned)((threads + 255) / 256);
+    if (Dk == 64)
+        hipLaunchKernelGGL((fta_fwd_combine_kernel<DT, 64>), dim3(blocks), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((fta_fwd_combine_kernel<DT, 128>), dim3(blocks), dim3(256), 0, st, a);
+    return fta::check_launch("fta_fwd_combine_kernel");
 }
 
 template <int DT>
@@ -1956,6 +2058,24 @@ size_t sel_bytes(int B, int H, const Geo& G) {
 // and the 64 partial counts per head they are summed from
 size_t fwd_bytes(int B, int H) { return fta::align_up((size_t)B * H * (2 + 64) * sizeof(int32_t)); }
 
+// Forward parts per workgroup.  A grid of fewer than 128 workgroups (under half
+// the CUs) is bound by each workgroup's sequential union walk, not by the chip:
+// the pipelined kernel then splits every walk into up to 4 parts (256 / grid)
+// and fta_fwd_combine_kernel merges them.
+int fwd_nsplit(int B, int H, const Geo& G) {
+    if (!(G.Dk == 64 || G.Dk == 128) || G.Mkv < 8) return 1;
+    const int64_t wgs = (int64_t)((G.Npq + 255) / 256) * B * H;
+    if (wgs >= 128) return 1;
+    const int64_t ns = 256 / wgs;
+    return (int)(ns > 4 ? 4 : ns < 2 ? 2 : ns);
+}
+// the parts' (m, L) and unnormalised O, after fwd_bytes in the workspace
+size_t split_bytes(int B, int H, const Geo& G, int ns) {
+    if (ns <= 1) return 0;
+    const size_t rows = (size_t)ns * B * H * G.Npq;
+    return fta::align_up(rows * sizeof(float2)) + fta::align_up(rows * G.Dk * sizeof(float));
+}
+
 // the backward workspace: membership bitmap, lse in log2 units, dK/dV launch order (KV blocks, then heads)
 size_t bwd_bytes(int B, int H, int N, const Geo& G) {
     return sel_bytes(B, H, G) + fta::align_up((size_t)B * H * N * sizeof(float)) +
@@ -1974,7 +2094,19 @@ size_t fta_sparse_attn_fwd_workspace_size(int B, int H, int N, int D, int q_bloc
     if (geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
                  &G) != FTA_OK)
         return 0;
-    return fwd_bytes(B, H);  // per-head work and XCD placement of the heads
+    // per-head work and XCD placement of the heads, then the split parts
+    return fwd_bytes(B, H) + split_bytes(B, H, G, fwd_nsplit(B, H, G));
+}
+
+int fta_sparse_attn_fwd_splits(int B, int H, int N, int D, int q_block_size, int kv_block_size, int q_pad_head,
+                               int q_pad_tail, int kv_pad_head, int kv_pad_tail) {
+    Geo G;
+    const int64_t nq = (int64_t)q_pad_head + N + q_pad_tail;
+    const int QM = q_block_size > 0 ? (int)(nq / q_block_size) : 0;
+    if (geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
+                 &G) != FTA_OK)
+        return 0;
+    return fwd_nsplit(B, H, G);
 }
 
 int fta_sparse_attn_fwd_gqa(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -1992,9 +2124,12 @@ int fta_sparse_attn_fwd_gqa(const void* q, const int64_t* q_strides, const void*
     if (W <= 0) return fta::arg_error("sparse_attn: qblock_topk must be positive");
     hipStream_t st = (hipStream_t)stream;
     AttnArgs a = {};
+    const int T = (G.Dk <= 160) ? 8 : 4;  // query tiles per workgroup
+    const int64_t wgs = (int64_t)((G.Npq + 32 * T - 1) / (32 * T)) * B * H;
     // XCD placement of the heads by their work (only with a workspace: callers
-    // that pass none keep the natural order)
-    if (workspace != nullptr && workspace_bytes >= fwd_bytes(B, H)) {
+    // that pass none keep the natural order; and only when the workgroups do not
+    // all run at once, one per CU, where the placement cannot change the time)
+    if (workspace != nullptr && workspace_bytes >= fwd_bytes(B, H) && wgs > 256) {
         int32_t* head_work = (int32_t*)workspace;
         int32_t* head_perm = head_work + B * H;
         if ((rc = fta::launch_head_order_merged(merged_indices, B * H, QM, W, G.Mkv, max(1, 256 / q_block_size), head_work, head_perm, st)) !=
@@ -2024,9 +2159,21 @@ int fta_sparse_attn_fwd_gqa(const void* q, const int64_t* q_strides, const void*
     fill_common(a, H, N, D, q_block_size, kv_block_size, q_pad_head, kv_pad_head, scale, G);
     a.Hk = Hk;
     a.G = H / Hk;
-    const int T = (G.Dk <= 160) ? 8 : 4;  // query tiles per workgroup
     a.wg_per_bh = (G.Npq + 32 * T - 1) / (32 * T);
-    a.total = a.wg_per_bh * B * H;
+    // split walks (small grids, pipelined kernel, workspace for the parts)
+    const int ns = fwd_nsplit(B, H, G);
+    const bool split = ns > 1 && workspace != nullptr &&
+                       workspace_bytes >= fwd_bytes(B, H) + split_bytes(B, H, G, ns) && k_strides[2] <= (1 << 24) &&
+                       v_strides[2] <= (1 << 24);
+    a.nsplit = split ? ns : 1;
+    a.nbh = B * H;
+    a.npq = G.Npq;
+    if (split) {
+        const size_t rows = (size_t)ns * B * H * G.Npq;
+        a.part_ml = (float2*)((char*)workspace + fwd_bytes(B, H));
+        a.part_o = (float*)((char*)a.part_ml + fta::align_up(rows * sizeof(float2)));
+    }
+    a.total = a.wg_per_bh * B * H * a.nsplit;
     if (dtype == FTA_DTYPE_BF16) return launch_fwd_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);
     if (dtype == FTA_DTYPE_F16) return launch_fwd_dt<FTA_DTYPE_F16>(a, G.Dk, a.total, st);
     return fta::arg_error("sparse_attn: dtype must be bf16 or fp16");

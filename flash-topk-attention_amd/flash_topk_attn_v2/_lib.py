@@ -52,6 +52,7 @@ _SIGNATURES = {
     "fta_build_reverse_indices": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p, _sz, _p]),
     "fta_sort_by_count": (_i, [_p, _i64, _p, _p, _p]),
     "fta_sparse_attn_fwd_workspace_size": (_sz, [_i] * 10),
+    "fta_sparse_attn_fwd_splits": (_i, [_i] * 10),
     "fta_sparse_attn_fwd": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _p, _i, _i, _i, _i, _i, _i,
                                  _i, _i, _f, _p, _i64p, _p, _p, _sz, _p]),
     "fta_sparse_attn_fwd_gqa": (_i, [_p, _i64p, _p, _i64p, _p, _i64p, _i, _i, _i, _i, _i, _i, _p, _i, _i, _i, _i,

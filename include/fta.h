@@ -239,6 +239,19 @@ size_t fta_sparse_attn_fwd_workspace_size(int B, int H, int N, int D, int q_bloc
                                           int kv_pad_head, int kv_pad_tail);
 
 /*
+ * Parts per workgroup walk of the forward with its workspace for this
+ * geometry (0 for an invalid one): 1, or 2-4 when the grid has fewer than 128
+ * workgroups and D <= 128.  Then each workgroup's walk over the union of its
+ * q-blocks' lists (ascending, per 512-block segment) is split into that many
+ * contiguous ranges, each with its own online-softmax anchor, and a combine
+ * kernel merges the parts' (O, max, sum).  No counterpart in the reference
+ * (its forward is never split); exposed so that callers and tests can tell
+ * which schedule rounds P.
+ */
+int fta_sparse_attn_fwd_splits(int B, int H, int N, int D, int q_block_size, int kv_block_size,
+                               int q_pad_head, int q_pad_tail, int kv_pad_head, int kv_pad_tail);
+
+/*
  * Block-sparse attention forward over the merged KV-block lists
  * (merged_indices [B][H][QM][W], -1 entries ignored, order irrelevant):
  * o [B][N][H][D] (strided, same dtype) and lse [B][H][N] (natural log,
@@ -248,8 +261,10 @@ size_t fta_sparse_attn_fwd_workspace_size(int B, int H, int N, int D, int q_bloc
  * (flash_topk_attn_v2/sparse_attn_cuda.py:42-110); lse = softmax_max + softmax_lse
  * of the reference (flash_topk_attn_v2/sparse_attn.py:391).
  * The workspace (fta_sparse_attn_fwd_workspace_size bytes: per-head work and
- * the XCD placement of the heads) is optional: with workspace == NULL or too
- * few bytes the heads run in natural order, with the same results.
+ * the XCD placement of the heads, and on small grids the split walks' partial
+ * outputs, see fta_sparse_attn_fwd_splits) is optional: with workspace == NULL
+ * or too few bytes the heads run in natural order and unsplit (the same o and
+ * lse up to the rounding of P before P.V, which the split moves).
  */
 int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k,
                         const int64_t* k_strides, const void* v, const int64_t* v_strides,

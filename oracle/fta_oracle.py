@@ -76,8 +76,9 @@ import numpy as np
 
 def round_to(x: np.ndarray, kind: Optional[str]) -> np.ndarray:
     """x rounded to bfloat16 / float16 (round to nearest, ties to even), as
-    float64; ``kind`` None returns x unchanged."""
-    if kind is None:
+    float64; ``kind`` None or "f64" returns x unchanged ("f64" as the
+    ``round_p`` of sparse_attn runs a kernel's schedule without rounding)."""
+    if kind is None or kind == "f64":
         return x
     if kind == "fp16":  # from float32, as the kernels round their fp32 values
         with np.errstate(over="ignore"):
@@ -321,6 +322,14 @@ def _online_pv(s: np.ndarray, v: np.ndarray, chunk: np.ndarray, c: float, round_
                anchor_slack: float) -> np.ndarray:
     """o = sum_j round(P_j) v_j / sum_j P_j with P anchored to a lazily updated
     running maximum per row (see sparse_attn); s are the unscaled scores."""
+    acc, l, _ = _online_pv_part(s, v, chunk, c, round_p, anchor_slack)
+    return acc / l[:, None]
+
+
+def _online_pv_part(s: np.ndarray, v: np.ndarray, chunk: np.ndarray, c: float, round_p: str,
+                    anchor_slack: float) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """The unnormalised (sum_j round(P_j) v_j, sum_j P_j, final anchor m) of
+    _online_pv."""
     rows = s.shape[0]
     m = np.full(rows, -np.inf)
     acc = np.zeros((rows, v.shape[1]))
@@ -339,7 +348,34 @@ def _online_pv(s: np.ndarray, v: np.ndarray, chunk: np.ndarray, c: float, round_
         p = np.exp2(sc * c - np.where(np.isfinite(m), m * c, 0.0)[:, None])
         l += p.sum(-1)
         acc += round_to(p, round_p) @ v[sel]
-    return acc / l[:, None]
+    return acc, l, m
+
+
+def _split_parts(merged_bh: np.ndarray, q_block_size: int, N: int, q_pad_head: int, Mkv: int, splits: int,
+                 p0: int, wg_rows: int = 256, seg: int = 512) -> dict:
+    """Part of each KV block in the split forward walk of the workgroup whose
+    padded query rows start at p0 (fta_sparse_attn_fwd_splits > 1): the union
+    of the blocks listed by the q-blocks with valid rows in [p0, p0 + wg_rows),
+    ascending per segment of `seg` blocks, cut into `splits` contiguous ranges
+    of union positions [U sp / splits, U (sp + 1) / splits)."""
+    QM = merged_bh.shape[0]
+    g = q_block_size
+    pend = p0 + wg_rows
+    union = set()
+    for qb in range(p0 // g, min((pend - 1) // g, QM - 1) + 1):
+        lo = max(qb * g, p0, q_pad_head)
+        hi = min(qb * g + g, pend, q_pad_head + N)
+        if lo >= hi:
+            continue
+        union.update(int(m) for m in merged_bh[qb] if 0 <= m < Mkv)
+    part = {}
+    for seg0 in range(0, Mkv, seg):
+        lst = sorted(m for m in union if seg0 <= m < seg0 + seg)
+        U = len(lst)
+        for sp in range(splits):
+            for pos in range((U * sp) // splits, (U * (sp + 1)) // splits):
+                part[lst[pos]] = sp
+    return part
 
 
 def sparse_attn(
@@ -356,6 +392,7 @@ def sparse_attn(
     qblocks: Optional[Sequence[Tuple[int, int, int]]] = None,
     round_p: Optional[str] = None,
     anchor_slack: float = 8.0,
+    splits: int = 1,
 ) -> Tuple[np.ndarray, np.ndarray]:
     """o [B, N, C] float64 and natural-log lse [B, H, N] (−inf and o = 0 for
     rows with no candidate token).  ``qblocks`` restricts the computation to the
@@ -370,7 +407,11 @@ def sparse_attn(
     ``anchor_slack`` in log2 units (this build's kernels: 8; 0 re-anchors
     whenever the maximum grows, as the reference's kernel does,
     v2/csrc/sparse_attn_kernel.cuh:145-160), and the accumulators are scaled by
-    2^(c m_old - c m_new) then."""
+    2^(c m_old - c m_new) then.  ``splits`` > 1 models this build's split
+    forward (small grids, fta_sparse_attn_fwd_splits): each 256-row workgroup's
+    union walk is cut into that many parts (_split_parts), each part runs the
+    schedule above from its own anchor, and the parts are merged as
+    o = sum_p acc_p 2^(c m_p - c m) / sum_p l_p 2^(c m_p - c m), m = max m_p."""
     B, N, C = q.shape
     H = num_heads
     D = C // H
@@ -399,10 +440,38 @@ def sparse_attn(
         if round_p is None:
             p = np.exp(s - row_lse[:, None])
             o[b, h, rs:re] = p @ v4[b, h, valid]
-        else:
+        elif splits <= 1:
             o[b, h, rs:re] = _online_pv(s / scale, v4[b, h, valid], _chunk_starts(ids[ids >= 0], N, kv_block_size,
                                                                                     kph),
                                         scale * math.log2(math.e), round_p, anchor_slack)
+        else:
+            c = scale * math.log2(math.e)
+            chunk = _chunk_starts(ids[ids >= 0], N, kv_block_size, kph)
+            tok_blk = (np.nonzero(valid)[0] + kph) // kv_block_size
+            Mkv = (kph + N + kv_padding[1]) // kv_block_size
+            r = rs
+            while r < re:  # rows of one workgroup share its parts
+                p0 = ((r + ph) // 256) * 256
+                r1 = min(re, p0 + 256 - ph)
+                part = _split_parts(merged_indices[b, h], q_block_size, N, ph, Mkv, splits, p0)
+                tp = np.array([part.get(int(m), -1) for m in tok_blk])
+                rows = r1 - r
+                acc = np.zeros((rows, D))
+                lsum = np.zeros(rows)
+                parts = []
+                for sp in range(splits):
+                    sel = tp == sp
+                    if sel.any():
+                        parts.append(_online_pv_part(s[r - rs:r1 - rs][:, sel] / scale, v4[b, h, valid][sel],
+                                                     chunk[sel], c, round_p, anchor_slack))
+                mm = np.max([np.where(l_ > 0, m_, -np.inf) for _, l_, m_ in parts], axis=0)
+                for a_, l_, m_ in parts:
+                    with np.errstate(invalid="ignore"):
+                        w = np.where(l_ > 0, np.exp2(c * (m_ - mm)), 0.0)
+                    acc += np.where(l_ > 0, w, 0.0)[:, None] * np.nan_to_num(a_)
+                    lsum += np.where(l_ > 0, w * l_, 0.0)
+                o[b, h, r:r1] = acc / lsum[:, None]
+                r = r1
         lse[b, h, rs:re] = row_lse
     return _from_bhnd(o), lse
 

@@ -42,6 +42,14 @@ def test_error_path_returns_status_without_gpu():
     assert rc == _lib.FTA_ERR_UNSUPPORTED
     assert L.fta_sparse_attn_bwd_workspace_size(1, 1, 100, 64, 32, 64, 0, 0, 0, 0) == 0  # 100 % 32 != 0
     assert L.fta_sparse_attn_fwd_workspace_size(1, 2, 128, 64, 32, 64, 0, 0, 0, 0) == 768  # head work, placement and 64 partial counts per head
+    # small grids split the forward's walks: 64 workgroups of 256 queries -> 4 parts,
+    # whose (m, L) float2 and unnormalised O (64 columns) follow, 256-byte aligned
+    assert L.fta_sparse_attn_fwd_splits(1, 8, 2048, 32, 64, 64, 0, 0, 0, 0) == 4
+    assert L.fta_sparse_attn_fwd_workspace_size(1, 8, 2048, 32, 64, 64, 0, 0, 0, 0) == 2304 + 4 * 8 * 2048 * (8 + 256)
+    assert L.fta_sparse_attn_fwd_splits(1, 32, 32768, 128, 32, 64, 0, 0, 0, 0) == 1  # 4096 workgroups
+    assert L.fta_sparse_attn_fwd_splits(1, 8, 2048, 160, 64, 64, 0, 0, 0, 0) == 1    # D > 128: not pipelined
+    assert L.fta_sparse_attn_fwd_splits(1, 2, 448, 64, 64, 64, 0, 0, 0, 0) == 1      # 7 KV blocks
+    assert L.fta_sparse_attn_fwd_splits(1, 2, 100, 64, 32, 64, 0, 0, 0, 0) == 0      # invalid geometry
     # backward scratch = membership bitmap [B*H][M_kv][ceil(QM/32)] uint32, lse in log2
     # units [B*H][N] fp32, dK/dV launch order [B*H][M_kv] int32, head work and head
     # placement [B*H] int32 each, each region 256-byte aligned

@@ -370,6 +370,8 @@ def check_attn_vs_oracle(q, k, v, do, o, lse, merged, H, g, b, qpad, kvpad, dt, 
     bound on a few elements, at most 1e-4 (o) / 5e-4 (gradients) of them."""
     from flash_topk_attn_v2.sparse_attn_bwd import preprocess_delta
 
+    from flash_topk_attn_v2 import _lib
+
     B, N, C = q.shape
     rk = round_kind(dt)
     qn, kn, vn = _rounded(q), _rounded(k), _rounded(v)
@@ -377,7 +379,9 @@ def check_attn_vs_oracle(q, k, v, do, o, lse, merged, H, g, b, qpad, kvpad, dt, 
         Dk = C // H
         kn = kn.reshape(B, N, -1, Dk).repeat(gqa_repeat, axis=2).reshape(B, N, C)
         vn = vn.reshape(B, N, -1, Dk).repeat(gqa_repeat, axis=2).reshape(B, N, C)
-    rr, rl = O.sparse_attn(qn, kn, vn, merged, H, g, b, None, qpad, kvpad, round_p=rk)
+    # the forward ran through the Python API (with its workspace): small grids split the walks
+    splits = _lib.lib().fta_sparse_attn_fwd_splits(B, H, N, C // H, g, b, qpad[0], qpad[1], kvpad[0], kvpad[1])
+    rr, rl = O.sparse_attn(qn, kn, vn, merged, H, g, b, None, qpad, kvpad, round_p=rk, splits=splits)
     assert_within(np32(o), rr, name="o vs rounding oracle")
     ro, _ = O.sparse_attn(qn, kn, vn, merged, H, g, b, None, qpad, kvpad)
     assert_close_frac(np32(o), ro, atol=2e-3, rtol=1e-2, name="o vs float64")
@@ -802,10 +806,11 @@ def test_head_placement_keeps_results(D):
     """The XCD head placement (forward with a workspace, combined backward) only
     reorders workgroups: o / lse equal the forward without a workspace, and the
     combined backward's dq / dk / dv equal the dQ and dK/dV entries run apart,
-    bit for bit, on heads of very unequal work (16 heads: placement active)."""
+    bit for bit, on heads of very unequal work (512 forward workgroups:
+    placement active, no split walks)."""
     from flash_topk_attn_v2 import _lib
 
-    B, H, N, g, b = 2, 8, 1024, 32, 64
+    B, H, N, g, b = 2, 16, 4096, 32, 64
     say(f"[head placement] B{B} H{H} N{N} D{D}")
     QM, M, W = N // g, N // b, 16
     rng = np.random.default_rng(5)
@@ -855,3 +860,84 @@ def test_head_placement_keeps_results(D):
     torch.cuda.synchronize()
     for a, c in zip(g1, g2):
         assert torch.equal(a, c)
+
+
+SPLIT_CASES = [
+    # B, H, Hk, N, D, g, b, q padding, kv padding, W
+    (1, 8, 8, 2048, 32, 64, 64, (0, 0), (0, 0), 32),
+    (1, 2, 2, 1000, 128, 32, 64, (8, 16), (24, 0), 24),
+    (2, 4, 2, 777, 96, 16, 64, (3, 4), (13, 42), 20),
+    (1, 3, 3, 640, 64, 64, 48, (0, 0), (0, 32), 16),
+    (1, 4, 1, 1536, 128, 32, 64, (0, 0), (0, 0), 8),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: f"B{c[0]}H{c[1]}k{c[2]}N{c[3]}D{c[4]}g{c[5]}b{c[6]}")
+def test_forward_split_walks(case):
+    """Small grids split each workgroup's union walk into parts merged by
+    fta_fwd_combine_kernel (forward with its workspace); without a workspace the
+    walk is not split.  Both must agree to fp32 rounding: lse to 1e-5 relative,
+    o to one bf16 rounding step; q-blocks with empty lists give o = 0 and lse =
+    -inf on both, and the split output also matches the float64 oracle."""
+    from flash_topk_attn_v2 import _lib
+
+    B, H, Hk, N, D, g, b, qpad, kvpad, W = case
+    say(f"[split walks] {case}")
+    QM = (qpad[0] + N + qpad[1]) // g
+    M = (kvpad[0] + N + kvpad[1]) // b
+    rng = np.random.default_rng(7)
+    merged = np.full((B, H, QM, W), -1, dtype=np.int32)
+    for bb in range(B):
+        for h in range(H):
+            for qm in range(QM):
+                n = 0 if (qm + h) % 7 == 3 else int(rng.integers(1, min(W, M) + 1))
+                merged[bb, h, qm, :n] = rng.permutation(M)[:n]
+    merged_t = torch.from_numpy(merged).cuda()
+    q = rand((B, N, H * D), 60, torch.bfloat16, "cuda")
+    k, v = (rand((B, N, Hk * D), 61 + i, torch.bfloat16, "cuda") for i in range(2))
+    L = _lib.lib()
+    qs, ks = _lib.i64arr([N * H * D, D, H * D]), _lib.i64arr([N * Hk * D, D, Hk * D])
+    geo = (B, H, N, D, g, b, qpad[0], qpad[1], kvpad[0], kvpad[1])
+    ws = _lib.workspace(L.fta_sparse_attn_fwd_workspace_size(*geo), "cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def fwd(w):
+        o = torch.full_like(q, 7.0)
+        lse = torch.full((B, H, N), 7.0, dtype=torch.float32, device="cuda")
+        rc = L.fta_sparse_attn_fwd_gqa(q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), ks,
+                                       _lib.dtype_code(q.dtype), B, H, Hk, N, D, merged_t.data_ptr(), QM, W, g, b,
+                                       qpad[0], qpad[1], kvpad[0], kvpad[1], D ** -0.5, o.data_ptr(), qs,
+                                       lse.data_ptr(), w.data_ptr() if w is not None else None,
+                                       w.numel() if w is not None else 0, stream)
+        _lib.check(rc, "fta_sparse_attn_fwd_gqa")
+        return o, lse
+
+    splits = L.fta_sparse_attn_fwd_splits(*geo)
+    assert splits > 1, "the case should split its walks"
+    o1, l1 = fwd(ws)
+    o2, l2 = fwd(None)
+    torch.cuda.synchronize()
+    l1n, l2n = l1.cpu().numpy(), l2.cpu().numpy()
+    assert np.array_equal(np.isinf(l1n), np.isinf(l2n))
+    fin = np.isfinite(l2n)
+    np.testing.assert_allclose(l1n[fin], l2n[fin], rtol=1e-5, atol=1e-5)
+    # empty lists: o = 0, lse = -inf
+    assert (~fin).any()
+    o1f, o2f = o1.float().cpu().numpy(), o2.float().cpu().numpy()
+    # each schedule against the rounding oracle of that schedule (every element), and
+    # both against the float64 oracle
+    qn, kn, vn = np32(q), np32(k), np32(v)
+    if Hk < H:  # the oracle takes one K/V head per query head
+        kn, vn = (x.reshape(B, N, Hk, D).repeat(H // Hk, axis=2).reshape(B, N, H * D) for x in (kn, vn))
+    rs_, rl = O.sparse_attn(qn, kn, vn, merged, H, g, b, None, qpad, kvpad, round_p="bf16", splits=splits)
+    assert_within(o1f, rs_, name="split o vs split rounding oracle")
+    r1_, _ = O.sparse_attn(qn, kn, vn, merged, H, g, b, None, qpad, kvpad, round_p="bf16")
+    assert_within(o2f, r1_, name="unsplit o vs rounding oracle")
+    ro, _ = O.sparse_attn(qn, kn, vn, merged, H, g, b, None, qpad, kvpad)
+    assert_close_frac(o1f, ro, atol=2e-3, rtol=1e-2, name="split o vs float64")
+    assert_close_frac(o2f, ro, atol=2e-3, rtol=1e-2, name="unsplit o vs float64")
+    empty = ~fin.transpose(0, 2, 1)  # [B, N, H]
+    assert (o1f.reshape(B, N, H, D)[empty] == 0).all()
+    rfin = np.isfinite(rl)
+    assert np.array_equal(rfin, fin)
+    np.testing.assert_allclose(l1n[fin], rl[fin], rtol=1e-4, atol=1e-4)

@@ -406,6 +406,65 @@ def test_online_softmax_schedule_without_rounding_is_softmax(slack):
     np.testing.assert_allclose(got, (w / w.sum(-1, keepdims=True)) @ v, rtol=1e-12, atol=1e-12)
 
 
+def test_split_parts_partition_the_workgroup_union():
+    """_split_parts (the split forward's parts): the parts of one workgroup
+    cover exactly the union of the blocks listed by its q-blocks with valid
+    rows, per 512-block segment in ascending order, in contiguous ranges whose
+    sizes differ by at most one; q-blocks whose rows all lie in padding or in
+    another workgroup add nothing."""
+    rng = _rng(43)
+    g, N, ph, Mkv = 48, 1000, 40, 1300
+    QM = (ph + N + 8) // g
+    merged = np.full((QM, 20), -1, dtype=np.int32)
+    for qb in range(QM):
+        n = int(rng.integers(0, 21))
+        merged[qb, :n] = rng.permutation(Mkv)[:n]
+    for splits in (2, 3, 4):
+        for p0 in (0, 256, 768):
+            part = O._split_parts(merged, g, N, ph, Mkv, splits, p0)
+            want = set()
+            for qb in range(QM):
+                lo, hi = max(qb * g, p0, ph), min(qb * g + g, p0 + 256, ph + N)
+                if lo < hi:
+                    want.update(int(m) for m in merged[qb] if m >= 0)
+            assert set(part) == want
+            for seg0 in (0, 512, 1024):
+                lst = sorted(m for m in want if seg0 <= m < seg0 + 512)
+                sps = [part[m] for m in lst]
+                assert sps == sorted(sps)  # contiguous, ascending
+                sizes = [sps.count(sp) for sp in range(splits)]
+                assert max(sizes) - min(sizes) <= 1 and sum(sizes) == len(lst)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 4])
+def test_split_schedule_without_rounding_is_softmax(splits):
+    """The split forward's schedule (per-part anchors, then the merge of the
+    parts' (acc, l, m)) equals the exact softmax(s) V when nothing is rounded,
+    over several workgroups, padding and two 512-block segments (one-key KV
+    blocks): a wrong part weight, sign or a dropped part fails this."""
+    rng = _rng(44)
+    B, N, H, D, g, b = 1, 600, 2, 16, 32, 1
+    qpad, kvpad = (8, 24), (0, 0)
+    QM = (qpad[0] + N + qpad[1]) // g
+    merged = np.full((B, H, QM, 300), -1, dtype=np.int32)
+    for h in range(H):
+        for qm in range(QM):
+            n = int(rng.integers(0, 301))
+            merged[0, h, qm, :n] = rng.permutation(N)[:n]
+    q = rng.standard_normal((B, N, H * D)) * 3
+    k = rng.standard_normal((B, N, H * D))
+    v = rng.standard_normal((B, N, H * D))
+    o64, l64 = O.sparse_attn(q, k, v, merged, H, g, b, None, qpad, kvpad)
+    os_, ls = O.sparse_attn(q, k, v, merged, H, g, b, None, qpad, kvpad, round_p="f64", splits=splits)
+    np.testing.assert_allclose(os_, o64, rtol=1e-10, atol=1e-12)
+    np.testing.assert_array_equal(ls, l64)
+    if splits > 1:  # with bf16 P the split schedule rounds differently from the unsplit one
+        ob1, _ = O.sparse_attn(q, k, v, merged, H, g, b, None, qpad, kvpad, round_p="bf16")
+        obs, _ = O.sparse_attn(q, k, v, merged, H, g, b, None, qpad, kvpad, round_p="bf16", splits=splits)
+        assert np.abs(obs - ob1).max() > 0
+        assert np.abs(obs - o64).max() < 2e-2 and np.abs(ob1 - o64).max() < 2e-2
+
+
 def test_rounding_modes_bound_and_exact_cases():
     """With every P exactly representable (all scores equal, so P = 1 / n after
     normalisation in the backward and 1 before it in the forward) the rounding
