@@ -330,6 +330,83 @@ __global__ __launch_bounds__(256) void fta_qblock_merge_wave_kernel(
 }
 
 // ----------------------------------------------------------------------------
+// q-block merge, one wave per slice, for g*K > 512 entries over at most
+// kMergeHistM blocks.  Same results as the kernels above: the wave adds its
+// slice's entries 64 at a time into an LDS histogram acc[Mt], resolving ids
+// repeated within a step in rounds through an LDS atomicMin owner (the lowest
+// lane, i.e. the earliest position, adds first), so every id's fp32 sum runs
+// in (row, slot) order; the positive sums (at most Mt <= 512) are then
+// compacted in id order and sorted in registers on 64-bit (score, ~id) keys.
+// This replaces a bitonic sort of all g*K (id, position) keys in LDS.
+// ----------------------------------------------------------------------------
+constexpr int kMergeHistM = 512;
+
+__global__ __launch_bounds__(256) void fta_qblock_merge_hist_kernel(
+    const int32_t* __restrict__ idx, const float* __restrict__ scr, int64_t num_slices, int g, int K, int Mt, int W,
+    int32_t* __restrict__ out_idx, float* __restrict__ out_scr, int32_t* __restrict__ counts) {
+    __shared__ float s_acc[4][kMergeHistM];
+    __shared__ int s_owner[4][kMergeHistM];
+    __shared__ unsigned long long s_key[4][kMergeHistM];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t slice = (int64_t)blockIdx.x * 4 + wave;
+    if (slice >= num_slices) return;  // no workgroup barrier below
+    volatile float* acc = s_acc[wave];
+    volatile int* owner = s_owner[wave];
+    unsigned long long* key = s_key[wave];
+    for (int m = lane; m < Mt; m += 64) acc[m] = 0.f;
+    fta_wave_sync();
+    const int n = g * K;
+    const int32_t* ip = idx + slice * (int64_t)n;
+    const float* sp = scr + slice * (int64_t)n;
+    for (int j0 = 0; j0 < n; j0 += 64) {
+        const int j = j0 + lane;
+        const int id = (j < n) ? ip[j] : -1;
+        const float sc = (j < n) ? sp[j] : 0.f;
+        bool pending = id >= 0 && id < Mt;
+        while (__ballot(pending) != 0ull) {
+            if (pending) owner[id] = 64;
+            if (pending) atomicMin(const_cast<int*>(&owner[id]), lane);
+            if (pending && owner[id] == lane) {
+                acc[id] = __fadd_rn(acc[id], sc);
+                pending = false;
+            }
+        }
+    }
+    fta_wave_sync();
+    // positive sums in id order
+    int P = 0;
+    for (int base = 0; base < Mt; base += 64) {
+        const int m = base + lane;
+        const float a = (m < Mt) ? acc[m] : 0.f;
+        const bool pos = a > 0.f;
+        const unsigned long long mask = __ballot(pos);
+        if (pos)
+            key[P + __popcll(mask & ((1ull << lane) - 1ull))] =
+                ((unsigned long long)__builtin_bit_cast(uint32_t, a) << 32) | (unsigned long long)(0xffffffffu - m);
+        P += __popcll(mask);
+    }
+    int S = 1;
+    while (S < P) S <<= 1;
+    for (int i = P + lane; i < S; i += 64) key[i] = 0ull;
+    fta_wave_sync();
+    fta_wave_sort<unsigned long long, true>(key, S, 0ull, lane);  // descending
+    const int keep = P < W ? P : W;
+    int32_t* oi = out_idx + slice * (int64_t)W;
+    float* os = out_scr ? out_scr + slice * (int64_t)W : nullptr;
+    for (int p = lane; p < W; p += 64) {
+        if (p < keep) {
+            const unsigned long long kv = key[p];
+            oi[p] = (int)(0xffffffffu - (uint32_t)(kv & 0xffffffffull));
+            if (os) os[p] = __builtin_bit_cast(float, (uint32_t)(kv >> 32));
+        } else {
+            oi[p] = -1;
+            if (os) os[p] = 0.f;
+        }
+    }
+    if (counts && lane == 0) counts[slice] = keep;
+}
+
+// ----------------------------------------------------------------------------
 // Reverse index (reference: flash_topk_attn_v2/sparse_attn_bwd.py:36-76,
 // csrc/build_reverse_indices_kernel.cu:6-104).
 // Membership bitmap sel[bh][m][qm/32] bit (qm%32) = q-block qm selected KV
@@ -764,6 +841,13 @@ int launch_qblock_merge(const int32_t* idx, const float* scr, int64_t num_slices
                         const int32_t* max_id, int W, int32_t* out_idx, float* out_scr, int32_t* counts,
                         hipStream_t st) {
     const int64_t n = (int64_t)g * K;
+    if (max_id == nullptr && n > 512 && Mt <= kMergeHistM) {
+        // many entries over few blocks: histogram per wave instead of a sort of every entry
+        const int64_t blocks = (num_slices + 3) / 4;
+        hipLaunchKernelGGL(fta_qblock_merge_hist_kernel, dim3((unsigned)blocks), dim3(256), 0, st, idx, scr,
+                           num_slices, g, K, Mt, W, out_idx, out_scr, counts);
+        return check_launch("fta_qblock_merge_hist_kernel");
+    }
     if (n >= 1 && n <= kMergeWaveMax) {
         int NP = 1;
         while (NP < n) NP <<= 1;

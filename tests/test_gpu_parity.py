@@ -234,6 +234,34 @@ def test_merge_bit_exact(g, K, Mt, W, pad, with_scores):
     np.testing.assert_array_equal(c.cpu().numpy(), rc)
 
 
+@pytest.mark.parametrize("g,K,Mt,W,dups", [(64, 32, 64, 2048, False), (48, 16, 500, 300, True),
+                                           (64, 16, 512, 512, False), (40, 13, 37, 16, True)])
+def test_merge_histogram_wave_bit_exact(g, K, Mt, W, dups):
+    """flash_qblock_merge with more than 512 entries per q-block over at most
+    512 blocks runs the per-wave LDS histogram (the reference's K = 32, g = 64
+    row: 2048 entries over 64 blocks).  Bit-exact against the oracle's
+    sequential (row, slot) sums, with ids repeated within a row and inside one
+    64-entry step (dups), ids past the block count and -1 entries ignored."""
+    say(f"[merge hist] g={g} K={K} Mt={Mt} W={W} dups={dups}")
+    rng = np.random.default_rng(9)
+    B, H, QM = 1, 3, 9
+    N = QM * g
+    idx = np.stack([rng.permutation(Mt + 5)[:K] for _ in range(B * H * N)]).reshape(B, H, N, K).astype(np.int32)
+    if dups:
+        idx[..., 1] = idx[..., 0]  # the same id twice in a row
+        idx[..., 2] = rng.integers(0, 3, size=(B, H, N))  # a few ids shared by most rows
+    idx[rng.random((B, H, N, K)) < 0.2] = -1
+    scr = (rng.random((B, H, N, K)) * 2 - 0.5).astype(np.float32)  # some negative scores
+    ti, ts = torch.from_numpy(idx).cuda(), torch.from_numpy(scr).cuda()
+    counts = torch.empty(B, H, QM, dtype=torch.int32, device="cuda")
+    m, sc = fta.flash_qblock_merge(ti, ts, g, W, Mt, counts)
+    torch.cuda.synchronize()
+    rm, rs = O.qblock_merge(idx, scr, g, W, Mt)
+    np.testing.assert_array_equal(m.cpu().numpy(), rm)
+    np.testing.assert_array_equal(sc.cpu().numpy(), rs)
+    np.testing.assert_array_equal(counts.cpu().numpy(), (rm >= 0).sum(-1))
+
+
 def test_merge_device_max_edge_cases():
     """build_qblock_topk_indices reads the max id on the device: all -1 rows give
     empty lists, and an id past the 4096-block sort limit raises as in the
