@@ -69,6 +69,9 @@ CONFIGS = {
     "C4": (2, 10000, 12, 64, torch.float16, 64, 8, 1.0, 16, None, (24, 24), (0, 0), "iid", True),
     "C5": (1, 16384, 16, 128, torch.bfloat16, 64, 16, 1.0, 32, 512, (0, 0), (0, 0), "iid_scaled", True),
     "C3": (1, 32768, 32, 128, torch.bfloat16, 64, 16, 0.9, 32, 256, (0, 0), (0, 0), "peaked", True),
+    # the largest block count the path supports (M = 4096: merge sort, reverse index, kv order,
+    # eight 512-block mask segments in the forward / dQ walks) on two heads of C3-style data
+    "Mmax": (1, 262144, 2, 128, torch.bfloat16, 64, 16, 0.9, 32, 256, (0, 0), (0, 0), "peaked", True),
 }
 
 
@@ -76,7 +79,7 @@ CONFIGS = {
 def test_config_full_size(name):
     B, N, H, D, dt, b, topk, thr, g, W, pad, qpad, data, bwd = CONFIGS[name]
     say(f"[config {name}] B{B} N{N} H{H} D{D} {dt} b{b} topk{topk} thr{thr} g{g} W{W} pad{pad}")
-    seed = {"C2g1": 1, "C2g32": 1, "C4": 4, "C5": 5, "C3": 2}[name]
+    seed = {"C2g1": 1, "C2g32": 1, "C4": 4, "C5": 5, "C3": 2, "Mmax": 6}[name]
     C = H * D
     if data == "peaked":
         q, k, v = _peaked(B, N, H, D, seed)
