@@ -330,6 +330,97 @@ __global__ __launch_bounds__(256) void fta_qblock_merge_wave_kernel(
 }
 
 // ----------------------------------------------------------------------------
+// q-block merge, one lane per slice, for g*K <= NMAX (32) entries (g = 1 or 2
+// q-blocks of a few queries).  Same results as the kernels above: the lane
+// adds each valid id's scores in position order (an entry joins the first
+// earlier entry with its id), then insertion-sorts the positive sums by
+// (score desc, id asc) in registers.  Replaces a 64-lane wave per slice, whose
+// bitonic networks ran at 64 elements for these 16- or 32-entry slices.
+// ----------------------------------------------------------------------------
+template <int NMAX>
+__global__ __launch_bounds__(256) void fta_qblock_merge_lane_kernel(
+    const int32_t* __restrict__ idx, const float* __restrict__ scr, int64_t num_slices, int n, int Mt_arg,
+    const int32_t* __restrict__ max_id, int W, int32_t* __restrict__ out_idx, float* __restrict__ out_scr,
+    int32_t* __restrict__ counts) {
+    const int64_t slice = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (slice >= num_slices) return;
+    const int Mt = max_id ? min(max(*max_id + 1, 1), 4096) : Mt_arg;
+    const int32_t* ip = idx + slice * (int64_t)n;
+    const float* sp = scr + slice * (int64_t)n;
+    int id[NMAX];
+    float sum[NMAX];
+    int U = 0;  // distinct valid ids so far, in first-appearance order
+#pragma unroll
+    for (int j = 0; j < NMAX; ++j) {
+        if (j < n) {
+            const int m = ip[j];
+            const float sc = sp[j];
+            if (m >= 0 && m < Mt) {
+                bool found = false;
+#pragma unroll
+                for (int u = 0; u < NMAX; ++u)
+                    if (u < U && id[u] == m && !found) {
+                        sum[u] = __fadd_rn(sum[u], sc);
+                        found = true;
+                    }
+                if (!found) {
+#pragma unroll
+                    for (int u = 0; u < NMAX; ++u)
+                        if (u == U) {
+                            id[u] = m;
+                            sum[u] = sc;
+                        }
+                    ++U;
+                }
+            }
+        }
+    }
+    // insertion sort of the positive sums: score desc, then id asc
+    int P = 0;
+    int oid[NMAX];
+    float osc[NMAX];
+#pragma unroll
+    for (int u = 0; u < NMAX; ++u) {
+        if (u < U && sum[u] > 0.f) {
+            const float v = sum[u];
+            const int m = id[u];
+            // position = entries ranking above (v, m); shift the rest down one slot
+            int pos = 0;
+#pragma unroll
+            for (int p = 0; p < NMAX; ++p)
+                if (p < P && (osc[p] > v || (osc[p] == v && oid[p] < m))) ++pos;
+#pragma unroll
+            for (int p = NMAX - 1; p > 0; --p)
+                if (p > pos && p <= P) {
+                    osc[p] = osc[p - 1];
+                    oid[p] = oid[p - 1];
+                }
+#pragma unroll
+            for (int p = 0; p < NMAX; ++p)
+                if (p == pos) {
+                    osc[p] = v;
+                    oid[p] = m;
+                }
+            ++P;
+        }
+    }
+    const int keep = P < W ? P : W;
+    int32_t* oi = out_idx + slice * (int64_t)W;
+    float* os = out_scr ? out_scr + slice * (int64_t)W : nullptr;
+#pragma unroll
+    for (int p = 0; p < NMAX; ++p)
+        if (p < W) {
+            oi[p] = (p < keep) ? oid[p] : -1;
+            if (os) os[p] = (p < keep) ? osc[p] : 0.f;
+        }
+    for (int p = NMAX; p < W; ++p) {
+        oi[p] = -1;
+        if (os) os[p] = 0.f;
+    }
+    if (counts) counts[slice] = keep;
+}
+
+// ----------------------------------------------------------------------------
 // q-block merge, one wave per slice, for g*K > 512 entries over at most
 // kMergeHistM blocks.  Same results as the kernels above: the wave adds its
 // slice's entries 64 at a time into an LDS histogram acc[Mt], resolving ids
@@ -841,6 +932,16 @@ int launch_qblock_merge(const int32_t* idx, const float* scr, int64_t num_slices
                         const int32_t* max_id, int W, int32_t* out_idx, float* out_scr, int32_t* counts,
                         hipStream_t st) {
     const int64_t n = (int64_t)g * K;
+    if (n >= 1 && n <= 32) {
+        const int64_t blocks = (num_slices + 255) / 256;
+        if (n <= 16)
+            hipLaunchKernelGGL(fta_qblock_merge_lane_kernel<16>, dim3((unsigned)blocks), dim3(256), 0, st, idx, scr,
+                               num_slices, (int)n, Mt, max_id, W, out_idx, out_scr, counts);
+        else
+            hipLaunchKernelGGL(fta_qblock_merge_lane_kernel<32>, dim3((unsigned)blocks), dim3(256), 0, st, idx, scr,
+                               num_slices, (int)n, Mt, max_id, W, out_idx, out_scr, counts);
+        return check_launch("fta_qblock_merge_lane_kernel");
+    }
     if (max_id == nullptr && n > 512 && Mt <= kMergeHistM) {
         // many entries over few blocks: histogram per wave instead of a sort of every entry
         const int64_t blocks = (num_slices + 3) / 4;

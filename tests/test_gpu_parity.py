@@ -235,16 +235,20 @@ def test_merge_bit_exact(g, K, Mt, W, pad, with_scores):
 
 
 @pytest.mark.parametrize("g,K,Mt,W,dups", [(64, 32, 64, 2048, False), (48, 16, 500, 300, True),
-                                           (64, 16, 512, 512, False), (40, 13, 37, 16, True)])
-def test_merge_histogram_wave_bit_exact(g, K, Mt, W, dups):
+                                           (64, 16, 512, 512, False), (40, 13, 37, 16, True),
+                                           (1, 16, 300, 16, True), (2, 16, 64, 40, True), (3, 7, 50, 8, False),
+                                           (1, 16, 4096, 16, False)])
+def test_merge_lane_and_histogram_bit_exact(g, K, Mt, W, dups):
     """flash_qblock_merge with more than 512 entries per q-block over at most
     512 blocks runs the per-wave LDS histogram (the reference's K = 32, g = 64
-    row: 2048 entries over 64 blocks).  Bit-exact against the oracle's
-    sequential (row, slot) sums, with ids repeated within a row and inside one
-    64-entry step (dups), ids past the block count and -1 entries ignored."""
-    say(f"[merge hist] g={g} K={K} Mt={Mt} W={W} dups={dups}")
+    row: 2048 entries over 64 blocks); with at most 32 entries per q-block it
+    runs one lane per q-block (g = 1: C2's q-blocks of one query).  Bit-exact
+    against the oracle's sequential (row, slot) sums, with ids repeated within
+    a row and inside one 64-entry step (dups), ids past the block count, -1
+    entries and non-positive sums ignored."""
+    say(f"[merge lane/hist] g={g} K={K} Mt={Mt} W={W} dups={dups}")
     rng = np.random.default_rng(9)
-    B, H, QM = 1, 3, 9
+    B, H, QM = 1, 3, 9 if g > 3 else 700
     N = QM * g
     idx = np.stack([rng.permutation(Mt + 5)[:K] for _ in range(B * H * N)]).reshape(B, H, N, K).astype(np.int32)
     if dups:
