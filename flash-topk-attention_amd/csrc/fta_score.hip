@@ -1321,29 +1321,39 @@ __device__ __forceinline__ void fta_topk_emit(float (&lv)[KB], int (&li)[KB], in
     }
     const bool aligned = ((reinterpret_cast<uintptr_t>(out_idx) | reinterpret_cast<uintptr_t>(out_raw) |
                            reinterpret_cast<uintptr_t>(out_avg)) & 15) == 0;
-    if (m_out <= CAP && aligned) {
-        // Stage each output's 64 x m_out block (contiguous in HBM) in this wave's
+    if (aligned) {
+        // Stage each output's rows x m_out block (contiguous in HBM) in this wave's
         // candidate buffer, then write it with 16-byte stores over consecutive
-        // addresses instead of one 4-byte store per (lane, slot).
+        // addresses instead of one 4-byte store per (lane, slot), which for
+        // m_out = 32 / 64 touched 64 cache lines per store.  Rows go in passes
+        // of rpp (a multiple of 4, so every pass starts 16-byte aligned) that
+        // fit the CAP x 64 buffer.
         float* st = &stage[0][0];
-        const int total = nrows * m_out, n4 = total >> 2;
+        const int rpp = min(64, ((CAP * 64) / m_out) & ~3);
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
             float* out = (k == 0) ? reinterpret_cast<float*>(out_idx) : (k == 1) ? out_raw : out_avg;
-            out += wrow0 * m_out;
+            for (int r0 = 0; r0 < nrows; r0 += rpp) {
+                const int rn = min(rpp, nrows - r0);
+                if (lane >= r0 && lane < r0 + rn) {
 #pragma unroll
-            for (int p = 0; p < KB; ++p)
-                if (p < m_out)
-                    st[lane * m_out + p] = (k == 0) ? __builtin_bit_cast(float, li[p]) : (k == 1) ? rawv[p] : lv[p];
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            for (int c = lane; c < n4; c += 64)
-                reinterpret_cast<float4*>(out)[c] = reinterpret_cast<const float4*>(st)[c];
-            for (int e = (n4 << 2) + lane; e < total; e += 64) out[e] = st[e];
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    for (int p = 0; p < KB; ++p)
+                        if (p < m_out)
+                            st[(lane - r0) * m_out + p] =
+                                (k == 0) ? __builtin_bit_cast(float, li[p]) : (k == 1) ? rawv[p] : lv[p];
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                float* o = out + (wrow0 + r0) * m_out;
+                const int total = rn * m_out, n4 = total >> 2;
+                for (int c = lane; c < n4; c += 64)
+                    reinterpret_cast<float4*>(o)[c] = reinterpret_cast<const float4*>(st)[c];
+                for (int e = (n4 << 2) + lane; e < total; e += 64) o[e] = st[e];
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
         }
         return;
     }
