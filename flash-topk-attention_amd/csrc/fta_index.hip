@@ -342,82 +342,109 @@ __global__ __launch_bounds__(256) void fta_qblock_merge_lane_kernel(
     const int32_t* __restrict__ idx, const float* __restrict__ scr, int64_t num_slices, int n, int Mt_arg,
     const int32_t* __restrict__ max_id, int W, int32_t* __restrict__ out_idx, float* __restrict__ out_scr,
     int32_t* __restrict__ counts) {
-    const int64_t slice = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (slice >= num_slices) return;
+    // The workgroup's 256 slices are contiguous in HBM (n entries each): they are
+    // read and their results written as whole blocks through LDS (rows padded to
+    // NMAX + 1 words against bank conflicts), so every global access is
+    // coalesced; one lane then works on one row.
+    constexpr int RS = NMAX + 1;
+    __shared__ int s_id[256 * RS];
+    __shared__ float s_sc[256 * RS];
+    __shared__ int s_keep[256];
+    const int tid = threadIdx.x;
+    const int64_t s0 = (int64_t)blockIdx.x * 256;
+    const int ns = (int)min((int64_t)256, num_slices - s0);
     const int Mt = max_id ? min(max(*max_id + 1, 1), 4096) : Mt_arg;
-    const int32_t* ip = idx + slice * (int64_t)n;
-    const float* sp = scr + slice * (int64_t)n;
-    int id[NMAX];
-    float sum[NMAX];
-    int U = 0;  // distinct valid ids so far, in first-appearance order
+    {
+        const int32_t* ib = idx + s0 * n;
+        const float* sb = scr + s0 * n;
+        for (int e = tid; e < ns * n; e += 256) {
+            const int r = e / n, c = e - r * n;
+            s_id[r * RS + c] = ib[e];
+            s_sc[r * RS + c] = sb[e];
+        }
+    }
+    __syncthreads();
+    int oid[NMAX];
+    float osc[NMAX];
+    int P = 0;
+    if (tid < ns) {
+        int id[NMAX];
+        float sum[NMAX];
+        int U = 0;  // distinct valid ids so far, in first-appearance order
 #pragma unroll
-    for (int j = 0; j < NMAX; ++j) {
-        if (j < n) {
-            const int m = ip[j];
-            const float sc = sp[j];
-            if (m >= 0 && m < Mt) {
-                bool found = false;
-#pragma unroll
-                for (int u = 0; u < NMAX; ++u)
-                    if (u < U && id[u] == m && !found) {
-                        sum[u] = __fadd_rn(sum[u], sc);
-                        found = true;
-                    }
-                if (!found) {
+        for (int j = 0; j < NMAX; ++j) {
+            if (j < n) {
+                const int m = s_id[tid * RS + j];
+                const float sc = s_sc[tid * RS + j];
+                if (m >= 0 && m < Mt) {
+                    bool found = false;
 #pragma unroll
                     for (int u = 0; u < NMAX; ++u)
-                        if (u == U) {
-                            id[u] = m;
-                            sum[u] = sc;
+                        if (u < U && id[u] == m && !found) {
+                            sum[u] = __fadd_rn(sum[u], sc);
+                            found = true;
                         }
-                    ++U;
+                    if (!found) {
+#pragma unroll
+                        for (int u = 0; u < NMAX; ++u)
+                            if (u == U) {
+                                id[u] = m;
+                                sum[u] = sc;
+                            }
+                        ++U;
+                    }
                 }
             }
         }
-    }
-    // insertion sort of the positive sums: score desc, then id asc
-    int P = 0;
-    int oid[NMAX];
-    float osc[NMAX];
+        // insertion sort of the positive sums: score desc, then id asc
 #pragma unroll
-    for (int u = 0; u < NMAX; ++u) {
-        if (u < U && sum[u] > 0.f) {
-            const float v = sum[u];
-            const int m = id[u];
-            // position = entries ranking above (v, m); shift the rest down one slot
-            int pos = 0;
+        for (int u = 0; u < NMAX; ++u) {
+            if (u < U && sum[u] > 0.f) {
+                const float v = sum[u];
+                const int m = id[u];
+                // position = entries ranking above (v, m); shift the rest down one slot
+                int pos = 0;
 #pragma unroll
-            for (int p = 0; p < NMAX; ++p)
-                if (p < P && (osc[p] > v || (osc[p] == v && oid[p] < m))) ++pos;
+                for (int p = 0; p < NMAX; ++p)
+                    if (p < P && (osc[p] > v || (osc[p] == v && oid[p] < m))) ++pos;
 #pragma unroll
-            for (int p = NMAX - 1; p > 0; --p)
-                if (p > pos && p <= P) {
-                    osc[p] = osc[p - 1];
-                    oid[p] = oid[p - 1];
-                }
+                for (int p = NMAX - 1; p > 0; --p)
+                    if (p > pos && p <= P) {
+                        osc[p] = osc[p - 1];
+                        oid[p] = oid[p - 1];
+                    }
 #pragma unroll
-            for (int p = 0; p < NMAX; ++p)
-                if (p == pos) {
-                    osc[p] = v;
-                    oid[p] = m;
-                }
-            ++P;
+                for (int p = 0; p < NMAX; ++p)
+                    if (p == pos) {
+                        osc[p] = v;
+                        oid[p] = m;
+                    }
+                ++P;
+            }
         }
     }
+    __syncthreads();  // every lane has read its row
     const int keep = P < W ? P : W;
-    int32_t* oi = out_idx + slice * (int64_t)W;
-    float* os = out_scr ? out_scr + slice * (int64_t)W : nullptr;
+    if (tid < ns) {
 #pragma unroll
-    for (int p = 0; p < NMAX; ++p)
-        if (p < W) {
-            oi[p] = (p < keep) ? oid[p] : -1;
-            if (os) os[p] = (p < keep) ? osc[p] : 0.f;
+        for (int p = 0; p < NMAX; ++p) {
+            s_id[tid * RS + p] = oid[p];
+            s_sc[tid * RS + p] = osc[p];
         }
-    for (int p = NMAX; p < W; ++p) {
-        oi[p] = -1;
-        if (os) os[p] = 0.f;
+        s_keep[tid] = keep;
+        if (counts) counts[s0 + tid] = keep;
     }
-    if (counts) counts[slice] = keep;
+    __syncthreads();
+    // the block of ns x W outputs, -1 / 0 after each row's kept entries
+    int32_t* ob = out_idx + s0 * W;
+    float* sb = out_scr ? out_scr + s0 * W : nullptr;
+    for (int e = tid; e < ns * W; e += 256) {
+        const int r = e / W, c = e - r * W;
+        const bool k = c < s_keep[r];  // then c < NMAX: inside the row
+        const int a = r * RS + (k ? c : 0);
+        ob[e] = k ? s_id[a] : -1;
+        if (sb) sb[e] = k ? s_sc[a] : 0.f;
+    }
 }
 
 // ----------------------------------------------------------------------------
