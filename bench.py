@@ -320,6 +320,8 @@ class Pipeline:
         shp = (B, H, N, m_out)
         self.sel_out = (torch.empty(shp, dtype=torch.int32, device=dev), torch.empty(shp, device=dev),
                         torch.empty(shp, device=dev))
+        if self.streams_ok:
+            self.scorer()  # ws_score holds valid streams from here on (select_streams reads them)
 
     # --- stage launchers
     def score(self):

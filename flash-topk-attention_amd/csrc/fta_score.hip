@@ -1536,7 +1536,7 @@ __global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_stream_kerne
     const uint2* __restrict__ pool, const int* __restrict__ cand_count, const int* __restrict__ chunk_tab, int maxch,
     const float* __restrict__ tau_key, const float* __restrict__ row_lse, int N, int qtiles, int M, int m_out,
     int bsz, int pad_head, int pad_tail, float threshold, int32_t* __restrict__ out_idx, float* __restrict__ out_raw,
-    float* __restrict__ out_avg, int* __restrict__ ovf_list, int* __restrict__ ovf_cnt) {
+    float* __restrict__ out_avg, int* __restrict__ ovf_list, int* __restrict__ ovf_cnt, int pool_chunks) {
     constexpr int CAP = 16;
     __shared__ __align__(16) float cand_v[4][CAP][64];
     __shared__ int cand_i[4][CAP][64];
@@ -1553,12 +1553,18 @@ __global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_stream_kerne
     {
         const int* c4 = cand_count + (int64_t)blockIdx.x * 4;
         if (min(min(c4[0], c4[1]), min(c4[2], c4[3])) < 0) {  // a stream of this tile is incomplete
-            if (tid == 0) ovf_list[atomicAdd(ovf_cnt, 1)] = blockIdx.x;
+            if (tid == 0) {
+                const int k = atomicAdd(ovf_cnt, 1);
+                if ((unsigned)k < gridDim.x) ovf_list[k] = blockIdx.x;
+            }
             return;
         }
     }
     const int* tab = chunk_tab + sw * maxch;
-    const int total = __builtin_amdgcn_readfirstlane(cand_count[sw]);
+    // Counts, chunk ids and the fallback count are read back from the workspace;
+    // they are clamped to what the workspace holds, so a workspace that no scorer
+    // run filled gives undefined outputs but no access outside it.
+    const int total = min(__builtin_amdgcn_readfirstlane(cand_count[sw]), maxch * kStreamChunk);
 
     float lv[KB];
     int li[KB];
@@ -1603,24 +1609,28 @@ __global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_stream_kerne
         wave_sync();
     };
     wave_sync();
-    // NC chunks of 64 entries per step, the next step's chunks loading meanwhile;
-    // the pre-filter reads, slot atomics and parking stores of a step's chunks
-    // are issued together, so their LDS latencies overlap.
+    // NC chunks of 64 entries per step, the next two steps' chunks loading
+    // meanwhile (one step ahead left the selector waiting on HBM latency); the
+    // pre-filter reads, slot atomics and parking stores of a step's chunks are
+    // issued together, so their LDS latencies overlap.
     constexpr int NC = 4;
     auto load_step = [&] __attribute__((always_inline)) (int c0, uint2 (&e)[NC]) {
         if (c0 >= total) return;
         // the step's 256 entries lie in one chunk; entries past the end (still
         // inside the chunk) are masked where they are used
         const int j = c0 / kStreamChunk;
-        const int id = (j == 0) ? (int)sw : tab[j];
+        int id = (j == 0) ? (int)sw : tab[j];
+        if ((unsigned)id >= (unsigned)pool_chunks) id = (int)sw;
         const uint2* ent = pool + (int64_t)id * kStreamChunk + (c0 - j * kStreamChunk);
 #pragma unroll
         for (int i = 0; i < NC; ++i) e[i] = ent[i * 64 + lane];
     };
-    uint2 ea[NC], eb[NC];
+    constexpr int SZ = NC * 64;
+    uint2 ea[NC], eb[NC], ec[NC];  // steps c0, c0 + SZ, c0 + 2 SZ
     load_step(0, ea);
-    for (int c0 = 0; c0 < total; c0 += NC * 64) {
-        load_step(c0 + NC * 64, eb);
+    load_step(SZ, eb);
+    for (int c0 = 0; c0 < total; c0 += SZ) {
+        load_step(c0 + 2 * SZ, ec);
         int owner[NC], m[NC];
         float x[NC];
         bool pend[NC];
@@ -1653,7 +1663,10 @@ __global__ __launch_bounds__(256, (KB <= 16) ? 4 : 2) void fta_topk_stream_kerne
             flush();
         }
 #pragma unroll
-        for (int i = 0; i < NC; ++i) ea[i] = eb[i];
+        for (int i = 0; i < NC; ++i) {
+            ea[i] = eb[i];
+            eb[i] = ec[i];
+        }
     }
     flush();
     const int nrows = min(64, N - n0);
@@ -1683,7 +1696,8 @@ __global__ __launch_bounds__(256, 1) void fta_stream_fallback_kernel(ScoreArgs a
                                                                     float threshold, int32_t* __restrict__ out_idx,
                                                                     float* __restrict__ out_raw,
                                                                     float* __restrict__ out_avg) {
-    const int n = __builtin_amdgcn_readfirstlane(*ovf_cnt);
+    // the listed tiles (count and ids clamped to the grid of the scoring launch)
+    const int n = min(__builtin_amdgcn_readfirstlane(*ovf_cnt), a.total);
     if ((int)blockIdx.x >= n) return;
     float* slot = slots + (int64_t)blockIdx.x * 256 * a.M;
     a.blk_lse = slot;
@@ -1692,6 +1706,7 @@ __global__ __launch_bounds__(256, 1) void fta_stream_fallback_kernel(ScoreArgs a
     a.tau_idx = nullptr;
     for (int r = blockIdx.x; r < n; r += gridDim.x) {
         const int tile = __builtin_amdgcn_readfirstlane(ovf_list[r]);
+        if ((unsigned)tile >= (unsigned)a.total) continue;  // workgroup-uniform
         fta_score_tile<DT, D, 0, 2, false, SB>(a, tile);
         __syncthreads();  // the slot is complete
         const int bh = tile / a.qtiles, qt = tile - bh * a.qtiles;
@@ -2153,7 +2168,7 @@ int launch_stream_select_dt(const ScoreArgs& sa, int Dk, const StreamBufs& sb, i
 #define FTA_LAUNCH_STREAM(KB)                                                                                     \
     hipLaunchKernelGGL(fta_topk_stream_kernel<KB>, dim3((unsigned)sa.total), dim3(256), 0, s, sb.pool, sb.count, \
                        sb.tab, sb.maxch, sb.tau_key, sa.row_lse, sa.N, qtiles, sa.M, m_out, sa.bsz, sa.pad_head,  \
-                       sa.pad_tail, threshold, idx, raw, avg, sb.ovf_list, sb.ctrs + 1)
+                       sa.pad_tail, threshold, idx, raw, avg, sb.ovf_list, sb.ctrs + 1, sb.pool_chunks)
     if (m_out <= 8)
         FTA_LAUNCH_STREAM(8);
     else if (m_out <= 16)

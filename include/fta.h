@@ -156,7 +156,10 @@ int fta_topk_score_candidates(const void* q, const void* k, int dtype, int B, in
  * again, so q and k are needed).  Same arguments as fta_topk_score;
  * FTA_ERR_UNSUPPORTED where fta_topk_score_candidates is.
  * fta_topk_score_candidates followed by this call gives the same outputs as
- * fta_topk_score.  Stands for the reference's top-k stage (topk_select_launch,
+ * fta_topk_score.  On a workspace that no fta_topk_score_candidates call
+ * filled for this geometry the outputs are undefined; the counts and chunk
+ * ids read from it are clamped, so no access leaves the workspace and the
+ * output arrays.  Stands for the reference's top-k stage (topk_select_launch,
  * flash_topk_attn_v2/csrc/topk_select.cpp, as called from
  * flash_topk_attn_v2/topk_select.py:185-311).
  */
