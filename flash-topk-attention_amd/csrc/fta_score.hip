@@ -1227,6 +1227,82 @@ __device__ __forceinline__ void fta_topk_flush(float (&lv)[KB], int (&li)[KB], i
     int mc = cnt;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) mc = max(mc, __shfl_xor(mc, off, 64));
+    if constexpr (KB == 32) {
+        // Lists of 32: the parked candidates are merged 16 at a time.  The batch
+        // is sorted (bitonic, descending by (avg, -index)); the top KB of list +
+        // batch is then max(list[i], batch[KB - 1 - i]) (a bitonic sequence:
+        // only the last 16 positions compare), sorted by a bitonic merge.  The
+        // list ends as the top KB of the accepted candidates, as with one
+        // insertion per candidate, at ~11 compare-exchanges per candidate
+        // instead of KB insertion steps.  (At KB = 64 the lists and the batch no
+        // longer fit the registers of two waves per SIMD: the insertion network
+        // below stays.)
+        auto ce = [](float& va, int& ia, float& vb, int& ib) {  // the better pair first
+            const bool sw = fta_better(vb, ib, va, ia);
+            const float v0 = sw ? vb : va, v1 = sw ? va : vb;
+            const int i0 = sw ? ib : ia, i1 = sw ? ia : ib;
+            va = v0;
+            vb = v1;
+            ia = i0;
+            ib = i1;
+        };
+        for (int jb = 0; jb < mc; jb += 16) {
+            float bv[16];
+            int bi[16];
+            bool any = false;
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int j = jb + u;
+                const bool in = (j < cnt) & (j < CAP);
+                const float xs = in ? cv[in ? j : 0][lane] : 0.f;
+                const int m = in ? ci[in ? j : 0][lane] : 0;
+                const bool edge = ((m == 0) & (pad_head > 0)) | ((m == M - 1) & (pad_tail > 0));
+                const float x = (MODE == 0) ? xs : xs - rl;
+                const float raw = (MODE == 0) ? x : fta_exp2(x);
+                const int vc = fta_valid_count(m, M, bsz, pad_head, pad_tail);
+                const float avg = fta_avg(raw, vc, bsz, inv_b);
+                const bool ok = active & in & (edge | ((x >= pre) & (raw >= thr_norm))) & fta_better(avg, m, tv, ti);
+                bv[u] = ok ? avg : -FTA_INF;
+                bi[u] = ok ? m : 0x7fffffff;
+                any |= ok;
+            }
+            if (__ballot(any) == 0ull) continue;
+#pragma unroll
+            for (int k = 2; k <= 16; k <<= 1)
+#pragma unroll
+                for (int j = k >> 1; j > 0; j >>= 1)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int l = i ^ j;
+                        if (l > i) {
+                            if ((i & k) == 0)
+                                ce(bv[i], bi[i], bv[l], bi[l]);
+                            else
+                                ce(bv[l], bi[l], bv[i], bi[i]);
+                        }
+                    }
+#pragma unroll
+            for (int i = KB - 16; i < KB; ++i) {
+                const float v2 = bv[KB - 1 - i];
+                const int i2 = bi[KB - 1 - i];
+                const bool take = fta_better(v2, i2, lv[i], li[i]);
+                lv[i] = take ? v2 : lv[i];
+                li[i] = take ? i2 : li[i];
+            }
+#pragma unroll
+            for (int j = KB >> 1; j > 0; j >>= 1)
+#pragma unroll
+                for (int i = 0; i < KB; ++i)
+                    if ((i & j) == 0) ce(lv[i], li[i], lv[i + j], li[i + j]);
+#pragma unroll
+            for (int p = 0; p < KB; ++p)
+                if (p == m_out - 1 && li[p] != 0x7fffffff) {
+                    tv = lv[p];
+                    ti = li[p];
+                }
+        }
+        mc = 0;  // the per-candidate loop below has nothing left
+    }
     for (int j = 0; j < mc; ++j) {
         const float xs = cv[j][lane];
         const int m = ci[j][lane];
