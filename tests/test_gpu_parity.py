@@ -108,6 +108,8 @@ SHORT_CASES = [
     (1, 512, 2, 64, 128, (0, 0), torch.bfloat16, "bnc"),     # M = 4: one unrolled pass
     (1, 600, 2, 128, 128, (100, 68), torch.bfloat16, "bnc"), # M = 6: pass + remainder
     (1, 896, 1, 64, 128, (0, 0), torch.float16, "bnc"),      # M = 7
+    (1, 40, 2, 64, 128, (0, 88), torch.bfloat16, "bnc"),     # M = 1, second chunk all padding
+    (1, 40, 2, 128, 128, (88, 0), torch.float16, "bnc"),     # M = 1, first chunk all padding
 ]
 
 
