@@ -187,19 +187,30 @@ V2_BWD_ROWS = (
 )
 
 
-def _median_ms(fn, stream, reps=5):
+def _median_ms(fn, stream, reps=20, warmup=3):
+    """Per-call GPU time of fn, timed the way the reference's V2 tables were
+    (``triton.testing.do_bench``, V2_BENCHMARK.md:72): before every call a
+    256 MB buffer is zeroed on the stream (the L2 / last-level cache starts
+    cold, and the host queues the call while the GPU is still clearing, so its
+    launch overhead is not timed), events bracket the call alone, and no call
+    waits for the previous one.  Median over ``reps`` calls."""
     import torch
 
-    fn()
-    ts = []
-    for _ in range(reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    flush = torch.empty(int(256e6 // 4), dtype=torch.int32, device="cuda")
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    # `stream` is the current stream: fn and the fill run on it
+    for e0, e1 in ev:
+        flush.zero_()
         e0.record(stream)
         fn()
         e1.record(stream)
-        torch.cuda.synchronize()
-        ts.append(e0.elapsed_time(e1))
-    return sorted(ts)[len(ts) // 2]
+    torch.cuda.synchronize()
+    ts = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
+    del flush
+    return ts[len(ts) // 2]
 
 
 def bench_v2_rows(dev, stream):
@@ -207,7 +218,8 @@ def bench_v2_rows(dev, stream):
     + top-k), flash_topk_attn forward given the merged indices, the end-to-end
     forward (score + merge + attention) and the backward (forward + backward
     minus forward, as the reference measures it); synthetic N(0, 1) inputs,
-    HIP events, median of 5.  One entry per (shape, stage) with the published
+    timed as the reference's tables were (cold cache, calls queued back to
+    back: `_median_ms`).  One entry per (shape, stage) with the published
     time and the GPU it was measured on."""
     import torch
 
@@ -269,6 +281,8 @@ def bench_v2_rows(dev, stream):
                 return fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, 64)
 
         def fwd_bwd():
+            for t in (ql, kl, vl):  # fresh gradients, not accumulated ones (do_bench's grad_to_none)
+                t.grad = None
             o, _ = fta.flash_topk_attn(ql, kl, vl, merged, counts, H, g, 64)
             o.backward(do)
 

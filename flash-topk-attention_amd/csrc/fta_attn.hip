@@ -1546,7 +1546,7 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
 
 // ----------------------------------------------------------------------------
 // dK / dV with the work of each key tile split over two waves (KV blocks of 33
-// to 64 keys, D = 64 or 128).  The WG owns the two 32-key tiles of one KV block;
+// to 64 keys, D = 64, 128 or 256).  The WG owns the two 32-key tiles of one KV block;
 // wave (tt, 0) holds K of tile tt and accumulates dV, wave (tt, 1) holds V of
 // tile tt and accumulates dK, both over the full D.  Per chunk of 32 queries:
 //   wave (tt, 0):  S = Q K^T,  P = 2^{c S - lse2}  -> LDS;  dV += P^T dO
@@ -1556,6 +1556,8 @@ __global__ __launch_bounds__(TT * CS * 64, 1) void fta_sparse_dkv_kernel(AttnArg
 // (the exponentials or the dS products), one of K / V and one set of
 // accumulators, so a WG fits twice on a CU (registers <= 256 per lane, LDS <
 // 80 KB): one WG's mask building and gather latency overlap the other's MFMAs.
+// At D = 256 (twice the stage bytes and accumulators) one WG runs per CU, with
+// the accumulators in the 512-register budget of one wave per SIMD.
 // One chunk per step; NST steps of Q, dO, lse and delta in flight through LDS
 // DMA, as in fta_sparse_dkv_kernel.
 // ----------------------------------------------------------------------------
@@ -1570,14 +1572,15 @@ struct DkvSplitShape {
     static constexpr int LD_OFF = 2 * TILE * 16;        // byte offset of lse / delta in a step
     static constexpr int STAGE_B = LD_OFF + 256;
     static constexpr int NST = (D <= 64) ? 4 : 3;
+    static constexpr int WPC = (D <= 128) ? 2 : 1;  // WGs per CU
     static_assert(2 * TILE % NTHR == 0, "whole DMA instructions per wave");
     static_assert(NST >= 3, "steps k - 1 and k live, at least one in flight");
-    static_assert(NST * STAGE_B + 2 * 2 * 32 * 32 * 4 + 3 * kSegC * 4 + 2 * kBitsW * 4 + 64 <= 80 * 1024,
-                  "two WGs per CU");
+    static_assert(NST * STAGE_B + 2 * 2 * 32 * 32 * 4 + 3 * kSegC * 4 + 2 * kBitsW * 4 + 64 <= 160 * 1024 / WPC,
+                  "WPC WGs per CU");
 };
 
 template <int DT, int D, bool GQA = false>
-__global__ __launch_bounds__(256, 2) void fta_sparse_dkv_split_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, DkvSplitShape<D>::WPC) void fta_sparse_dkv_split_kernel(AttnArgs a) {
     using E = Elem<DT>;
     using Sh = DkvSplitShape<D>;
     constexpr int NW = Sh::NW, QSEG = Sh::QSEG, TILE = Sh::TILE, LQ = Sh::LQ, NST = Sh::NST;
@@ -2040,7 +2043,13 @@ int launch_dkv_dt(AttnArgs& a, int Dk, int Tb, int B, int H, int ntiles, hipStre
                 FTA_DKV_GO(128, 4, 1);
             break;
         FTA_DKV(160, 4, 2, 2, 2, 2)
-        FTA_DKV(256, 4, 4, 1, 4, 1)
+        case 256:
+            if (Tb == 2)
+                gqa ? go(fta_sparse_dkv_split_kernel<DT, 256, true>, 2, 4)
+                    : go(fta_sparse_dkv_split_kernel<DT, 256, false>, 2, 4);
+            else
+                FTA_DKV_GO(256, 4, 1);
+            break;
 #undef FTA_DKV
 #undef FTA_DKV_GO
         default:
@@ -2234,10 +2243,11 @@ int bwd_common(AttnArgs& a, Geo& G, const void* q, const int64_t* q_strides, con
     return FTA_OK;
 }
 
-// 64-key blocks at D 64 / 128 (the split dK/dV kernel) run in the launch order
-// of fta_kv_order_kernel and the head placement of fta_head_balance_kernel
+// 64-key blocks at D 64 / 128 / 256 (the split dK/dV kernel) run in the launch
+// order of fta_kv_order_kernel and the head placement of fta_head_balance_kernel
 bool uses_kv_order(int kv_block_size, const Geo& G) {
-    return kv_block_size > 32 && kv_block_size <= 64 && (G.Dk == 64 || G.Dk == 128) && G.Mkv <= 4096;
+    return kv_block_size > 32 && kv_block_size <= 64 && (G.Dk == 64 || G.Dk == 128 || G.Dk == 256) &&
+           G.Mkv <= 4096;
 }
 
 // the head placement fta_sparse_attn_bwd_dkv left in the workspace (null if it made none)

@@ -324,6 +324,14 @@ ATTN_CASES = [
     (1, 700, 2, 48, 32, 64, (0, 4), (0, 4), 8, torch.bfloat16),
     (1, 500, 2, 80, 20, 64, (0, 0), (0, 12), 6, torch.float16),
     (1, 40, 2, 64, 8, 64, (0, 0), (0, 24), 2, torch.bfloat16),
+    # D = 256 (and 176 / 192 / 224 padded to it) with 64-key blocks: the split dK/dV kernel
+    (1, 1024, 2, 256, 32, 64, (0, 0), (0, 0), 12, torch.bfloat16),
+    (1, 777, 2, 256, 64, 64, (13, 42), (5, 50), 6, torch.float16),
+    (1, 1000, 2, 256, 16, 64, (4, 4), (12, 12), 10, torch.bfloat16),
+    (1, 500, 2, 192, 32, 64, (0, 12), (0, 12), 6, torch.bfloat16),
+    # D = 160 (and 144 padded to it) with 64-key blocks (generic dK/dV kernel, one KV block per WG)
+    (1, 1024, 2, 160, 32, 64, (0, 0), (0, 0), 10, torch.float16),
+    (1, 700, 2, 144, 32, 64, (0, 4), (0, 4), 8, torch.bfloat16),
 ]
 
 
@@ -491,6 +499,8 @@ GQA_CASES = [
     (2, 600, 6, 2, 64, 16, 64, (4, 4), (12, 28), 6, torch.float16),
     (1, 700, 4, 1, 96, 32, 96, (0, 4), (5, 63), 5, torch.bfloat16),      # generic dK/dV, 3 tiles per block
     (1, 512, 4, 2, 32, 32, 32, (0, 0), (0, 0), 6, torch.bfloat16),       # one tile per block
+    (1, 640, 4, 2, 256, 32, 64, (0, 0), (0, 0), 6, torch.bfloat16),      # split dK/dV kernel at D = 256
+    (1, 500, 4, 2, 160, 20, 64, (0, 0), (0, 12), 5, torch.float16),      # generic dK/dV at D = 160
 ]
 
 
