@@ -345,7 +345,7 @@ int fta_sparse_attn_bwd_dq(const void* q, const int64_t* q_strides, const void* 
  * dK / dV alone (Hk heads, each summed over its H / Hk query heads without
  * atomics).  Builds the KV block -> q-block membership bitmap and the lse in
  * log2 units in the workspace (fta_sparse_attn_bwd_workspace_size bytes) and
- * walks it; for 64-key blocks at D 64 / 128 the workspace also holds the launch
+ * walks it; for 64-key blocks at D 64 / 128 / 256 the workspace also holds the launch
  * order (KV blocks by selection count) and the XCD placement of the heads.  Replaces build_reverse_indices_launch + sparse_attn_bwd_dkv_launch
  * (flash_topk_attn_v2/csrc/build_reverse_indices.cpp:3-14,
  * sparse_attn_bwd_dkv.cpp:3-20) behind flash_sparse_attn_bwd_dkv_cuda
