@@ -23,6 +23,7 @@
 #include "fta_common.h"
 #include "fta_host.h"
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -910,8 +911,11 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
 // (as in fta_sparse_fwd_pipe_kernel), NST - 1 chunks ahead, so the gather
 // latency is hidden and the operand reads (K and V rows, K^T transposed) are
 // free of LDS bank conflicts.
+// SPLIT: workgroup (tiles, part sp) walks union positions [sp U / nsplit,
+// (sp + 1) U / nsplit) of each mask segment and writes its unscaled fp32 dQ
+// partial; fta_dq_combine_kernel adds the parts (dQ is linear in them).
 // ----------------------------------------------------------------------------
-template <int DT, int D>
+template <int DT, int D, bool SPLIT>
 __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) {
     using E = Elem<DT>;
     constexpr int NW = 8, T = 8;
@@ -926,9 +930,18 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
     __shared__ int s_tmp[8];
 
     const int wgi = fta_xcd_remap(blockIdx.x, a.total);
-    const int hp = wgi / a.wg_per_bh;                     // head position
+    int hp, wq, sp = 0;  // head position, tile group, part
+    if constexpr (SPLIT) {
+        const int per = a.wg_per_bh * a.nsplit;
+        hp = wgi / per;
+        const int r = wgi - hp * per;
+        wq = r / a.nsplit;
+        sp = r - wq * a.nsplit;
+    } else {
+        hp = wgi / a.wg_per_bh;
+        wq = wgi - hp * a.wg_per_bh;
+    }
     const int bh = a.head_perm ? a.head_perm[hp] : hp;  // (b, h)
-    const int wq = wgi - hp * a.wg_per_bh;
     const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -983,12 +996,18 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
     for (int seg0 = 0; seg0 < a.Mkv; seg0 += kSeg) {
         const int segn = min(kSeg, a.Mkv - seg0);
         const int U = fta_build_q_masks<T>(a, bh, p0, seg0, segn, sMask, sList, s_tmp);
-        if (U == 0) continue;
-        const int iters = U * nch;
+        int u_lo = 0, u_n = U;  // this part's union positions (workgroup-uniform)
+        if constexpr (SPLIT) {
+            u_lo = (U * sp) / a.nsplit;
+            u_n = (U * (sp + 1)) / a.nsplit - u_lo;
+        }
+        // no wave reads sMask / sList below when the part is empty
+        if (u_n == 0) continue;
+        const int iters = u_n * nch;
 
         auto issue = [&](int st, int it) {
             const uint32_t sb = lds0 + st * Sh::STAGE_B;
-            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int u = u_lo + it / nch, ch = it - (it / nch) * nch;
             const int m = __builtin_amdgcn_readfirstlane(seg0 + sList[u]);
             const int kb = m * a.kvb - a.kv_pad + ch * 64;
             const int rem = a.kvb - ch * 64;
@@ -1026,7 +1045,7 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
             __syncthreads();  // chunk it visible; every wave is past chunk it - 1
             if (it + NST - 1 < iters) issue(cur == 0 ? NST - 1 : cur - 1, it + NST - 1);
 
-            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int u = u_lo + it / nch, ch = it - (it / nch) * nch;
             const int ml = sList[u];
             const int m = seg0 + ml;
             const int kb = m * a.kvb - a.kv_pad + ch * 64;
@@ -1107,6 +1126,19 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
         __syncthreads();  // every wave is done with sMask / sList before the next segment rebuilds them
     }
 
+    if constexpr (SPLIT) {
+        // the part's unscaled dQ, by padded position (rows outside [0, N) hold zeros)
+        const int p = p0 + 32 * wave + (lane & 31);
+        if (p >= a.npq) return;
+        float* po = a.part_o + (((int64_t)sp * a.nbh + bh) * a.npq + p) * D;
+#pragma unroll
+        for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; i += 4)
+                *reinterpret_cast<float4*>(po + dt * 32 + c_row(i, lane)) =
+                    make_float4(acc[dt][i], acc[dt][i + 1], acc[dt][i + 2], acc[dt][i + 3]);
+        return;
+    }
     if (!qok) return;
     uint16_t* op = a.out0 + b * a.o0_sb + h * a.o0_sh + (int64_t)tq * a.o0_sn;
 #pragma unroll
@@ -1121,6 +1153,42 @@ __global__ __launch_bounds__(512, 1) void fta_sparse_dq_pipe_kernel(AttnArgs a) 
                 *reinterpret_cast<uint2*>(op + d) = w;
             }
         }
+}
+
+// Sum of the dQ kernel's split parts: one thread per (b·h, query, 8 columns);
+// dQ = scale · sum_p dQ_p, parts added in order.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void fta_dq_combine_kernel(AttnArgs a) {
+    using E = Elem<DT>;
+    constexpr int DC = D / 8;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)a.nbh * a.N * DC) return;
+    const int dc = (int)(idx % DC);
+    const int64_t rest = idx / DC;
+    const int t = (int)(rest % a.N), bh = (int)(rest / a.N);
+    const int d0 = dc * 8;
+    if (d0 >= a.Dreal) return;
+    const int p = t + a.q_pad;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < a.nsplit; ++sp) {
+        const float* src = a.part_o + (((int64_t)sp * a.nbh + bh) * a.npq + p) * D + d0;
+        const float4 x0 = *reinterpret_cast<const float4*>(src);
+        const float4 x1 = *reinterpret_cast<const float4*>(src + 4);
+        o[0] += x0.x;
+        o[1] += x0.y;
+        o[2] += x0.z;
+        o[3] += x0.w;
+        o[4] += x1.x;
+        o[5] += x1.y;
+        o[6] += x1.z;
+        o[7] += x1.w;
+    }
+    const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
+    uint16_t* op = a.out0 + b * a.o0_sb + h * a.o0_sh + (int64_t)t * a.o0_sn + d0;
+    *reinterpret_cast<uint2*>(op) =
+        make_uint2(E::pack2(o[0] * a.scale, o[1] * a.scale), E::pack2(o[2] * a.scale, o[3] * a.scale));
+    *reinterpret_cast<uint2*>(op + 4) =
+        make_uint2(E::pack2(o[4] * a.scale, o[5] * a.scale), E::pack2(o[6] * a.scale, o[7] * a.scale));
 }
 
 // ----------------------------------------------------------------------------
@@ -1579,7 +1647,7 @@ struct DkvSplitShape {
                   "WPC WGs per CU");
 };
 
-template <int DT, int D, bool GQA = false>
+template <int DT, int D, bool GQA, bool SPLIT>
 __global__ __launch_bounds__(256, DkvSplitShape<D>::WPC) void fta_sparse_dkv_split_kernel(AttnArgs a) {
     using E = Elem<DT>;
     using Sh = DkvSplitShape<D>;
@@ -1599,9 +1667,18 @@ __global__ __launch_bounds__(256, DkvSplitShape<D>::WPC) void fta_sparse_dkv_spl
     __shared__ int s_tmp[8];
 
     const int wgi = fta_xcd_remap(blockIdx.x, a.total);
-    const int hp = wgi / a.wg_per_bh;  // head position
+    int hp, wk0, sp = 0;  // head position, launch rank, part
+    if constexpr (SPLIT) {
+        const int per = a.wg_per_bh * a.nsplit;
+        hp = wgi / per;
+        const int r = wgi - hp * per;
+        wk0 = r / a.nsplit;
+        sp = r - wk0 * a.nsplit;
+    } else {
+        hp = wgi / a.wg_per_bh;
+        wk0 = wgi - hp * a.wg_per_bh;
+    }
     const int bhk = a.head_perm ? a.head_perm[hp] : hp;  // (b, K/V head)
-    const int wk0 = wgi - hp * a.wg_per_bh;
     const int wk = a.kv_order ? a.kv_order[(int64_t)bhk * a.wg_per_bh + wk0] : wk0;  // KV block
     const int b = bhk / a.Hk, hk = bhk - (bhk / a.Hk) * a.Hk;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1684,13 +1761,21 @@ __global__ __launch_bounds__(256, DkvSplitShape<D>::WPC) void fta_sparse_dkv_spl
             }
             for (int seg0 = 0; seg0 < a.NC; seg0 += kSegC) {
                 const int segn = min(kSegC, a.NC - seg0);
-                const int U = fta_build_kv_masks<TT>(a, bh, wk, Tb, seg0, segn, bits_lds, sBits, sMask, sList, s_tmp);
+                const int Ua = fta_build_kv_masks<TT>(a, bh, wk, Tb, seg0, segn, bits_lds, sBits, sMask, sList, s_tmp);
+                // this part's chunk-list positions [u_lo, u_lo + U) (workgroup-uniform)
+                int u_lo = 0, U = Ua;
+                if constexpr (SPLIT) {
+                    u_lo = (Ua * sp) / a.nsplit;
+                    U = (Ua * (sp + 1)) / a.nsplit - u_lo;
+                }
+                // no wave reads sMask / sList below when the part is empty
                 if (U == 0) continue;
+                const int* lst = sList + u_lo;
 
                 // gather chunk list entry k into stage buffer st
                 auto issue = [&](int st, int k) {
                     const uint32_t sbase = lds0 + st * Sh::STAGE_B;
-                    const int c = __builtin_amdgcn_readfirstlane(seg0 + sList[k]);
+                    const int c = __builtin_amdgcn_readfirstlane(seg0 + lst[k]);
                     const int t0 = 32 * c - a.q_pad;
                     if (t0 >= 0 && t0 + 31 < a.N) {
 #pragma unroll
@@ -1743,7 +1828,7 @@ __global__ __launch_bounds__(256, DkvSplitShape<D>::WPC) void fta_sparse_dkv_spl
                     __syncthreads();
                     if (k + NST - 2 < U) issue(cur >= 2 ? cur - 2 : cur + NST - 2, k + NST - 2);
                     const int prv = cur == 0 ? NST - 1 : cur - 1;  // stage buffer of step k - 1
-                    const uint32_t mk = (k < U) ? __builtin_amdgcn_readfirstlane(sMask[tt][sList[k]]) : 0u;
+                    const uint32_t mk = (k < U) ? __builtin_amdgcn_readfirstlane(sMask[tt][lst[k]]) : 0u;
                     const uint16_t* qb = reinterpret_cast<const uint16_t*>(&sStage[cur][0]);
                     const uint16_t* ob = qb + TILE * 8;
                     const float* ld = reinterpret_cast<const float*>(&sStage[cur][Sh::LD_OFF]);
@@ -1838,6 +1923,16 @@ __global__ __launch_bounds__(256, DkvSplitShape<D>::WPC) void fta_sparse_dkv_spl
         }
 
         // C layout: lane column = d, rows = keys c_row(i, lane); role 0 stores dV, role 1 dK
+        if constexpr (SPLIT) {
+            // the part's unscaled fp32 dK (role 1) or dV (role 0), rows wk * 64 + key
+            float* po = a.part_o + ((((int64_t)(HV ? 0 : 1) * a.nsplit + sp) * a.nbh + bhk) * a.npq +
+                                    (int64_t)wk * 64 + 32 * tt) * D;
+#pragma unroll
+            for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) po[(int64_t)c_row(i, lane) * D + dt * 32 + (lane & 31)] = acc[dt][i];
+            return;
+        }
         uint16_t* out = HV ? a.out0 + b * a.o0_sb + hk * a.o0_sh : a.out1 + b * a.o1_sb + hk * a.o1_sh;
         const int64_t osn = HV ? a.o0_sn : a.o1_sn;
         const float osc = HV ? a.scale : 1.f;
@@ -1859,6 +1954,46 @@ __global__ __launch_bounds__(256, DkvSplitShape<D>::WPC) void fta_sparse_dkv_spl
         run(std::false_type{});
 }
 
+
+// Sum of the split dK/dV parts: one thread per (b·K/V head, key, 8 columns) and
+// tensor; dK = scale · sum_p dK_p, dV = sum_p dV_p, parts added in order.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void fta_dkv_combine_kernel(AttnArgs a) {
+    using E = Elem<DT>;
+    constexpr int DC = D / 8;
+    const int64_t per = (int64_t)a.nbh * a.N * DC;
+    int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= 2 * per) return;
+    const int ten = idx >= per;  // 0: dK, 1: dV
+    idx -= ten * per;
+    const int dc = (int)(idx % DC);
+    const int64_t rest = idx / DC;
+    const int t = (int)(rest % a.N), bhk = (int)(rest / a.N);
+    const int d0 = dc * 8;
+    if (d0 >= a.Dreal) return;
+    const int kp = t + a.kv_pad;
+    const int64_t row = (int64_t)(kp / a.kvb) * 64 + kp % a.kvb;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < a.nsplit; ++sp) {
+        const float* src = a.part_o + ((((int64_t)ten * a.nsplit + sp) * a.nbh + bhk) * a.npq + row) * D + d0;
+        const float4 x0 = *reinterpret_cast<const float4*>(src);
+        const float4 x1 = *reinterpret_cast<const float4*>(src + 4);
+        o[0] += x0.x;
+        o[1] += x0.y;
+        o[2] += x0.z;
+        o[3] += x0.w;
+        o[4] += x1.x;
+        o[5] += x1.y;
+        o[6] += x1.z;
+        o[7] += x1.w;
+    }
+    const float sc = ten ? 1.f : a.scale;
+    const int b = bhk / a.Hk, hk = bhk - (bhk / a.Hk) * a.Hk;
+    uint16_t* op = ten ? a.out1 + b * a.o1_sb + hk * a.o1_sh + (int64_t)t * a.o1_sn + d0
+                       : a.out0 + b * a.o0_sb + hk * a.o0_sh + (int64_t)t * a.o0_sn + d0;
+    *reinterpret_cast<uint2*>(op) = make_uint2(E::pack2(o[0] * sc, o[1] * sc), E::pack2(o[2] * sc, o[3] * sc));
+    *reinterpret_cast<uint2*>(op + 4) = make_uint2(E::pack2(o[4] * sc, o[5] * sc), E::pack2(o[6] * sc, o[7] * sc));
+}
 
 // lse2 = lse * log2(e) (the same fp32 product the kernels formed per element)
 __global__ __launch_bounds__(256) void fta_lse2_kernel(const float* __restrict__ lse, float* __restrict__ lse2,
@@ -1974,15 +2109,19 @@ int launch_dq_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
         break;
         FTA_DQ(32, 8)
         case 64:
-            if (pipe_ok)
-                hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 64>), dim3(grid), dim3(512), 0, st, a);
+            if (pipe_ok && a.nsplit > 1)
+                hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 64, true>), dim3(grid), dim3(512), 0, st, a);
+            else if (pipe_ok)
+                hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 64, false>), dim3(grid), dim3(512), 0, st, a);
             else
                 hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, 64, 8>), dim3(grid), dim3(512), 0, st, a);
             break;
         FTA_DQ(96, 8)
         case 128:
-            if (pipe_ok)
-                hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 128>), dim3(grid), dim3(512), 0, st, a);
+            if (pipe_ok && a.nsplit > 1)
+                hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 128, true>), dim3(grid), dim3(512), 0, st, a);
+            else if (pipe_ok)
+                hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 128, false>), dim3(grid), dim3(512), 0, st, a);
             else
                 hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, 128, 8>), dim3(grid), dim3(512), 0, st, a);
             break;
@@ -1992,7 +2131,15 @@ int launch_dq_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
         default:
             return fta::arg_error("sparse_attn_bwd: unsupported head dim");
     }
-    return fta::check_launch("fta_sparse_dq_kernel");
+    int rc = fta::check_launch("fta_sparse_dq_kernel");
+    if (rc != FTA_OK || !(pipe_ok && a.nsplit > 1)) return rc;
+    const int64_t threads = (int64_t)a.nbh * a.N * (Dk / 8);
+    const unsigned blocks = (unsigned)((threads + 255) / 256);
+    if (Dk == 64)
+        hipLaunchKernelGGL((fta_dq_combine_kernel<DT, 64>), dim3(blocks), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((fta_dq_combine_kernel<DT, 128>), dim3(blocks), dim3(256), 0, st, a);
+    return fta::check_launch("fta_dq_combine_kernel");
 }
 
 // dK/dV launch shape: TT key tiles x CS chunk slots.  TT covers the 32-key tiles
@@ -2001,18 +2148,17 @@ int launch_dq_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
 // spill), use one slot (TT = all waves).
 template <int DT>
 int launch_dkv_dt(AttnArgs& a, int Dk, int Tb, int B, int H, int ntiles, hipStream_t st) {
-    int TT = 0;
     const bool gqa = a.G > 1;
-    auto go = [&](auto kern, int tt, int nw) {
-        TT = tt;
+    // ns: parts per KV block (the split kernel with a.nsplit > 1), else 1
+    auto go = [&](auto kern, int tt, int nw, int ns) {
         a.wg_per_bh = (ntiles + tt - 1) / tt;
-        a.total = a.wg_per_bh * B * H;
+        a.total = a.wg_per_bh * B * H * ns;
         hipLaunchKernelGGL(kern, dim3(a.total), dim3(nw * 64), 0, st, a);
     };
     switch (Dk) {
 #define FTA_DKV_GO(DK, TTX, CSX)                                                             \
-    (gqa ? go(fta_sparse_dkv_kernel<DT, DK, TTX, CSX, true>, TTX, TTX * CSX)                 \
-         : go(fta_sparse_dkv_kernel<DT, DK, TTX, CSX, false>, TTX, TTX * CSX))
+    (gqa ? go(fta_sparse_dkv_kernel<DT, DK, TTX, CSX, true>, TTX, TTX * CSX, 1)              \
+         : go(fta_sparse_dkv_kernel<DT, DK, TTX, CSX, false>, TTX, TTX * CSX, 1))
 #define FTA_DKV(DK, NW, TT1, CS1, TT2, CS2)                                                  \
     case DK:                                                                                 \
         if (Tb == 1)                                                                         \
@@ -2022,11 +2168,17 @@ int launch_dkv_dt(AttnArgs& a, int Dk, int Tb, int B, int H, int ntiles, hipStre
         else                                                                                 \
             FTA_DKV_GO(DK, NW, 1);                                                           \
         break;
+#define FTA_DKV_SPLIT(DK)                                                                            \
+    if (a.nsplit > 1)                                                                                \
+        gqa ? go(fta_sparse_dkv_split_kernel<DT, DK, true, true>, 2, 4, a.nsplit)                    \
+            : go(fta_sparse_dkv_split_kernel<DT, DK, false, true>, 2, 4, a.nsplit);                  \
+    else                                                                                             \
+        gqa ? go(fta_sparse_dkv_split_kernel<DT, DK, true, false>, 2, 4, 1)                          \
+            : go(fta_sparse_dkv_split_kernel<DT, DK, false, false>, 2, 4, 1)
         FTA_DKV(32, 8, 1, 4, 2, 4)
         case 64:
             if (Tb == 2)
-                gqa ? go(fta_sparse_dkv_split_kernel<DT, 64, true>, 2, 4)
-                    : go(fta_sparse_dkv_split_kernel<DT, 64, false>, 2, 4);
+                FTA_DKV_SPLIT(64);
             else if (Tb == 1)
                 FTA_DKV_GO(64, 1, 4);
             else
@@ -2035,8 +2187,7 @@ int launch_dkv_dt(AttnArgs& a, int Dk, int Tb, int B, int H, int ntiles, hipStre
         FTA_DKV(96, 4, 1, 4, 2, 2)
         case 128:
             if (Tb == 2)
-                gqa ? go(fta_sparse_dkv_split_kernel<DT, 128, true>, 2, 4)
-                    : go(fta_sparse_dkv_split_kernel<DT, 128, false>, 2, 4);
+                FTA_DKV_SPLIT(128);
             else if (Tb == 1)
                 FTA_DKV_GO(128, 1, 4);
             else
@@ -2045,18 +2196,28 @@ int launch_dkv_dt(AttnArgs& a, int Dk, int Tb, int B, int H, int ntiles, hipStre
         FTA_DKV(160, 4, 2, 2, 2, 2)
         case 256:
             if (Tb == 2)
-                gqa ? go(fta_sparse_dkv_split_kernel<DT, 256, true>, 2, 4)
-                    : go(fta_sparse_dkv_split_kernel<DT, 256, false>, 2, 4);
+                FTA_DKV_SPLIT(256);
             else
                 FTA_DKV_GO(256, 4, 1);
             break;
+#undef FTA_DKV_SPLIT
 #undef FTA_DKV
 #undef FTA_DKV_GO
         default:
             return fta::arg_error("sparse_attn_bwd: unsupported head dim");
     }
-    (void)TT;
-    return fta::check_launch("fta_sparse_dkv_kernel");
+    int rc = fta::check_launch("fta_sparse_dkv_kernel");
+    if (rc != FTA_OK || a.nsplit <= 1) return rc;
+    // the parts' sums: dK and dV, one thread per (b * Hk, key, 8 columns) each
+    const int64_t threads = 2 * (int64_t)a.nbh * a.N * (Dk / 8);
+    const unsigned blocks = (unsigned)((threads + 255) / 256);
+    if (Dk == 64)
+        hipLaunchKernelGGL((fta_dkv_combine_kernel<DT, 64>), dim3(blocks), dim3(256), 0, st, a);
+    else if (Dk == 128)
+        hipLaunchKernelGGL((fta_dkv_combine_kernel<DT, 128>), dim3(blocks), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((fta_dkv_combine_kernel<DT, 256>), dim3(blocks), dim3(256), 0, st, a);
+    return fta::check_launch("fta_dkv_combine_kernel");
 }
 
 size_t sel_bytes(int B, int H, const Geo& G) {
@@ -2083,6 +2244,30 @@ size_t split_bytes(int B, int H, const Geo& G, int ns) {
     if (ns <= 1) return 0;
     const size_t rows = (size_t)ns * B * H * G.Npq;
     return fta::align_up(rows * sizeof(float2)) + fta::align_up(rows * G.Dk * sizeof(float));
+}
+
+// dQ's split parts (the forward's rule for small grids: its workgroups cover the
+// same 256-query tiles), after bwd_bytes in the workspace of the combined backward
+size_t dq_split_bytes(int B, int H, const Geo& G, int ns) {
+    if (ns <= 1) return 0;
+    return fta::align_up((size_t)ns * B * H * G.Npq * G.Dk * sizeof(float));
+}
+
+// dK/dV parts of the split kernel (64-key blocks, D 64 / 128 / 256) on small
+// grids: fewer workgroups than the CUs hold (two per CU, one at D = 256) get
+// up to 4 parts per KV block; [dK, dV][part][b * Hk][KV block * 64 + key][Dk]
+// fp32, after bwd_bytes (dQ's parts reuse the same bytes after dK/dV is done)
+int dkv_nsplit(int B, int Hk, int kv_block_size, const Geo& G) {
+    if (!(kv_block_size > 32 && kv_block_size <= 64 && (G.Dk == 64 || G.Dk == 128 || G.Dk == 256))) return 1;
+    const int64_t wgs = (int64_t)G.Mkv * B * Hk;
+    const int64_t cap = (G.Dk <= 128) ? 512 : 256;
+    if (wgs >= cap) return 1;
+    const int64_t ns = cap / wgs;
+    return (int)(ns > 4 ? 4 : ns < 2 ? 2 : ns);
+}
+size_t dkv_split_bytes(int B, int Hk, const Geo& G, int ns) {
+    if (ns <= 1) return 0;
+    return fta::align_up((size_t)2 * ns * B * Hk * G.Mkv * 64 * G.Dk * sizeof(float));
 }
 
 // the backward workspace: membership bitmap, lse in log2 units, dK/dV launch order (KV blocks, then heads)
@@ -2197,7 +2382,11 @@ size_t fta_sparse_attn_bwd_workspace_size(int B, int H, int N, int D, int q_bloc
     if (geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM,
                  &G) != FTA_OK)
         return 0;
-    return bwd_bytes(B, H, N, G);  // membership bitmap KV block -> q-blocks, lse in log2 units
+    // membership bitmap KV block -> q-blocks, lse in log2 units, launch order, then
+    // the split parts of dK/dV and of dQ (one region: dQ runs after dK/dV is done);
+    // the dK/dV parts are sized for one K/V head per query head
+    return bwd_bytes(B, H, N, G) + std::max(dq_split_bytes(B, H, G, fwd_nsplit(B, H, G)),
+                                            dkv_split_bytes(B, H, G, dkv_nsplit(B, H, kv_block_size, G)));
 }
 
 }  // extern "C"
@@ -2264,12 +2453,13 @@ const int32_t* dkv_head_perm(const void* workspace, int B, int H, int N, int D, 
 }
 
 // dQ with an optional head placement (null: natural order)
+// split_ws / split_bytes: room for dQ's split parts (null: no split)
 int bwd_dq_impl(const int32_t* head_perm, const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
                 const void* v, const int64_t* v_strides, const void* dout, const int64_t* do_strides,
                 int dtype, int B, int H, int Hk, int N, int D, const int32_t* merged_indices, int QM, int W,
                 int q_block_size, int kv_block_size, int q_pad_head, int q_pad_tail, int kv_pad_head,
                 int kv_pad_tail, float scale, const float* lse, const float* delta, void* dq,
-                const int64_t* dq_strides, void* stream) {
+                const int64_t* dq_strides, void* split_ws, size_t split_avail, void* stream) {
     FTA_TRY_BEGIN
     AttnArgs a;
     Geo G;
@@ -2285,7 +2475,14 @@ int bwd_dq_impl(const int32_t* head_perm, const void* q, const int64_t* q_stride
     a.o0_sn = dq_strides[2];
     const int Tq = (G.Dk <= 128) ? 8 : 4;  // query tiles per dQ workgroup
     a.wg_per_bh = (G.Npq + 32 * Tq - 1) / (32 * Tq);
-    a.total = a.wg_per_bh * B * H;
+    // small grids: each workgroup's union walk in 2-4 parts, summed by fta_dq_combine_kernel
+    const int ns = fwd_nsplit(B, H, G);
+    const bool split = ns > 1 && split_ws != nullptr && split_avail >= dq_split_bytes(B, H, G, ns);
+    a.nsplit = split ? ns : 1;
+    a.nbh = B * H;
+    a.npq = G.Npq;
+    a.part_o = split ? (float*)split_ws : nullptr;
+    a.total = a.wg_per_bh * B * H * a.nsplit;
     if (dtype == FTA_DTYPE_BF16) return launch_dq_dt<FTA_DTYPE_BF16>(a, G.Dk, a.total, st);
     if (dtype == FTA_DTYPE_F16) return launch_dq_dt<FTA_DTYPE_F16>(a, G.Dk, a.total, st);
     return fta::arg_error("sparse_attn_bwd: dtype must be bf16 or fp16");
@@ -2303,7 +2500,7 @@ int fta_sparse_attn_bwd_dq(const void* q, const int64_t* q_strides, const void* 
                            const int64_t* dq_strides, void* stream) {
     return bwd_dq_impl(nullptr, q, q_strides, k, k_strides, v, v_strides, dout, do_strides, dtype, B, H, Hk, N, D,
                        merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head,
-                       kv_pad_tail, scale, lse, delta, dq, dq_strides, stream);
+                       kv_pad_tail, scale, lse, delta, dq, dq_strides, nullptr, 0, stream);
 }
 
 int fta_sparse_attn_bwd_dkv(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -2354,6 +2551,15 @@ int fta_sparse_attn_bwd_dkv(const void* q, const int64_t* q_strides, const void*
     a.o1_sn = dv_strides[2];
     const int Tb = (kv_block_size + 31) / 32;
     const int ntiles = G.Mkv * Tb;
+    // small grids: each KV block's chunk list in parts (split kernel), summed by
+    // fta_dkv_combine_kernel, when the workspace has room for the parts
+    const int ns = dkv_nsplit(B, Hk, kv_block_size, G);
+    const size_t used = bwd_bytes(B, H, N, G);
+    const bool split = ns > 1 && workspace_bytes >= used + dkv_split_bytes(B, Hk, G, ns);
+    a.nsplit = split ? ns : 1;
+    a.nbh = B * Hk;
+    a.npq = G.Mkv * 64;
+    a.part_o = split ? (float*)((char*)workspace + used) : nullptr;
     // one dK/dV WG set per K/V head; each walks the G query heads that share it
     if (dtype == FTA_DTYPE_BF16) return launch_dkv_dt<FTA_DTYPE_BF16>(a, G.Dk, Tb, B, Hk, ntiles, st);
     return launch_dkv_dt<FTA_DTYPE_F16>(a, G.Dk, Tb, B, Hk, ntiles, st);
@@ -2377,9 +2583,15 @@ int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void*
     const int32_t* perm = (Hk == H) ? dkv_head_perm(workspace, B, H, N, D, QM, q_block_size, kv_block_size,
                                                     q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail)
                                     : nullptr;
+    // dQ's split parts go after the dK/dV pass's bytes (it has validated the geometry)
+    Geo G;
+    geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head, kv_pad_tail, QM, &G);
+    const size_t used = bwd_bytes(B, H, N, G);
+    void* split_ws = workspace_bytes > used ? (char*)workspace + used : nullptr;
     return bwd_dq_impl(perm, q, q_strides, k, k_strides, v, v_strides, dout, do_strides, dtype, B, H, Hk, N, D,
                        merged_indices, QM, W, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head,
-                       kv_pad_tail, scale, lse, delta, dq, dq_strides, stream);
+                       kv_pad_tail, scale, lse, delta, dq, dq_strides, split_ws,
+                       split_ws ? workspace_bytes - used : 0, stream);
 }
 
 int fta_sparse_attn_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -2454,8 +2666,15 @@ extern "C" int fta_sparse_attn_bwd_noalloc(
     const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv, const int64_t* dv_strides,
     void* stream) {
     FTA_TRY_BEGIN
-    const size_t need = fta_sparse_attn_bwd_workspace_size(B, H, N, D, q_block_size, kv_block_size, q_pad_head,
-                                                           q_pad_tail, kv_pad_head, kv_pad_tail);
+    // the bitmap, log2 lse and launch order must fit; dQ's split parts are used
+    // only when they fit as well (fta_sparse_attn_bwd_gqa checks the room left)
+    Geo G;
+    size_t need = fta_sparse_attn_bwd_workspace_size(B, H, N, D, q_block_size, kv_block_size, q_pad_head,
+                                                     q_pad_tail, kv_pad_head, kv_pad_tail);
+    const int64_t nq = (int64_t)q_pad_head + N + q_pad_tail;
+    if (q_block_size > 0 && geometry(B, H, N, D, q_block_size, kv_block_size, q_pad_head, q_pad_tail, kv_pad_head,
+                                     kv_pad_tail, (int)(nq / q_block_size), &G) == FTA_OK)
+        need = bwd_bytes(B, H, N, G);
     if (need > (size_t)FTA_NOALLOC_SCRATCH_BYTES)
         return fta::unsupported(
             "sparse_attn_bwd_noalloc: the problem needs more scratch than FTA_NOALLOC_SCRATCH_BYTES "

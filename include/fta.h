@@ -300,6 +300,17 @@ int fta_sparse_attn_fwd_gqa(const void* q, const int64_t* q_strides, const void*
                             int kv_pad_tail, float scale, void* o, const int64_t* o_strides,
                             float* lse, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Backward workspace: the membership bitmap, the lse in log2 units and the
+ * dK/dV launch order, plus, on small grids, room for split walks (one region,
+ * used by dK/dV and then by dQ): dK/dV with fewer workgroups than the GPU holds
+ * at once (64-key blocks at D 64 / 128 / 256) and dQ with fewer than 128
+ * workgroups walk their lists in 2-4 parts whose fp32 sums are added by a
+ * combine kernel.  A smaller workspace (at least the bitmap, lse and order)
+ * runs the walks unsplit: the results then differ only in fp32 summation
+ * order.  Sized for Hk = H; with Hk < H the dK/dV parts may not fit, and
+ * dK/dV then runs unsplit.
+ */
 size_t fta_sparse_attn_bwd_workspace_size(int B, int H, int N, int D, int q_block_size,
                                           int kv_block_size, int q_pad_head, int q_pad_tail,
                                           int kv_pad_head, int kv_pad_tail);
@@ -383,8 +394,8 @@ int fta_sparse_attn_bwd_gqa(const void* q, const int64_t* q_strides, const void*
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving or training loops, harnesses that forbid hipMalloc).  Same arguments
  * and results as fta_sparse_attn_bwd_gqa without (workspace, workspace_bytes):
- * the scratch (membership bitmap + lse in log2 units, the size that
- * fta_sparse_attn_bwd_workspace_size reports) lives in a device array of
+ * the scratch (membership bitmap + lse in log2 units + launch order, and the
+ * split parts of small grids when they fit too) lives in a device array of
  * FTA_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the
  * process ends.  The array belongs to the library's code object: every process
  * that loads the library reserves it on each GPU where the library's kernels

@@ -53,7 +53,21 @@ def test_error_path_returns_status_without_gpu():
     # backward scratch = membership bitmap [B*H][M_kv][ceil(QM/32)] uint32, lse in log2
     # units [B*H][N] fp32, dK/dV launch order [B*H][M_kv] int32, head work and head
     # placement [B*H] int32 each, each region 256-byte aligned
-    assert L.fta_sparse_attn_bwd_workspace_size(1, 2, 128, 64, 32, 64, 0, 0, 0, 0) == 256 + 1024 + 256 + 256
+    # plus the split parts of small grids, one region shared by dK/dV and then dQ:
+    # dK/dV [2][parts][B*H][M_kv * 64][D] fp32 with up to 4 parts while fewer
+    # workgroups than 512 (two per CU) run; dQ [parts][B*H][N][D] fp32 as for the
+    # forward's split walks (fewer than 128 workgroups, at least 8 KV blocks).
+    # B1 H2 N128 D64: 4 dK/dV workgroups, 4 parts; dQ not split (2 KV blocks)
+    assert L.fta_sparse_attn_bwd_workspace_size(1, 2, 128, 64, 32, 64, 0, 0, 0, 0) == (
+        256 + 1024 + 256 + 256 + 2 * 4 * 2 * 2 * 64 * 64 * 4)
+    # B1 H8 N2048 D64: 256 dK/dV workgroups (2 parts) and 64 dQ workgroups (4 parts),
+    # the same 16 MiB either way
+    assert L.fta_sparse_attn_bwd_workspace_size(1, 8, 2048, 64, 64, 64, 0, 0, 0, 0) == (
+        1024 + 8 * 2048 * 4 + 1024 + 256 + 4 * 8 * 2048 * 64 * 4)
+    assert 4 * 8 * 2048 * 64 * 4 == 2 * 2 * 8 * 32 * 64 * 64 * 4
+    # 4096 dQ workgroups at C3: no split parts
+    assert L.fta_sparse_attn_bwd_workspace_size(1, 32, 32768, 128, 32, 64, 0, 0, 0, 0) == (
+        32 * 512 * 32 * 4 + 32 * 32768 * 4 + 32 * 512 * 4 + 256)
 
 
 def test_api_validation_matches_reference_errors():

@@ -985,3 +985,82 @@ def test_forward_split_walks(case):
     rfin = np.isfinite(rl)
     assert np.array_equal(rfin, fin)
     np.testing.assert_allclose(l1n[fin], rl[fin], rtol=1e-4, atol=1e-4)
+
+
+def _bwd_bytes_unsplit(B, H, N, g, b, qpad, kvpad):
+    """The backward workspace without split parts: membership bitmap, log2 lse,
+    launch order, head work and placement, each 256-byte aligned."""
+    al = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    QM = (qpad[0] + N + qpad[1]) // g
+    M = (kvpad[0] + N + kvpad[1]) // b
+    return al(B * H * M * ((QM + 31) // 32) * 4) + al(B * H * N * 4) + al(B * H * M * 4) + al(B * H * 2 * 4)
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: f"B{c[0]}H{c[1]}k{c[2]}N{c[3]}D{c[4]}g{c[5]}b{c[6]}")
+def test_bwd_split_walks(case):
+    """Small grids also split the backward's walks when the workspace has room:
+    dQ's union walks (fta_dq_combine_kernel adds the parts) and, for 64-key
+    blocks, each KV block's chunk list in dK/dV (fta_dkv_combine_kernel).
+    Against the same entry points without room for parts (fta_sparse_attn_bwd_dq
+    has no workspace; fta_sparse_attn_bwd_dkv given the bare minimum): the same
+    fp32 sums in another order, so each element is equal or one 16-bit rounding
+    step away.  The split results against the rounding oracle (every element)
+    follow through the Python API in test_sparse_attn_fwd_bwd_vs_oracle, whose
+    small cases split."""
+    from flash_topk_attn_v2 import _lib
+    from flash_topk_attn_v2.sparse_attn_bwd import preprocess_delta
+
+    B, H, Hk, N, D, g, b, qpad, kvpad, W = case
+    say(f"[bwd split walks] {case}")
+    QM = (qpad[0] + N + qpad[1]) // g
+    M = (kvpad[0] + N + kvpad[1]) // b
+    rng = np.random.default_rng(8)
+    merged = np.full((B, H, QM, W), -1, dtype=np.int32)
+    for bb in range(B):
+        for h in range(H):
+            for qm in range(QM):
+                n = 0 if (qm + h) % 7 == 3 else int(rng.integers(1, min(W, M) + 1))
+                merged[bb, h, qm, :n] = rng.permutation(M)[:n]
+    merged_t = torch.from_numpy(merged).cuda()
+    q, do = (rand((B, N, H * D), 70 + i, torch.bfloat16, "cuda") for i in range(2))
+    k, v = (rand((B, N, Hk * D), 72 + i, torch.bfloat16, "cuda") for i in range(2))
+    L = _lib.lib()
+    qs, ks = _lib.i64arr([N * H * D, D, H * D]), _lib.i64arr([N * Hk * D, D, Hk * D])
+    geo = (B, H, N, D, g, b, qpad[0], qpad[1], kvpad[0], kvpad[1])
+    stream = torch.cuda.current_stream().cuda_stream
+    assert L.fta_sparse_attn_fwd_splits(*geo) > 1, "the case should split its walks"
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, N, dtype=torch.float32, device="cuda")
+    ws_f = _lib.workspace(L.fta_sparse_attn_fwd_workspace_size(*geo), "cuda")
+    _lib.check(L.fta_sparse_attn_fwd_gqa(q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), ks, _lib.DTYPE_BF16, B, H,
+                                         Hk, N, D, merged_t.data_ptr(), QM, W, g, b, qpad[0], qpad[1], kvpad[0],
+                                         kvpad[1], D ** -0.5, o.data_ptr(), qs, lse.data_ptr(), ws_f.data_ptr(),
+                                         ws_f.numel(), stream), "fta_sparse_attn_fwd_gqa")
+    delta = preprocess_delta(o, do, H)
+    ws_b = _lib.workspace(L.fta_sparse_attn_bwd_workspace_size(*geo), "cuda")
+    bare = _bwd_bytes_unsplit(B, H, N, g, b, qpad, kvpad)
+    assert ws_b.numel() > bare, "the workspace should hold split parts"
+    args = (q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), ks, do.data_ptr(), qs, _lib.DTYPE_BF16, B, H, Hk, N, D,
+            merged_t.data_ptr(), QM, W, g, b, qpad[0], qpad[1], kvpad[0], kvpad[1], D ** -0.5, lse.data_ptr(),
+            delta.data_ptr())
+    g1 = [torch.full_like(q, 7.0), torch.full_like(k, 7.0), torch.full_like(v, 7.0)]
+    _lib.check(L.fta_sparse_attn_bwd_gqa(*args, g1[0].data_ptr(), qs, g1[1].data_ptr(), ks, g1[2].data_ptr(), ks,
+                                         ws_b.data_ptr(), ws_b.numel(), stream), "fta_sparse_attn_bwd_gqa")
+    g2 = [torch.full_like(q, 7.0), torch.full_like(k, 7.0), torch.full_like(v, 7.0)]
+    _lib.check(L.fta_sparse_attn_bwd_dq(*args, g2[0].data_ptr(), qs, stream), "fta_sparse_attn_bwd_dq")
+    _lib.check(L.fta_sparse_attn_bwd_dkv(*args, g2[1].data_ptr(), ks, g2[2].data_ptr(), ks, ws_b.data_ptr(), bare,
+                                         stream), "fta_sparse_attn_bwd_dkv")
+    torch.cuda.synchronize()
+    for name, x, y in zip(("dq", "dk", "dv"), g1, g2):
+        a, c = x.float(), y.float()
+        # one bf16 rounding step is at most 2^-7 of the larger magnitude; where the partial
+        # sums cancel, the fp32 reassociation error is absolute (2^-16 of the largest
+        # magnitude allows for it); empty lists give zeros on both
+        step = torch.maximum(a.abs(), c.abs()) * 2.0 ** -7 + c.abs().max() * 2.0 ** -16
+        bad = (a - c).abs() > step
+        if bad.any():
+            j = int(((a - c).abs() / step).argmax())
+            say(f"{name} worst: split {a.flatten()[j].item()} unsplit {c.flatten()[j].item()} "
+                f"max {c.abs().max().item()}")
+        assert not bad.any(), f"{name}: {int(bad.sum())} elements differ by more than one rounding step"
+        assert (a != c).float().mean() < 0.05, f"{name}: the split should change few roundings"
