@@ -727,7 +727,7 @@ __global__ __launch_bounds__(256) void fta_fwd_combine_kernel(AttnArgs a) {
 //   S^T = K Q^T, P^T = 2^{c S^T - lse2}, dP^T = V dO^T, dS^T = P^T (dP^T - delta),
 //   dQ^T += K^T dS^T  (K^T from the T layout).
 // ----------------------------------------------------------------------------
-template <int DT, int D, int NW>
+template <int DT, int D, int NW, bool SPLIT>
 __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
     using E = Elem<DT>;
     constexpr int NB = (D <= 160) ? 2 : 1;  // LDS buffers (D = 256 single-buffers to fit 160 KB)
@@ -745,8 +745,17 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
     __shared__ int s_tmp[8];
 
     const int wgi = fta_xcd_remap(blockIdx.x, a.total);
-    const int bh = wgi / a.wg_per_bh;
-    const int wq = wgi - bh * a.wg_per_bh;
+    int bh, wq, sp = 0;  // (b, h), tile group, part (as in fta_sparse_dq_pipe_kernel)
+    if constexpr (SPLIT) {
+        const int per = a.wg_per_bh * a.nsplit;
+        bh = wgi / per;
+        const int r = wgi - bh * per;
+        wq = r / a.nsplit;
+        sp = r - wq * a.nsplit;
+    } else {
+        bh = wgi / a.wg_per_bh;
+        wq = wgi - bh * a.wg_per_bh;
+    }
     const int b = bh / a.H, h = bh - (bh / a.H) * a.H;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int hf = lane >> 5;
@@ -786,10 +795,15 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
     for (int seg0 = 0; seg0 < a.Mkv; seg0 += kSeg) {
         const int segn = min(kSeg, a.Mkv - seg0);
         const int U = fta_build_q_masks<T>(a, bh, p0, seg0, segn, sMask, sList, s_tmp);
-        if (U == 0) continue;
-        const int iters = U * nch;
+        int u_lo = 0, u_n = U;  // this part's union positions (workgroup-uniform)
+        if constexpr (SPLIT) {
+            u_lo = (U * sp) / a.nsplit;
+            u_n = (U * (sp + 1)) / a.nsplit - u_lo;
+        }
+        if (u_n == 0) continue;
+        const int iters = u_n * nch;
         auto load = [&](int it) {
-            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int u = u_lo + it / nch, ch = it - (it / nch) * nch;
             const int m = seg0 + sList[u];
             const int kb = m * a.kvb - a.kv_pad + ch * 64;
             const int rem = a.kvb - ch * 64;
@@ -821,7 +835,7 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
         for (int it = 0; it < iters; ++it) {
             const int buf = (NB == 2) ? (it & 1) : 0;
             if (it + 1 < iters) load(it + 1);
-            const int u = it / nch, ch = it - (it / nch) * nch;
+            const int u = u_lo + it / nch, ch = it - (it / nch) * nch;
             const int ml = sList[u];
             const int m = seg0 + ml;
             const int kb = m * a.kvb - a.kv_pad + ch * 64;
@@ -889,6 +903,19 @@ __global__ __launch_bounds__(NW * 64, 1) void fta_sparse_dq_kernel(AttnArgs a) {
         }
     }
 
+    if constexpr (SPLIT) {
+        // the part's unscaled dQ, by padded position (rows outside [0, N) hold zeros)
+        const int p = p0 + 32 * wave + (lane & 31);
+        if (p >= a.npq) return;
+        float* po = a.part_o + (((int64_t)sp * a.nbh + bh) * a.npq + p) * D;
+#pragma unroll
+        for (int dt = 0; dt < DT32; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; i += 4)
+                *reinterpret_cast<float4*>(po + dt * 32 + c_row(i, lane)) =
+                    make_float4(acc[dt][i], acc[dt][i + 1], acc[dt][i + 2], acc[dt][i + 3]);
+        return;
+    }
     if (!qok) return;
     uint16_t* op = a.out0 + b * a.o0_sb + h * a.o0_sh + (int64_t)tq * a.o0_sn;
 #pragma unroll
@@ -2102,28 +2129,40 @@ template <int DT>
 int launch_dq_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
     // the pipelined kernel keeps per-lane row offsets (64 rows x stride) in 32 bits
     const bool pipe_ok = a.k_sn <= (1 << 24) && a.v_sn <= (1 << 24);
+    // split walks (decided by the caller, grid included): the pipelined kernels (D 64 /
+    // 128) or the register-staged ones (D 160 / 256)
+    const bool split = a.nsplit > 1;
+    if (split && !(Dk == 160 || Dk == 256 || ((Dk == 64 || Dk == 128) && pipe_ok)))
+        return fta::arg_error("sparse_attn_bwd: no split dQ kernel for this shape");
     switch (Dk) {
 #define FTA_DQ(DK, NW)                                                                                  \
     case DK:                                                                                             \
-        hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, DK, NW>), dim3(grid), dim3(NW * 64), 0, st, a);     \
+        if (split)                                                                                       \
+            hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, DK, NW, true>), dim3(grid), dim3(NW * 64), 0, st, a); \
+        else                                                                                             \
+            hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, DK, NW, false>), dim3(grid), dim3(NW * 64), 0, st, a); \
         break;
-        FTA_DQ(32, 8)
+        case 32:
+            hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, 32, 8, false>), dim3(grid), dim3(512), 0, st, a);
+            break;
         case 64:
-            if (pipe_ok && a.nsplit > 1)
+            if (split)
                 hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 64, true>), dim3(grid), dim3(512), 0, st, a);
             else if (pipe_ok)
                 hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 64, false>), dim3(grid), dim3(512), 0, st, a);
             else
-                hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, 64, 8>), dim3(grid), dim3(512), 0, st, a);
+                hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, 64, 8, false>), dim3(grid), dim3(512), 0, st, a);
             break;
-        FTA_DQ(96, 8)
+        case 96:
+            hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, 96, 8, false>), dim3(grid), dim3(512), 0, st, a);
+            break;
         case 128:
-            if (pipe_ok && a.nsplit > 1)
+            if (split)
                 hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 128, true>), dim3(grid), dim3(512), 0, st, a);
             else if (pipe_ok)
                 hipLaunchKernelGGL((fta_sparse_dq_pipe_kernel<DT, 128, false>), dim3(grid), dim3(512), 0, st, a);
             else
-                hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, 128, 8>), dim3(grid), dim3(512), 0, st, a);
+                hipLaunchKernelGGL((fta_sparse_dq_kernel<DT, 128, 8, false>), dim3(grid), dim3(512), 0, st, a);
             break;
         FTA_DQ(160, 4)
         FTA_DQ(256, 4)
@@ -2132,13 +2171,15 @@ int launch_dq_dt(AttnArgs& a, int Dk, int grid, hipStream_t st) {
             return fta::arg_error("sparse_attn_bwd: unsupported head dim");
     }
     int rc = fta::check_launch("fta_sparse_dq_kernel");
-    if (rc != FTA_OK || !(pipe_ok && a.nsplit > 1)) return rc;
+    if (rc != FTA_OK || !split) return rc;
     const int64_t threads = (int64_t)a.nbh * a.N * (Dk / 8);
     const unsigned blocks = (unsigned)((threads + 255) / 256);
-    if (Dk == 64)
-        hipLaunchKernelGGL((fta_dq_combine_kernel<DT, 64>), dim3(blocks), dim3(256), 0, st, a);
-    else
-        hipLaunchKernelGGL((fta_dq_combine_kernel<DT, 128>), dim3(blocks), dim3(256), 0, st, a);
+    switch (Dk) {
+        case 64: hipLaunchKernelGGL((fta_dq_combine_kernel<DT, 64>), dim3(blocks), dim3(256), 0, st, a); break;
+        case 128: hipLaunchKernelGGL((fta_dq_combine_kernel<DT, 128>), dim3(blocks), dim3(256), 0, st, a); break;
+        case 160: hipLaunchKernelGGL((fta_dq_combine_kernel<DT, 160>), dim3(blocks), dim3(256), 0, st, a); break;
+        default: hipLaunchKernelGGL((fta_dq_combine_kernel<DT, 256>), dim3(blocks), dim3(256), 0, st, a); break;
+    }
     return fta::check_launch("fta_dq_combine_kernel");
 }
 
@@ -2246,8 +2287,18 @@ size_t split_bytes(int B, int H, const Geo& G, int ns) {
     return fta::align_up(rows * sizeof(float2)) + fta::align_up(rows * G.Dk * sizeof(float));
 }
 
-// dQ's split parts (the forward's rule for small grids: its workgroups cover the
-// same 256-query tiles), after bwd_bytes in the workspace of the combined backward
+// dQ's split walks on small grids: the forward's rule for the pipelined kernels
+// (D 64 / 128, 256-query workgroups); the register-staged ones at D 160 / 256
+// (128-query workgroups, one per CU) split while at most half the CUs are busy
+int dq_nsplit(int B, int H, const Geo& G) {
+    if (G.Dk == 64 || G.Dk == 128) return fwd_nsplit(B, H, G);
+    if (!(G.Dk == 160 || G.Dk == 256) || G.Mkv < 8) return 1;
+    const int64_t wgs = (int64_t)((G.Npq + 127) / 128) * B * H;
+    if (wgs > 128) return 1;
+    const int64_t ns = 256 / wgs;
+    return (int)(ns > 4 ? 4 : ns < 2 ? 2 : ns);
+}
+// dQ's split parts, after bwd_bytes in the workspace of the combined backward
 size_t dq_split_bytes(int B, int H, const Geo& G, int ns) {
     if (ns <= 1) return 0;
     return fta::align_up((size_t)ns * B * H * G.Npq * G.Dk * sizeof(float));
@@ -2385,7 +2436,7 @@ size_t fta_sparse_attn_bwd_workspace_size(int B, int H, int N, int D, int q_bloc
     // membership bitmap KV block -> q-blocks, lse in log2 units, launch order, then
     // the split parts of dK/dV and of dQ (one region: dQ runs after dK/dV is done);
     // the dK/dV parts are sized for one K/V head per query head
-    return bwd_bytes(B, H, N, G) + std::max(dq_split_bytes(B, H, G, fwd_nsplit(B, H, G)),
+    return bwd_bytes(B, H, N, G) + std::max(dq_split_bytes(B, H, G, dq_nsplit(B, H, G)),
                                             dkv_split_bytes(B, H, G, dkv_nsplit(B, H, kv_block_size, G)));
 }
 
@@ -2476,8 +2527,10 @@ int bwd_dq_impl(const int32_t* head_perm, const void* q, const int64_t* q_stride
     const int Tq = (G.Dk <= 128) ? 8 : 4;  // query tiles per dQ workgroup
     a.wg_per_bh = (G.Npq + 32 * Tq - 1) / (32 * Tq);
     // small grids: each workgroup's union walk in 2-4 parts, summed by fta_dq_combine_kernel
-    const int ns = fwd_nsplit(B, H, G);
-    const bool split = ns > 1 && split_ws != nullptr && split_avail >= dq_split_bytes(B, H, G, ns);
+    const int ns = dq_nsplit(B, H, G);
+    const bool pipe_ok = a.k_sn <= (1 << 24) && a.v_sn <= (1 << 24);
+    const bool split = ns > 1 && (G.Dk > 128 || pipe_ok) && split_ws != nullptr &&
+                       split_avail >= dq_split_bytes(B, H, G, ns);
     a.nsplit = split ? ns : 1;
     a.nbh = B * H;
     a.npq = G.Npq;

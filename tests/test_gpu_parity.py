@@ -996,7 +996,14 @@ def _bwd_bytes_unsplit(B, H, N, g, b, qpad, kvpad):
     return al(B * H * M * ((QM + 31) // 32) * 4) + al(B * H * N * 4) + al(B * H * M * 4) + al(B * H * 2 * 4)
 
 
-@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: f"B{c[0]}H{c[1]}k{c[2]}N{c[3]}D{c[4]}g{c[5]}b{c[6]}")
+BWD_SPLIT_CASES = SPLIT_CASES + [
+    # the register-staged dQ kernel (D 160 / 256; the forward does not split there)
+    (1, 8, 8, 2048, 256, 64, 64, (0, 0), (0, 0), 16),
+    (1, 4, 2, 1000, 160, 32, 64, (8, 16), (24, 0), 12),
+]
+
+
+@pytest.mark.parametrize("case", BWD_SPLIT_CASES, ids=lambda c: f"B{c[0]}H{c[1]}k{c[2]}N{c[3]}D{c[4]}g{c[5]}b{c[6]}")
 def test_bwd_split_walks(case):
     """Small grids also split the backward's walks when the workspace has room:
     dQ's union walks (fta_dq_combine_kernel adds the parts) and, for 64-key
@@ -1028,7 +1035,7 @@ def test_bwd_split_walks(case):
     qs, ks = _lib.i64arr([N * H * D, D, H * D]), _lib.i64arr([N * Hk * D, D, Hk * D])
     geo = (B, H, N, D, g, b, qpad[0], qpad[1], kvpad[0], kvpad[1])
     stream = torch.cuda.current_stream().cuda_stream
-    assert L.fta_sparse_attn_fwd_splits(*geo) > 1, "the case should split its walks"
+    assert D > 128 or L.fta_sparse_attn_fwd_splits(*geo) > 1, "the case should split its walks"
     o = torch.empty_like(q)
     lse = torch.empty(B, H, N, dtype=torch.float32, device="cuda")
     ws_f = _lib.workspace(L.fta_sparse_attn_fwd_workspace_size(*geo), "cuda")
