@@ -305,8 +305,8 @@ int fta_sparse_attn_fwd_gqa(const void* q, const int64_t* q_strides, const void*
  * dK/dV launch order, plus, on small grids, room for split walks (one region,
  * used by dK/dV and then by dQ): dK/dV with fewer workgroups than the GPU holds
  * at once (64-key blocks at D 64 / 128 / 256) and dQ with fewer than 128
- * workgroups walk their lists in 2-4 parts whose fp32 sums are added by a
- * combine kernel.  A smaller workspace (at least the bitmap, lse and order)
+ * workgroups (at most 128 at D 160 / 256) walk their lists in 2-4 parts whose
+ * fp32 sums are added by a combine kernel.  A smaller workspace (at least the bitmap, lse and order)
  * runs the walks unsplit: the results then differ only in fp32 summation
  * order.  Sized for Hk = H; with Hk < H the dK/dV parts may not fit, and
  * dK/dV then runs unsplit.
