@@ -447,9 +447,10 @@ def check_attn_vs_oracle(q, k, v, do, o, lse, merged, H, g, b, qpad, kvpad, dt, 
             rr_ = rr_.reshape(B, N, -1, gqa_repeat, Dk).sum(3).reshape(B, N, -1)
             r64 = r64.reshape(B, N, -1, gqa_repeat, Dk).sum(3).reshape(B, N, -1)
         assert_within(np32(t.grad), rr_, name=f"{name} vs rounding oracle")
-        s2 = max(1.0, np.abs(r64).max() / 4)
-        assert_close_frac(np32(t.grad), r64, atol=2e-3 * s2, rtol=1e-2, name=f"{name} vs float64", min_frac=0.9995,
-                          hard_atol=1e-2 * s2)
+        # unscaled bound (the largest |gradient| is reported)
+        say(f"{name} vs float64: max |ref| {np.abs(r64).max():.3f}")
+        assert_close_frac(np32(t.grad), r64, atol=2e-3, rtol=1e-2, name=f"{name} vs float64", min_frac=0.9995,
+                          hard_atol=1e-2)
 
 
 def test_dkv_launch_order_many_blocks():

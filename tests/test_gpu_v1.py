@@ -142,9 +142,10 @@ def test_score_with_dense_output_and_backward(case):
     dq64, dk64, dv64 = O.sparse_attn_bwd(qn, kn, vn, don, merged, H, 64, 64, None, pad64, pad64)
     for name, got, ref, r64 in (("dq", q.grad, dq, dq64), ("dk", k.grad, dk, dk64), ("dv", v.grad, dv, dv64)):
         assert_within(to3(got), ref, name=f"{name} vs rounding oracle")
-        s = max(1.0, np.abs(r64).max() / 4)
-        assert_close_frac(to3(got), r64, atol=2e-3 * s, rtol=1e-2, name=f"{name} vs f64", min_frac=0.9995,
-                          hard_atol=1e-2 * s)
+        # unscaled bound (the largest |gradient| is reported)
+        say(f"{name} vs f64: max |ref| {np.abs(r64).max():.3f}")
+        assert_close_frac(to3(got), r64, atol=2e-3, rtol=1e-2, name=f"{name} vs f64", min_frac=0.9995,
+                          hard_atol=1e-2)
 
 
 ATTN_CASES = [
