@@ -1001,6 +1001,9 @@ BWD_SPLIT_CASES = SPLIT_CASES + [
     # the register-staged dQ kernel (D 160 / 256; the forward does not split there)
     (1, 8, 8, 2048, 256, 64, 64, (0, 0), (0, 0), 16),
     (1, 4, 2, 1000, 160, 32, 64, (8, 16), (24, 0), 12),
+    # 33-key blocks (a second tile of one key) and the D = 256 dK/dV split with GQA
+    (1, 2, 2, 990, 64, 32, 33, (0, 2), (0, 0), 10),
+    (1, 4, 2, 1024, 256, 32, 64, (0, 0), (0, 0), 8),
 ]
 
 
