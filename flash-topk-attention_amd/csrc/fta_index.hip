@@ -160,6 +160,9 @@ __global__ __launch_bounds__(256) void fta_qblock_merge_kernel(const int32_t* __
 // No workgroup barrier: up to four waves, each on its own slice and LDS region.
 // ----------------------------------------------------------------------------
 constexpr int kMergeWaveMax = 4096;  // largest g*K of the one-wave path
+// valid entries from which the one-wave path sums per id in an LDS histogram
+// instead of sorting the entries (dense lists: few duplicate ids per 64)
+constexpr int kMergeWaveHistNV = 384;
 
 __device__ __forceinline__ void fta_wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -286,27 +289,67 @@ __global__ __launch_bounds__(256) void fta_qblock_merge_wave_kernel(
         if (valid) key[NV + __popcll(vm & ((1ull << lane) - 1ull))] = kv;
         NV += __popcll(vm);
     }
-    int NS = 1;
-    while (NS < NV) NS <<= 1;
-    for (int i = NV + lane; i < NS; i += 64) key[i] = 0xffffffffu;
-    fta_wave_sync();
-    fta_wave_sort<uint32_t, false>(key, NS, 0xffffffffu, lane);
     int P = 0;
-    for (int r0 = 0; r0 < NV; r0 += 64) {
-        const int i = r0 + lane;
-        const uint32_t kv = (i < NV) ? key[i] : 0xffffffffu;
-        const uint32_t id = kv >> 16;
-        const bool head = kv != 0xffffffffu && (i == 0 || (key[i - 1] >> 16) != id);
-        float sum = 0.f;
-        if (head)
-            for (int j = i; j < NV && (key[j] >> 16) == id; ++j) sum = __fadd_rn(sum, sc[key[j] & 0xffffu]);
-        const bool pos = head && sum > 0.f;
-        const unsigned long long mask = __ballot(pos);
-        const int off = __popcll(mask & ((1ull << lane) - 1ull));
-        if (pos)
-            out[P + off] = ((unsigned long long)__builtin_bit_cast(uint32_t, sum) << 32) |
-                           (unsigned long long)(0xffffffffu - id);
-        P += __popcll(mask);
+    if (NV >= kMergeWaveHistNV && Mt <= NP) {
+        // Nearly every entry valid: per-id sums in an LDS histogram over the
+        // Mt ids (in the `out` bytes) instead of a sort of NV keys.  Entries
+        // are added in position order (compacted order; within 64, lowest lane
+        // first through owner rounds), the same fp32 additions as the sorted
+        // runs below.  The positive sums then go to the key / score bytes.
+        volatile float* acc = reinterpret_cast<volatile float*>(base);              // [Mt]
+        volatile int* owner = reinterpret_cast<volatile int*>(base + (size_t)NP * 4);  // [Mt]
+        for (int m = lane; m < Mt; m += 64) acc[m] = 0.f;
+        fta_wave_sync();
+        for (int r0 = 0; r0 < NV; r0 += 64) {
+            const int i = r0 + lane;
+            bool pending = i < NV;
+            const uint32_t kv = pending ? key[i] : 0u;
+            const int id = (int)(kv >> 16);
+            const float v = pending ? sc[kv & 0xffffu] : 0.f;
+            while (__ballot(pending) != 0ull) {
+                if (pending) owner[id] = 64;
+                if (pending) atomicMin(const_cast<int*>(&owner[id]), lane);
+                if (pending && owner[id] == lane) {
+                    acc[id] = __fadd_rn(acc[id], v);
+                    pending = false;
+                }
+            }
+        }
+        fta_wave_sync();
+        out = reinterpret_cast<unsigned long long*>(base + (size_t)NP * 8);  // over key / sc
+        for (int m0 = 0; m0 < Mt; m0 += 64) {
+            const int m = m0 + lane;
+            const float sum = (m < Mt) ? acc[m] : 0.f;
+            const bool pos = sum > 0.f;
+            const unsigned long long mask = __ballot(pos);
+            if (pos)
+                out[P + __popcll(mask & ((1ull << lane) - 1ull))] =
+                    ((unsigned long long)__builtin_bit_cast(uint32_t, sum) << 32) |
+                    (unsigned long long)(0xffffffffu - (uint32_t)m);
+            P += __popcll(mask);
+        }
+    } else {
+        int NS = 1;
+        while (NS < NV) NS <<= 1;
+        for (int i = NV + lane; i < NS; i += 64) key[i] = 0xffffffffu;
+        fta_wave_sync();
+        fta_wave_sort<uint32_t, false>(key, NS, 0xffffffffu, lane);
+        for (int r0 = 0; r0 < NV; r0 += 64) {
+            const int i = r0 + lane;
+            const uint32_t kv = (i < NV) ? key[i] : 0xffffffffu;
+            const uint32_t id = kv >> 16;
+            const bool head = kv != 0xffffffffu && (i == 0 || (key[i - 1] >> 16) != id);
+            float sum = 0.f;
+            if (head)
+                for (int j = i; j < NV && (key[j] >> 16) == id; ++j) sum = __fadd_rn(sum, sc[key[j] & 0xffffu]);
+            const bool pos = head && sum > 0.f;
+            const unsigned long long mask = __ballot(pos);
+            const int off = __popcll(mask & ((1ull << lane) - 1ull));
+            if (pos)
+                out[P + off] = ((unsigned long long)__builtin_bit_cast(uint32_t, sum) << 32) |
+                               (unsigned long long)(0xffffffffu - id);
+            P += __popcll(mask);
+        }
     }
     int S = 1;
     while (S < P) S <<= 1;

@@ -239,12 +239,15 @@ def test_merge_bit_exact(g, K, Mt, W, pad, with_scores):
 @pytest.mark.parametrize("g,K,Mt,W,dups", [(64, 32, 64, 2048, False), (48, 16, 500, 300, True),
                                            (64, 16, 512, 512, False), (40, 13, 37, 16, True),
                                            (1, 16, 300, 16, True), (2, 16, 64, 40, True), (3, 7, 50, 8, False),
-                                           (1, 16, 4096, 16, False)])
+                                           (1, 16, 4096, 16, False),
+                                           # 512 entries, ~410 valid: the one-wave kernel's histogram branch
+                                           (32, 16, 400, 256, True)])
 def test_merge_lane_and_histogram_bit_exact(g, K, Mt, W, dups):
     """flash_qblock_merge with more than 512 entries per q-block over at most
     512 blocks runs the per-wave LDS histogram (the reference's K = 32, g = 64
     row: 2048 entries over 64 blocks); with at most 32 entries per q-block it
-    runs one lane per q-block (g = 1: C2's q-blocks of one query).  Bit-exact
+    runs one lane per q-block (g = 1: C2's q-blocks of one query); the one-wave
+    kernel sums slices with 384 or more valid entries in an LDS histogram too.  Bit-exact
     against the oracle's sequential (row, slot) sums, with ids repeated within
     a row and inside one 64-entry step (dups), ids past the block count, -1
     entries and non-positive sums ignored."""
