@@ -65,6 +65,15 @@ def test_error_path_returns_status_without_gpu():
     assert L.fta_sparse_attn_bwd_workspace_size(1, 8, 2048, 64, 64, 64, 0, 0, 0, 0) == (
         1024 + 8 * 2048 * 4 + 1024 + 256 + 4 * 8 * 2048 * 64 * 4)
     assert 4 * 8 * 2048 * 64 * 4 == 2 * 2 * 8 * 32 * 64 * 64 * 4
+    # D 160 / 256 (register-staged dQ, 128-query workgroups): split while at most 128
+    # workgroups run; the D = 256 dK/dV split while fewer than 256 (one per CU)
+    bare = 1024 + 8 * 2048 * 4 + 1024 + 256
+    assert L.fta_sparse_attn_bwd_workspace_size(1, 8, 2048, 256, 64, 64, 0, 0, 0, 0) == (
+        bare + 2 * 8 * 2048 * 256 * 4)  # 128 dQ workgroups: 2 parts; 256 dK/dV workgroups: none
+    assert L.fta_sparse_attn_bwd_workspace_size(1, 8, 4096, 256, 64, 64, 0, 0, 0, 0) == (
+        8 * 64 * 2 * 4 + 8 * 4096 * 4 + 8 * 64 * 4 + 256)  # 256 dQ workgroups: no split parts
+    assert L.fta_sparse_attn_bwd_workspace_size(1, 4, 1024, 160, 32, 64, 0, 0, 0, 0) == (
+        256 + 4 * 1024 * 4 + 256 + 256 + 4 * 4 * 1024 * 160 * 4)  # 32 dQ workgroups: 4 parts
     # 4096 dQ workgroups at C3: no split parts
     assert L.fta_sparse_attn_bwd_workspace_size(1, 32, 32768, 128, 32, 64, 0, 0, 0, 0) == (
         32 * 512 * 32 * 4 + 32 * 32768 * 4 + 32 * 512 * 4 + 256)
