@@ -40,11 +40,13 @@ def check_topk_gap(gpu_idx, ref_scores_avg, ref_idx, atol_gap=1e-6):
     return bad, len(diff[0])
 
 
-def assert_close_frac(got, ref, atol, rtol, min_frac=0.9999, hard_atol=1e-2, name=""):
+def assert_close_frac(got, ref, atol, rtol, min_frac=0.9999, hard_atol=1e-2, name="", slack=None):
     """bf16/fp16 tolerance: |got - ref| <= atol + rtol*|ref| on at least
     ``min_frac`` of the elements (P is rounded to 16 bits before the P.V / dS.K
     products, as in the reference kernels, so isolated elements can exceed the
-    per-element bound), and never more than ``hard_atol`` + rtol*|ref|."""
+    per-element bound), and never more than ``hard_atol`` + rtol*|ref| (+ the
+    per-element ``slack``, e.g. a multiple of what that 16-bit rounding moves
+    the element by, for long sums of rounded terms)."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert got.shape == ref.shape, name
@@ -52,7 +54,9 @@ def assert_close_frac(got, ref, atol, rtol, min_frac=0.9999, hard_atol=1e-2, nam
     ok = err <= atol + rtol * np.abs(ref)
     frac = ok.mean() if ok.size else 1.0
     assert frac >= min_frac, f"{name}: only {frac:.6f} of elements within atol={atol}, rtol={rtol}; max err {err.max()}"
-    assert np.all(err <= hard_atol + rtol * np.abs(ref)), f"{name}: max err {err.max()} beyond hard bound"
+    hard = hard_atol + rtol * np.abs(ref) + (0.0 if slack is None else np.asarray(slack, dtype=np.float64))
+    bad = err > hard
+    assert not bad.any(), f"{name}: max err {err.max()} beyond hard bound ({int(bad.sum())} elements)"
 
 
 def assert_within(got, ref, atol=2e-3, rtol=1e-2, name=""):

@@ -335,6 +335,9 @@ ATTN_CASES = [
     # D = 160 (and 144 padded to it) with 64-key blocks (generic dK/dV kernel, one KV block per WG)
     (1, 1024, 2, 160, 32, 64, (0, 0), (0, 0), 10, torch.float16),
     (1, 700, 2, 144, 32, 64, (0, 4), (0, 4), 8, torch.bfloat16),
+    # long dK sums of 16-bit dS terms (|dK| up to 6): the float64 check's hard bound
+    # must allow for that rounding (a random sweep found it)
+    (1, 2244, 3, 64, 64, 48, (56, 4), (45, 15), 2, torch.bfloat16),
 ]
 
 
@@ -450,10 +453,12 @@ def check_attn_vs_oracle(q, k, v, do, o, lse, merged, H, g, b, qpad, kvpad, dt, 
             rr_ = rr_.reshape(B, N, -1, gqa_repeat, Dk).sum(3).reshape(B, N, -1)
             r64 = r64.reshape(B, N, -1, gqa_repeat, Dk).sum(3).reshape(B, N, -1)
         assert_within(np32(t.grad), rr_, name=f"{name} vs rounding oracle")
-        # unscaled bound (the largest |gradient| is reported)
+        # unscaled bound (the largest |gradient| is reported); the hard bound also allows
+        # twice what the 16-bit rounding of P / dS moves each element (rounding oracle
+        # against float64), which long sums of rounded terms make exceed 1e-2
         say(f"{name} vs float64: max |ref| {np.abs(r64).max():.3f}")
         assert_close_frac(np32(t.grad), r64, atol=2e-3, rtol=1e-2, name=f"{name} vs float64", min_frac=0.9995,
-                          hard_atol=1e-2)
+                          hard_atol=1e-2, slack=2 * np.abs(rr_ - r64))
 
 
 def test_dkv_launch_order_many_blocks():

@@ -142,10 +142,11 @@ def test_score_with_dense_output_and_backward(case):
     dq64, dk64, dv64 = O.sparse_attn_bwd(qn, kn, vn, don, merged, H, 64, 64, None, pad64, pad64)
     for name, got, ref, r64 in (("dq", q.grad, dq, dq64), ("dk", k.grad, dk, dk64), ("dv", v.grad, dv, dv64)):
         assert_within(to3(got), ref, name=f"{name} vs rounding oracle")
-        # unscaled bound (the largest |gradient| is reported)
+        # unscaled bound (the largest |gradient| is reported); the hard bound also allows
+        # twice what the 16-bit rounding of P / dS moves each element
         say(f"{name} vs f64: max |ref| {np.abs(r64).max():.3f}")
         assert_close_frac(to3(got), r64, atol=2e-3, rtol=1e-2, name=f"{name} vs f64", min_frac=0.9995,
-                          hard_atol=1e-2)
+                          hard_atol=1e-2, slack=2 * np.abs(ref - r64))
 
 
 ATTN_CASES = [
