@@ -690,9 +690,9 @@ def _pattern_qk(N, H, D, pattern, seed, b=64):
     g = torch.Generator(device="cpu").manual_seed(seed)
     C = H * D
     if pattern == "peaked":
-        M = N // b
+        M = -(-N // b)  # blocks covering N (the last one partial when b does not divide N)
         cent = torch.randn(1, M, C, generator=g)
-        k = 0.3 * torch.randn(1, N, C, generator=g) + cent.repeat_interleave(b, dim=1)
+        k = 0.3 * torch.randn(1, N, C, generator=g) + cent.repeat_interleave(b, dim=1)[:, :N]
         pick = torch.randint(0, M, (1, N), generator=g)
         q = 0.3 * torch.randn(1, N, C, generator=g) + torch.gather(cent, 1, pick.unsqueeze(-1).expand(1, N, C))
     elif pattern == "iid":
@@ -768,6 +768,9 @@ STREAM_CASES = [
     (2048, 2, 32, (0, 0), 8, 1.0, "increasing"),
     (1000, 2, 80, (24, 0), 12, 0.95, "iid"),
     (2048, 1, 48, (0, 0), 24, 0.9, "ties", 128),
+    # block-centred data with both paddings and a partial last block (a random sweep)
+    (5167, 2, 64, (59, 22), 32, 0.9, "peaked", 64),
+    (1682, 1, 96, (50, 60), 3, 1.0, "peaked", 128),
 ]
 
 
