@@ -84,32 +84,39 @@ def check_topk_f64(gpu_idx, avg64, raw64, threshold, m_out, gap=1e-6):
     gpu_idx [R, m_out] (-1 after the cut), avg64 / raw64 [R, M] float64.  The
     float64 selection sorts by avg descending (ties to the lower index), keeps
     through the first position whose float64 cumulative raw sum reaches the
-    threshold, capped at m_out.  A row may differ only (a) by blocks whose
-    float64 averages lie within `gap` of each other (near-ties) or (b) in the
-    cut, where the float64 cumulative sum at the shorter cut lies within `gap`
-    of the threshold.  Returns the number of rows that differ otherwise."""
+    threshold, capped at m_out.  A GPU row passes when it is that selection
+    for some order of the blocks whose float64 averages lie within `gap` of
+    each other (near-ties): its blocks are distinct, their averages do not
+    rise by more than `gap` along the list, no block left out ranks more than
+    `gap` above the last one kept, and the cut is where the float64
+    cumulative sum taken in the GPU's order first reaches the threshold
+    (within `gap`) or the list is full.  So a near-tie may swap two blocks,
+    and when the swap falls where the sum crosses the threshold it may move
+    the cut by that block.  Returns the number of rows that fail."""
     gpu_idx = np.asarray(gpu_idx)
     R, M = avg64.shape
+    cap = min(m_out, M)
     bad = 0
     for r in range(R):
-        order = np.lexsort((np.arange(M), -avg64[r]))
-        cs = np.cumsum(raw64[r, order])
-        hit = np.nonzero(cs >= threshold)[0]
-        cut64 = min(int(hit[0]) + 1 if hit.size else M, m_out)
         g = gpu_idx[r]
-        cutg = int((g >= 0).sum())
-        if cutg != cut64:
-            lo = min(cutg, cut64)
-            if not (lo >= 1 and abs(cs[lo - 1] - threshold) < gap):
-                bad += 1
-                continue
-        n = min(cutg, cut64)
-        ref = order[:n]
-        got = g[:n]
-        if np.array_equal(ref, got):
+        n = int((g >= 0).sum())
+        lst = g[:n]
+        if n == 0 or (g[n:] != -1).any() or len(set(lst.tolist())) != n or (lst >= M).any():
+            bad += 1
             continue
-        # near-ties: the sorted float64 averages of both lists agree within gap
-        # position by position, and the lists hold the same blocks up to such swaps
-        if not np.all(np.abs(avg64[r, ref] - avg64[r, got]) < gap):
+        a = avg64[r, lst]
+        if np.any(a[1:] > a[:-1] + gap):
+            bad += 1
+            continue
+        out = np.ones(M, dtype=bool)
+        out[lst] = False
+        if out.any() and avg64[r, out].max() > a[-1] + gap:
+            bad += 1
+            continue
+        cs = np.cumsum(raw64[r, lst])
+        if n >= 2 and cs[-2] >= threshold + gap:  # the sum reached the threshold before the last block
+            bad += 1
+            continue
+        if n < cap and cs[-1] < threshold - gap:  # stopped before reaching it, list not full
             bad += 1
     return bad

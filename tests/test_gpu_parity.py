@@ -193,7 +193,11 @@ def test_drawn_scoring_geometries(seed):
         np.testing.assert_array_equal(got[2].cpu().numpy(), ra)
 
 
-@pytest.mark.parametrize("case", SCORE_CASES[:4], ids=lambda c: f"N{c[1]}D{c[3]}b{c[4]}")
+@pytest.mark.parametrize("case", SCORE_CASES[:4] + [
+    # a near-tie (a full block and a 12-key edge block, averages within 1e-10) where the
+    # cumulative sum crosses 0.5: the cut moves with the tie's order (a random sweep)
+    (2, 1293, 2, 80, 96, (84, 63), torch.bfloat16, "bhnd"),
+], ids=lambda c: f"N{c[1]}D{c[3]}b{c[4]}")
 def test_topk_score_vs_float64_oracle(case):
     """Top-k (thresholds 1.0, 0.9, 0.5) against the selection on float64 block
     scores: identical except near-ties (< 1e-6) and cuts where the float64

@@ -506,7 +506,8 @@ def test_rounding_modes_bound_and_exact_cases():
 
 def test_check_topk_f64_rules():
     """The float64 top-k comparison used by the GPU tests accepts only near-ties
-    and near-threshold cuts."""
+    (including one at the threshold crossing, which moves the cut) and
+    near-threshold cuts."""
     from _helpers import check_topk_f64
 
     raw = np.array([[0.5, 0.3, 0.15, 0.05]])
@@ -518,6 +519,21 @@ def test_check_topk_f64_rules():
     assert check_topk_f64(np.array([[0, 1, 2]]), raw2, raw2, 0.9, 3) == 0  # cum 0.9 - 1e-9: near the threshold
     raw3 = np.array([[0.4, 0.4 + 1e-9, 0.2]])
     assert check_topk_f64(np.array([[0, 1, 2]]), raw3, raw3, 1.0, 3) == 0  # near-tie swap
+    # a near-tie where the sum crosses the threshold: either order is a valid
+    # selection, and the cut follows the order (block 2: small edge block whose
+    # average ties block 1's)
+    raw4 = np.array([[0.45, 0.30, 0.012, 0.238]])
+    avg4 = np.array([[0.45, 0.30, 0.30 + 1e-10, 0.238]])
+    assert check_topk_f64(np.array([[0, 2, 1, -1]]), avg4, raw4, 0.5, 4) == 0  # 0.45, 0.462, 0.762
+    assert check_topk_f64(np.array([[0, 1, -1, -1]]), avg4, raw4, 0.5, 4) == 0  # 0.45, 0.75
+    assert check_topk_f64(np.array([[0, 2, 1, 3]]), avg4, raw4, 0.5, 4) == 1   # past the crossing
+    assert check_topk_f64(np.array([[0, 2, -1, -1]]), avg4, raw4, 0.5, 4) == 1  # stops at 0.462
+    # a block left out that ranks above the last one kept, a repeated block, -1 inside
+    assert check_topk_f64(np.array([[0, 3, -1, -1]]), avg4, raw4, 0.5, 4) == 1
+    assert check_topk_f64(np.array([[0, 0, -1, -1]]), avg4, raw4, 0.5, 4) == 1
+    assert check_topk_f64(np.array([[0, -1, 1, -1]]), avg4, raw4, 0.5, 4) == 1
+    # a full list (m_out = 2) may stop below the threshold
+    assert check_topk_f64(np.array([[0, 1]]), avg4, raw4, 0.9, 2) == 0
 
 
 def test_torch_cpu_baseline_matches_numpy_oracle():
