@@ -220,7 +220,8 @@ def test_topk_score_vs_float64_oracle(case):
 @pytest.mark.parametrize("g,K,Mt,W,pad", [(32, 16, 128, None, (0, 0)), (1, 16, 128, None, (0, 0)),
                                           (16, 8, 157, 128, (3, 13)), (32, 16, 512, 256, (0, 0)),
                                           (4, 64, 4096, 300, (1, 3)),
-                                          (64, 80, 700, 512, (5, 9))])  # g*K > 4096: histogram kernel
+                                          (64, 80, 700, 512, (5, 9)),  # g*K > 4096: histogram kernel
+                                          (24, 1, 419, None, (3, 7))])  # one entry per query
 @pytest.mark.parametrize("with_scores", [False, True])
 def test_merge_bit_exact(g, K, Mt, W, pad, with_scores):
     say(f"[merge] g={g} K={K} Mt={Mt} W={W} pad={pad} scores={with_scores}")
@@ -228,7 +229,8 @@ def test_merge_bit_exact(g, K, Mt, W, pad, with_scores):
     B, H = 1, 2
     N = 64 * g - pad[0] - pad[1]
     idx = np.stack([rng.permutation(Mt)[:K] for _ in range(B * H * N)]).reshape(B, H, N, K).astype(np.int32)
-    idx[..., K - 2:][rng.random((B, H, N, 2)) < 0.3] = -1  # ragged rows
+    kr = min(2, K)
+    idx[..., K - kr:][rng.random((B, H, N, kr)) < 0.3] = -1  # ragged rows
     scr = rng.random((B, H, N, K)).astype(np.float32) if with_scores else None
     ti = torch.from_numpy(idx).cuda()
     ts = torch.from_numpy(scr).cuda() if with_scores else None
