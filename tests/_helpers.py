@@ -44,17 +44,19 @@ def assert_close_frac(got, ref, atol, rtol, min_frac=0.9999, hard_atol=1e-2, nam
     """bf16/fp16 tolerance: |got - ref| <= atol + rtol*|ref| on at least
     ``min_frac`` of the elements (P is rounded to 16 bits before the P.V / dS.K
     products, as in the reference kernels, so isolated elements can exceed the
-    per-element bound), and never more than ``hard_atol`` + rtol*|ref| (+ the
-    per-element ``slack``, e.g. a multiple of what that 16-bit rounding moves
-    the element by, for long sums of rounded terms)."""
+    per-element bound), and never more than ``hard_atol`` + rtol*|ref|.  Both
+    bounds add the per-element ``slack`` when given: a multiple of what that
+    16-bit rounding itself moves the element by, which long sums of rounded
+    terms make larger than the fixed bounds."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     assert got.shape == ref.shape, name
     err = np.abs(got - ref)
-    ok = err <= atol + rtol * np.abs(ref)
+    extra = 0.0 if slack is None else np.asarray(slack, dtype=np.float64)
+    ok = err <= atol + rtol * np.abs(ref) + extra
     frac = ok.mean() if ok.size else 1.0
     assert frac >= min_frac, f"{name}: only {frac:.6f} of elements within atol={atol}, rtol={rtol}; max err {err.max()}"
-    hard = hard_atol + rtol * np.abs(ref) + (0.0 if slack is None else np.asarray(slack, dtype=np.float64))
+    hard = hard_atol + rtol * np.abs(ref) + extra
     bad = err > hard
     assert not bad.any(), f"{name}: max err {err.max()} beyond hard bound ({int(bad.sum())} elements)"
 

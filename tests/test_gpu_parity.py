@@ -516,6 +516,8 @@ GQA_CASES = [
     (1, 512, 4, 2, 32, 32, 32, (0, 0), (0, 0), 6, torch.bfloat16),       # one tile per block
     (1, 640, 4, 2, 256, 32, 64, (0, 0), (0, 0), 6, torch.bfloat16),      # split dK/dV kernel at D = 256
     (1, 500, 4, 2, 160, 20, 64, (0, 0), (0, 12), 5, torch.float16),      # generic dK/dV at D = 160
+    # 16-key blocks: dK / dV sum many rounded terms over two query heads (a random sweep)
+    (2, 1533, 4, 2, 96, 16, 16, (3, 0), (5, 14), 2, torch.bfloat16),
 ]
 
 
