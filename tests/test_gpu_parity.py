@@ -818,6 +818,9 @@ def test_topk_candidate_streams_exact(case):
     ("increasing", 32, 128, 60, 128),
     ("jump", 16, 128, 0, 128),
     ("increasing", 16, 96, 0, 64),
+    ("ties", 1, 64, 60, 64),
+    ("peaked", 26, 128, 0, 64),
+    ("decreasing", 28, 96, 0, 128),
 ])
 def test_topk_stream_pool_overflow_fallback(pattern, topk, D, extra_chunks, b):
     """Candidate streams share a pool sized by the workspace; tiles whose
